@@ -1,0 +1,162 @@
+/*
+ * torch_projectors_hip.h — C ABI of the MI355X (gfx950) projector library
+ * libtorch_projectors_hip.so.
+ *
+ * One entry point per dispatcher op of the reference
+ * (csrc/torch_projectors.cpp:23-36).  Each replaces the reference's
+ * `*_cuda` host wrapper for that op; the wrapper it replaces is cited above
+ * each declaration.  Tensors become (pointer, sizes) pairs:
+ *
+ *   - every array is dense, row-major, in device memory of the current HIP
+ *     device, and must not alias another argument;
+ *   - complex arrays are interleaved (re, im) pairs of the real type chosen
+ *     by `dtype` (TP_F32: complex64 / float32, TP_F64: complex128 / float64);
+ *     rotations, shifts and weights use that same real type;
+ *   - an optional input is passed as NULL when absent;
+ *   - an optional gradient output is passed as NULL when it is not wanted
+ *     (the reference decides this from `requires_grad`, projection_utils.h:112-113);
+ *   - every output element is written by the call (no pre-zeroing needed);
+ *   - work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
+ *     the call returns without synchronising.
+ *
+ * Shapes (n = projection box, N = reconstruction box, h = N/2+1, hp = n/2+1):
+ *   2D reconstruction  [B, N, h]        3D reconstruction [B, N, N, h]
+ *   projections        [B, P, n, hp]    weights           [B, P, n, hp] (real)
+ *   rotations          [B_rot, P, 2, 2] or [B_rot, P, 3, 3], B_rot in {1, B}
+ *   shifts             [B_shift, P, 2], B_shift in {1, B}; component 0 pairs
+ *                      with the row frequency, component 1 with the column
+ *   rotation/shift gradients have the shape of rotations/shifts.
+ *
+ * `interpolation` is TP_LINEAR or TP_CUBIC; `has_cutoff` = 0 means the
+ * reference default cutoff n/2 (cpu/3d/projection_3d_to_2d_kernels.cpp:147-149).
+ *
+ * Return value: TP_OK, or an error code with a message in tp_last_error()
+ * (thread-local).  Argument errors are detected before anything is enqueued.
+ */
+#ifndef TORCH_PROJECTORS_HIP_H
+#define TORCH_PROJECTORS_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TP_OK 0
+#define TP_ERR_INVALID 1 /* invalid argument (shape, dtype, pointer) */
+#define TP_ERR_HIP 2     /* HIP runtime / launch failure */
+
+#define TP_F32 0 /* complex64 + float32 */
+#define TP_F64 1 /* complex128 + float64 */
+
+#define TP_LINEAR 0
+#define TP_CUBIC 1
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* tp_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int tp_abi_version(void);
+
+/* Reconstruction box produced by the backprojection ops: ceil(n*os) rounded
+ * up to even (cpu/3d/backprojection_2d_to_3d_kernels.cpp:129-132). */
+int64_t tp_backproject_rec_boxsize(int64_t proj_boxsize, double oversampling);
+
+/* ---------------------------------------------------------------- 2D -> 2D */
+
+/* Replaces project_2d_forw_cuda (cuda/2d/projection_2d_kernels.cu:633-758). */
+int tp_project_2d_forw(int dtype,
+                       const void* reconstruction, int64_t B, int64_t rec_boxsize, int64_t rec_boxsize_half,
+                       const void* rotations, int64_t B_rot, int64_t P,
+                       const void* shifts, int64_t B_shift,
+                       int64_t proj_boxsize,
+                       int interpolation, double oversampling, int has_cutoff, double fourier_radius_cutoff,
+                       void* projections,
+                       void* stream);
+
+/* Replaces project_2d_back_cuda (cuda/2d/projection_2d_kernels.cu:760-920).
+ * grad_reconstruction has the reconstruction's shape. */
+int tp_project_2d_back(int dtype,
+                       const void* grad_projections, int64_t B, int64_t P, int64_t proj_boxsize, int64_t proj_boxsize_half,
+                       const void* reconstruction, int64_t rec_boxsize, int64_t rec_boxsize_half,
+                       const void* rotations, int64_t B_rot,
+                       const void* shifts, int64_t B_shift,
+                       int interpolation, double oversampling, int has_cutoff, double fourier_radius_cutoff,
+                       void* grad_reconstruction, void* grad_rotations, void* grad_shifts,
+                       void* stream);
+
+/* Replaces backproject_2d_forw_cuda (cuda/2d/backprojection_2d_kernels.cu:827-977).
+ * Outputs have shape [B, N, N/2+1] with N = tp_backproject_rec_boxsize(n, os);
+ * weight_reconstruction must be non-NULL exactly when weights is. */
+int tp_backproject_2d_forw(int dtype,
+                           const void* projections, int64_t B, int64_t P, int64_t proj_boxsize, int64_t proj_boxsize_half,
+                           const void* weights,
+                           const void* rotations, int64_t B_rot,
+                           const void* shifts, int64_t B_shift,
+                           int interpolation, double oversampling, int has_cutoff, double fourier_radius_cutoff,
+                           void* data_reconstruction, void* weight_reconstruction,
+                           void* stream);
+
+/* Replaces backproject_2d_back_cuda (cuda/2d/backprojection_2d_kernels.cu:979-1191).
+ * grad_weights (shape of weights) may only be non-NULL when weights is; it is
+ * all zeros when grad_weight_rec is NULL. */
+int tp_backproject_2d_back(int dtype,
+                           const void* grad_data_rec, const void* grad_weight_rec, int64_t rec_boxsize, int64_t rec_boxsize_half,
+                           const void* projections, int64_t B, int64_t P, int64_t proj_boxsize, int64_t proj_boxsize_half,
+                           const void* weights,
+                           const void* rotations, int64_t B_rot,
+                           const void* shifts, int64_t B_shift,
+                           int interpolation, double oversampling, int has_cutoff, double fourier_radius_cutoff,
+                           void* grad_projections, void* grad_weights, void* grad_rotations, void* grad_shifts,
+                           void* stream);
+
+/* ---------------------------------------------------------------- 3D <-> 2D */
+
+/* Replaces project_3d_to_2d_forw_cuda (cuda/3d/projection_3d_to_2d_kernels.cu:814-1015).
+ * rec_depth must equal rec_boxsize. */
+int tp_project_3d_to_2d_forw(int dtype,
+                             const void* reconstruction, int64_t B, int64_t rec_depth, int64_t rec_boxsize, int64_t rec_boxsize_half,
+                             const void* rotations, int64_t B_rot, int64_t P,
+                             const void* shifts, int64_t B_shift,
+                             int64_t proj_boxsize,
+                             int interpolation, double oversampling, int has_cutoff, double fourier_radius_cutoff,
+                             void* projections,
+                             void* stream);
+
+/* Replaces project_3d_to_2d_back_cuda (cuda/3d/projection_3d_to_2d_kernels.cu:1018-1179). */
+int tp_project_3d_to_2d_back(int dtype,
+                             const void* grad_projections, int64_t B, int64_t P, int64_t proj_boxsize, int64_t proj_boxsize_half,
+                             const void* reconstruction, int64_t rec_depth, int64_t rec_boxsize, int64_t rec_boxsize_half,
+                             const void* rotations, int64_t B_rot,
+                             const void* shifts, int64_t B_shift,
+                             int interpolation, double oversampling, int has_cutoff, double fourier_radius_cutoff,
+                             void* grad_reconstruction, void* grad_rotations, void* grad_shifts,
+                             void* stream);
+
+/* Replaces backproject_2d_to_3d_forw_cuda (cuda/3d/backprojection_2d_to_3d_kernels.cu:1001-1188).
+ * Outputs have shape [B, N, N, N/2+1] with N = tp_backproject_rec_boxsize(n, os). */
+int tp_backproject_2d_to_3d_forw(int dtype,
+                                 const void* projections, int64_t B, int64_t P, int64_t proj_boxsize, int64_t proj_boxsize_half,
+                                 const void* weights,
+                                 const void* rotations, int64_t B_rot,
+                                 const void* shifts, int64_t B_shift,
+                                 int interpolation, double oversampling, int has_cutoff, double fourier_radius_cutoff,
+                                 void* data_reconstruction, void* weight_reconstruction,
+                                 void* stream);
+
+/* Replaces backproject_2d_to_3d_back_cuda (cuda/3d/backprojection_2d_to_3d_kernels.cu:1191-1404). */
+int tp_backproject_2d_to_3d_back(int dtype,
+                                 const void* grad_data_rec, const void* grad_weight_rec, int64_t rec_boxsize, int64_t rec_boxsize_half,
+                                 const void* projections, int64_t B, int64_t P, int64_t proj_boxsize, int64_t proj_boxsize_half,
+                                 const void* weights,
+                                 const void* rotations, int64_t B_rot,
+                                 const void* shifts, int64_t B_shift,
+                                 int interpolation, double oversampling, int has_cutoff, double fourier_radius_cutoff,
+                                 void* grad_projections, void* grad_weights, void* grad_rotations, void* grad_shifts,
+                                 void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TORCH_PROJECTORS_HIP_H */
