@@ -1,0 +1,235 @@
+// Backprojection (scatter) and its gradient (gather) for the 2D->2D and
+// 2D->3D operators.
+//
+//   k_backproject_forw  replaces backproject_2d_forw_cpu / backproject_2d_to_3d_forw_cpu
+//                       (cpu/2d/backprojection_2d_kernels.cpp:99-282,
+//                        cpu/3d/backprojection_2d_to_3d_kernels.cpp:98-303)
+//   k_backproject_back  replaces backproject_2d_back_cpu / backproject_2d_to_3d_back_cpu
+//                       (cpu/2d/backprojection_2d_kernels.cpp:291-537,
+//                        cpu/3d/backprojection_2d_to_3d_kernels.cpp:312-590)
+#include "tp_device.hh"
+#include "tp_launch.hh"
+
+namespace tp {
+
+namespace {
+
+constexpr double kTwoPi = 6.283185307179586476925286766559;
+
+// One lane per projection pixel: v = proj * conj(phase) is spread over the
+// transposed stencil into the data volume, |tap weight| * w into the weight
+// volume, Friedel-aware, out-of-range taps dropped, and every x = 0 target
+// also feeds its Hermitian partner (projection_utils.h:371-406, 451-493;
+// weight lambdas cpu/3d/backprojection_2d_to_3d_kernels.cpp:245-285).
+template <int DIM, typename T, bool CUBIC, bool WEIGHTS>
+__global__ __launch_bounds__(kBlock) void k_backproject_forw(Geom g, const Cx<T>* __restrict__ proj,
+                                                             const T* __restrict__ weights,
+                                                             const T* __restrict__ rot, const T* __restrict__ shifts,
+                                                             Cx<T>* __restrict__ data, T* __restrict__ wrec) {
+    constexpr int RS = DIM * DIM;
+    const T cut2 = T(g.cut2);
+    for (int64_t w = blockIdx.x; w < g.work; w += gridDim.x) {
+        const int64_t bp = w / g.chunks;
+        const int pix = int(w - bp * g.chunks) * kBlock + int(threadIdx.x);
+        if (pix >= g.npix) continue;
+        const int64_t b = bp / g.P, p = bp - b * g.P;
+        const int i = pix / g.hp, j = pix - i * g.hp;
+        const T r = freq_of<T>(i, g.n), c = T(j);
+        if (filtered(r, c, cut2) || (j == 0 && i >= g.n / 2)) continue;
+        const T* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * RS;
+        T x[3], sc, sr;
+        rotate<DIM>(R, r, c, g.os, x, sc, sr);
+        const int64_t pidx = bp * g.npix + pix;
+        Cx<T> v = proj[pidx];
+        if (shifts) {
+            const T* S = shifts + ((g.B_shift == 1 ? 0 : b) * g.P + p) * 2;
+            v = cmul(v, cconj(phase<T>(r, c, S[0], S[1], g.phase_k)));
+        }
+        const T wpix = WEIGHTS ? weights[pidx] : T(0);
+        Cx<T>* db = data + b * g.vol;
+        T* wb = WEIGHTS ? wrec + b * g.vol : nullptr;
+        const int N = g.N, H = g.H;
+        distribute<DIM, T, CUBIC>(x, [&](int d, int rr, int cc, T wd, T wr, T wc) {
+            bool cj;
+            const int64_t idx = scatter_index<DIM>(N, H, d, rr, cc, cj);
+            if (idx < 0) return;
+            Cx<T> tv = tap_value<DIM, T>(v, wd, wr, wc);
+            if (cj) tv.im = -tv.im;
+            atomic_add_cx(&db[idx], tv);
+            const int64_t m = cc == 0 ? mirror_index<DIM>(N, H, d, rr) : -1;
+            if (m >= 0) atomic_add_cx(&db[m], cconj(tv));
+            if (WEIGHTS) {
+                const T fw = wpix * tap_weight<DIM, T>(wd, wr, wc);
+                atomic_add(&wb[idx], fw);
+                if (m >= 0) atomic_add(&wb[m], fw);
+            }
+        });
+    }
+}
+
+// Gradient of the backprojection: grad_proj gathers grad_data_rec with the
+// forward phase; grad_weights gathers grad_weight_rec (always (bi/tri)linear,
+// Friedel flip without conjugation, zero outside); rotation and shift
+// gradients pair the conj-phased projection with the spatial derivative /
+// value of grad_data_rec (backprojection_2d_to_3d_kernels.cpp:451-567).
+template <int DIM, typename T, bool CUBIC, bool WG, bool ROT, bool SHIFT>
+__global__ __launch_bounds__(kBlock) void k_backproject_back(Geom g, const Cx<T>* __restrict__ gdata,
+                                                             const T* __restrict__ gw, const Cx<T>* __restrict__ proj,
+                                                             const T* __restrict__ rot, const T* __restrict__ shifts,
+                                                             Cx<T>* __restrict__ gproj, T* __restrict__ gweights,
+                                                             T* __restrict__ grot, T* __restrict__ gshift) {
+    constexpr int RS = DIM * DIM;
+    constexpr int K = RS + 2;
+    __shared__ T red[kBlock / 64][K];
+    const T cut2 = T(g.cut2);
+    for (int64_t w = blockIdx.x; w < g.work; w += gridDim.x) {
+        const int64_t bp = w / g.chunks;
+        const int pix = int(w - bp * g.chunks) * kBlock + int(threadIdx.x);
+        const int64_t b = bp / g.P, p = bp - b * g.P;
+        const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
+        T acc[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) acc[k] = T(0);
+        if (pix < g.npix) {
+            const int i = pix / g.hp, j = pix - i * g.hp;
+            const T r = freq_of<T>(i, g.n), c = T(j);
+            const int64_t pidx = bp * g.npix + pix;
+            Cx<T> out = {0, 0};
+            T outw = T(0);
+            if (!filtered(r, c, cut2) && !(j == 0 && i >= g.n / 2)) {
+                const T* R = rot + (rb * g.P + p) * RS;
+                const T* S = shifts ? shifts + (sb * g.P + p) * 2 : nullptr;
+                T x[3], sc, sr;
+                rotate<DIM>(R, r, c, g.os, x, sc, sr);
+                const Interp<T> it = interpolate<DIM, T, CUBIC, ROT>(gdata + b * g.vol, g.N, g.H, x);
+                Cx<T> ph = {T(1), T(0)};
+                if (S) ph = phase<T>(r, c, S[0], S[1], g.phase_k);
+                out = S ? cmul(it.v, ph) : it.v;
+                if (WG) outw = weight_grad_interp<DIM, T>(gw + b * g.vol, g.N, g.H, x);
+                if (ROT || SHIFT) {
+                    Cx<T> pv = proj[pidx];
+                    if (S) pv = cmul(pv, cconj(ph));
+                    if (ROT) {
+                        const T s[3] = {sc, sr, T(0.0)};
+#pragma unroll
+                        for (int row = 0; row < DIM; ++row)
+#pragma unroll
+                            for (int k = 0; k < DIM; ++k)
+                                acc[row * DIM + k] += cmul(pv, cconj(cscale(it.g[row], s[k]))).re;
+                    }
+                    if (SHIFT) {
+                        const Cx<T> kr = {T(0), T(-kTwoPi * double(r) / double(g.n))};
+                        const Cx<T> kc = {T(0), T(-kTwoPi * double(c) / double(g.n))};
+                        acc[RS] += cmul(pv, cconj(cmul(kr, it.v))).re;
+                        acc[RS + 1] += cmul(pv, cconj(cmul(kc, it.v))).re;
+                    }
+                }
+            }
+            gproj[pidx] = out;
+            if (gweights) gweights[pidx] = outw;
+        }
+        if (ROT || SHIFT) {
+            block_sum<T, K>(acc, red);
+            if (threadIdx.x == 0) {
+                if (ROT)
+                    for (int k = 0; k < RS; ++k) atomic_add(&grot[(rb * g.P + p) * RS + k], acc[k]);
+                if (SHIFT)
+                    for (int k = 0; k < 2; ++k) atomic_add(&gshift[(sb * g.P + p) * 2 + k], acc[RS + k]);
+            }
+        }
+    }
+}
+
+template <int DIM, typename T, bool CUBIC>
+hipError_t forw(const Geom& g, const void* proj, const void* weights, const void* rot, const void* shifts, void* data,
+                void* wrec, hipStream_t s) {
+    if (weights)
+        hipLaunchKernelGGL((k_backproject_forw<DIM, T, CUBIC, true>), dim3(grid_for(g.work)), dim3(kBlock), 0, s, g,
+                           (const Cx<T>*)proj, (const T*)weights, (const T*)rot, (const T*)shifts, (Cx<T>*)data,
+                           (T*)wrec);
+    else
+        hipLaunchKernelGGL((k_backproject_forw<DIM, T, CUBIC, false>), dim3(grid_for(g.work)), dim3(kBlock), 0, s,
+                           g, (const Cx<T>*)proj, (const T*)nullptr, (const T*)rot, (const T*)shifts, (Cx<T>*)data,
+                           (T*)nullptr);
+    return hipGetLastError();
+}
+
+template <int DIM, typename T, bool CUBIC, bool WG, bool ROT, bool SHIFT>
+hipError_t back8(const Geom& g, const void* gdata, const void* gw, const void* proj, const void* rot,
+                 const void* shifts, void* gproj, void* gweights, void* grot, void* gshift, hipStream_t s) {
+    hipLaunchKernelGGL((k_backproject_back<DIM, T, CUBIC, WG, ROT, SHIFT>), dim3(grid_for(g.work)), dim3(kBlock), 0,
+                       s, g, (const Cx<T>*)gdata, (const T*)gw, (const Cx<T>*)proj, (const T*)rot, (const T*)shifts,
+                       (Cx<T>*)gproj, (T*)gweights, (T*)grot, (T*)gshift);
+    return hipGetLastError();
+}
+
+template <int DIM, typename T, bool CUBIC, bool WG>
+hipError_t back4(const Geom& g, const void* gdata, const void* gw, const void* proj, const void* rot,
+                 const void* shifts, void* gproj, void* gweights, void* grot, void* gshift, hipStream_t s) {
+    if (grot && gshift)
+        return back8<DIM, T, CUBIC, WG, true, true>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+    if (grot)
+        return back8<DIM, T, CUBIC, WG, true, false>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift,
+                                                     s);
+    if (gshift)
+        return back8<DIM, T, CUBIC, WG, false, true>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift,
+                                                     s);
+    return back8<DIM, T, CUBIC, WG, false, false>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+}
+
+template <int DIM, typename T, bool CUBIC>
+hipError_t back(const Geom& g, const void* gdata, const void* gw, const void* proj, const void* rot,
+                const void* shifts, void* gproj, void* gweights, void* grot, void* gshift, hipStream_t s) {
+    if (gw && gweights)
+        return back4<DIM, T, CUBIC, true>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+    return back4<DIM, T, CUBIC, false>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+}
+
+#define TP_DISPATCH(dim, dt, cubic, FN, ...)                                                  \
+    do {                                                                                      \
+        if (dim == 2) {                                                                       \
+            if (dt == 0) return cubic ? FN<2, float, true>(__VA_ARGS__) : FN<2, float, false>(__VA_ARGS__);    \
+            return cubic ? FN<2, double, true>(__VA_ARGS__) : FN<2, double, false>(__VA_ARGS__);               \
+        }                                                                                     \
+        if (dt == 0) return cubic ? FN<3, float, true>(__VA_ARGS__) : FN<3, float, false>(__VA_ARGS__);        \
+        return cubic ? FN<3, double, true>(__VA_ARGS__) : FN<3, double, false>(__VA_ARGS__);                   \
+    } while (0)
+
+// Zero fill with 16-byte stores over the aligned body.
+__global__ __launch_bounds__(kBlock) void k_zero(uint32_t* __restrict__ p, int64_t head, int64_t quads,
+                                                 int64_t words) {
+    const int64_t stride = int64_t(gridDim.x) * kBlock;
+    const int64_t t = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+    if (t < head) p[t] = 0u;
+    uint4* q = reinterpret_cast<uint4*>(p + head);
+    for (int64_t k = t; k < quads; k += stride) q[k] = make_uint4(0u, 0u, 0u, 0u);
+    for (int64_t k = head + quads * 4 + t; k < words; k += stride) p[k] = 0u;
+}
+
+}  // namespace
+
+hipError_t launch_zero(void* p, int64_t words, hipStream_t s) {
+    if (words <= 0) return hipSuccess;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    int64_t head = int64_t(((16 - (a & 15)) & 15) / 4);
+    if (head > words) head = words;
+    const int64_t quads = (words - head) / 4;
+    int64_t blocks = (quads + kBlock - 1) / kBlock;
+    if (blocks < 1) blocks = 1;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(k_zero, dim3(unsigned(blocks)), dim3(kBlock), 0, s, (uint32_t*)p, head, quads, words);
+    return hipGetLastError();
+}
+
+hipError_t launch_backproject_forw(int dim, int dt, bool cubic, const Geom& g, const void* proj, const void* weights,
+                                   const void* rot, const void* shifts, void* data, void* wrec, hipStream_t s) {
+    TP_DISPATCH(dim, dt, cubic, forw, g, proj, weights, rot, shifts, data, wrec, s);
+}
+
+hipError_t launch_backproject_back(int dim, int dt, bool cubic, const Geom& g, const void* gdata, const void* gw,
+                                   const void* proj, const void* rot, const void* shifts, void* gproj,
+                                   void* gweights, void* grot, void* gshift, hipStream_t s) {
+    TP_DISPATCH(dim, dt, cubic, back, g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+}
+
+}  // namespace tp

@@ -1,0 +1,175 @@
+// Forward projection (gather) and its adjoint/gradient (scatter) for the
+// 2D->2D and 3D->2D operators.
+//
+//   k_project_forw  replaces project_2d_forw_cpu / project_3d_to_2d_forw_cpu
+//                   (cpu/2d/projection_2d_kernels.cpp:96-202,
+//                    cpu/3d/projection_3d_to_2d_kernels.cpp:97-212)
+//   k_project_back  replaces project_2d_back_cpu / project_3d_to_2d_back_cpu
+//                   (cpu/2d/projection_2d_kernels.cpp:209-375,
+//                    cpu/3d/projection_3d_to_2d_kernels.cpp:219-402)
+//
+// One lane per output rfft pixel; a 256-lane block covers 256 consecutive
+// pixels (row-major i, j) of one pose, so a wavefront walks neighbouring
+// columns of neighbouring rows and its taps land on neighbouring volume
+// lines.  Blocks loop over (pose, chunk) work items with a grid stride.
+#include "tp_device.hh"
+#include "tp_launch.hh"
+
+namespace tp {
+
+namespace {
+
+constexpr double kTwoPi = 6.283185307179586476925286766559;
+
+template <int DIM, typename T, bool CUBIC>
+__global__ __launch_bounds__(kBlock) void k_project_forw(Geom g, const Cx<T>* __restrict__ rec,
+                                                         const T* __restrict__ rot, const T* __restrict__ shifts,
+                                                         Cx<T>* __restrict__ out) {
+    constexpr int RS = DIM * DIM;
+    const T cut2 = T(g.cut2);
+    for (int64_t w = blockIdx.x; w < g.work; w += gridDim.x) {
+        const int64_t bp = w / g.chunks;
+        const int pix = int(w - bp * g.chunks) * kBlock + int(threadIdx.x);
+        if (pix >= g.npix) continue;
+        const int64_t b = bp / g.P, p = bp - b * g.P;
+        const int i = pix / g.hp, j = pix - i * g.hp;
+        const T r = freq_of<T>(i, g.n), c = T(j);
+        Cx<T> v = {0, 0};
+        if (!filtered(r, c, cut2)) {
+            const T* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * RS;
+            T x[3], sc, sr;
+            rotate<DIM>(R, r, c, g.os, x, sc, sr);
+            v = interpolate<DIM, T, CUBIC, false>(rec + b * g.vol, g.N, g.H, x).v;
+            if (shifts) {
+                const T* S = shifts + ((g.B_shift == 1 ? 0 : b) * g.P + p) * 2;
+                v = cmul(v, phase<T>(r, c, S[0], S[1], g.phase_k));
+            }
+        }
+        out[bp * g.npix + pix] = v;
+    }
+}
+
+// Gradient of the forward projection.  The reconstruction gradient is the
+// transposed interpolation of g' = g * conj(phase), scattered Friedel-aware
+// with out-of-range taps dropped and no x = 0 mirror
+// (projection_utils.h:336-362, 414-443).  Rotation and shift gradients are
+// per-pose sums, reduced across the block before one atomic per component.
+template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT>
+__global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __restrict__ gproj,
+                                                         const Cx<T>* __restrict__ rec, const T* __restrict__ rot,
+                                                         const T* __restrict__ shifts, Cx<T>* __restrict__ grec,
+                                                         T* __restrict__ grot, T* __restrict__ gshift) {
+    constexpr int RS = DIM * DIM;
+    constexpr int K = RS + 2;
+    __shared__ T red[kBlock / 64][K];
+    const T cut2 = T(g.cut2);
+    for (int64_t w = blockIdx.x; w < g.work; w += gridDim.x) {
+        const int64_t bp = w / g.chunks;
+        const int pix = int(w - bp * g.chunks) * kBlock + int(threadIdx.x);
+        const int64_t b = bp / g.P, p = bp - b * g.P;
+        const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
+        T acc[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) acc[k] = T(0);
+        if (pix < g.npix) {
+            const int i = pix / g.hp, j = pix - i * g.hp;
+            const T r = freq_of<T>(i, g.n), c = T(j);
+            // masked pixels and the Friedel half of the x = 0 line are skipped
+            if (!filtered(r, c, cut2) && !(j == 0 && i >= g.n / 2)) {
+                const T* R = rot + (rb * g.P + p) * RS;
+                const T* S = shifts ? shifts + (sb * g.P + p) * 2 : nullptr;
+                T x[3], sc, sr;
+                rotate<DIM>(R, r, c, g.os, x, sc, sr);
+                const Cx<T> g0 = gproj[bp * g.npix + pix];
+                const Cx<T> gg = S ? cmul(g0, phase<T>(-r, -c, S[0], S[1], g.phase_k)) : g0;
+                Cx<T>* gb = grec + b * g.vol;
+                const int N = g.N, H = g.H;
+                distribute<DIM, T, CUBIC>(x, [&](int d, int rr, int cc, T wd, T wr, T wc) {
+                    bool cj;
+                    const int64_t idx = scatter_index<DIM>(N, H, d, rr, cc, cj);
+                    if (idx < 0) return;
+                    Cx<T> v = tap_value<DIM, T>(gg, wd, wr, wc);
+                    if (cj) v.im = -v.im;
+                    atomic_add_cx(&gb[idx], v);
+                });
+                if (ROT || SHIFT) {
+                    const Interp<T> it = interpolate<DIM, T, CUBIC, ROT>(rec + b * g.vol, N, H, x);
+                    if (ROT) {
+                        const T s[3] = {sc, sr, T(0.0)};
+#pragma unroll
+                        for (int row = 0; row < DIM; ++row)
+#pragma unroll
+                            for (int k = 0; k < DIM; ++k)
+                                acc[row * DIM + k] += cmul(gg, cconj(cscale(it.g[row], s[k]))).re;
+                    }
+                    if (SHIFT) {
+                        const Cx<T> mod = cmul(it.v, phase<T>(r, c, S[0], S[1], g.phase_k));
+                        const Cx<T> kr = {T(0), T(-kTwoPi * double(r) / double(g.n))};
+                        const Cx<T> kc = {T(0), T(-kTwoPi * double(c) / double(g.n))};
+                        acc[RS] += cmul(g0, cconj(cmul(kr, mod))).re;
+                        acc[RS + 1] += cmul(g0, cconj(cmul(kc, mod))).re;
+                    }
+                }
+            }
+        }
+        if (ROT || SHIFT) {
+            block_sum<T, K>(acc, red);
+            if (threadIdx.x == 0) {
+                if (ROT)
+                    for (int k = 0; k < RS; ++k) atomic_add(&grot[(rb * g.P + p) * RS + k], acc[k]);
+                if (SHIFT)
+                    for (int k = 0; k < 2; ++k) atomic_add(&gshift[(sb * g.P + p) * 2 + k], acc[RS + k]);
+            }
+        }
+    }
+}
+
+template <int DIM, typename T, bool CUBIC>
+hipError_t forw(const Geom& g, const void* rec, const void* rot, const void* shifts, void* out, hipStream_t s) {
+    hipLaunchKernelGGL((k_project_forw<DIM, T, CUBIC>), dim3(grid_for(g.work)), dim3(kBlock), 0, s, g,
+                       (const Cx<T>*)rec, (const T*)rot, (const T*)shifts, (Cx<T>*)out);
+    return hipGetLastError();
+}
+
+template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT>
+hipError_t back4(const Geom& g, const void* gproj, const void* rec, const void* rot, const void* shifts, void* grec,
+                 void* grot, void* gshift, hipStream_t s) {
+    hipLaunchKernelGGL((k_project_back<DIM, T, CUBIC, ROT, SHIFT>), dim3(grid_for(g.work)), dim3(kBlock), 0, s, g,
+                       (const Cx<T>*)gproj, (const Cx<T>*)rec, (const T*)rot, (const T*)shifts, (Cx<T>*)grec,
+                       (T*)grot, (T*)gshift);
+    return hipGetLastError();
+}
+
+template <int DIM, typename T, bool CUBIC>
+hipError_t back(const Geom& g, const void* gproj, const void* rec, const void* rot, const void* shifts, void* grec,
+                void* grot, void* gshift, hipStream_t s) {
+    if (grot && gshift) return back4<DIM, T, CUBIC, true, true>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+    if (grot) return back4<DIM, T, CUBIC, true, false>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+    if (gshift) return back4<DIM, T, CUBIC, false, true>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+    return back4<DIM, T, CUBIC, false, false>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+}
+
+#define TP_DISPATCH(dim, dt, cubic, FN, ...)                                                  \
+    do {                                                                                      \
+        if (dim == 2) {                                                                       \
+            if (dt == 0) return cubic ? FN<2, float, true>(__VA_ARGS__) : FN<2, float, false>(__VA_ARGS__);    \
+            return cubic ? FN<2, double, true>(__VA_ARGS__) : FN<2, double, false>(__VA_ARGS__);               \
+        }                                                                                     \
+        if (dt == 0) return cubic ? FN<3, float, true>(__VA_ARGS__) : FN<3, float, false>(__VA_ARGS__);        \
+        return cubic ? FN<3, double, true>(__VA_ARGS__) : FN<3, double, false>(__VA_ARGS__);                   \
+    } while (0)
+
+}  // namespace
+
+hipError_t launch_project_forw(int dim, int dt, bool cubic, const Geom& g, const void* rec, const void* rot,
+                               const void* shifts, void* out, hipStream_t s) {
+    TP_DISPATCH(dim, dt, cubic, forw, g, rec, rot, shifts, out, s);
+}
+
+hipError_t launch_project_back(int dim, int dt, bool cubic, const Geom& g, const void* gproj, const void* rec,
+                               const void* rot, const void* shifts, void* grec, void* grot, void* gshift,
+                               hipStream_t s) {
+    TP_DISPATCH(dim, dt, cubic, back, g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+}
+
+}  // namespace tp
