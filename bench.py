@@ -1,0 +1,302 @@
+"""Benchmark of the MI355X projector operators on one GPU.
+
+Default workload (the headline of the metric): one step = a 3D linear
+central-slice projection `project_3d_to_2d_forw` of a 2x-oversampled
+512x512x257 complex64 volume onto 2048 poses (256x129 rfft projections),
+followed by the weighted backprojection `backproject_2d_to_3d_forw` of those
+2048 projections into a 512x512x257 data volume and its float32 weight volume.
+
+Prints ONE JSON line: whole-step Fourier samples/s (samples = B*P*n*(n/2+1)
+per op), per-op rates, the HBM roofline of the dominant op (algorithmic
+bytes per call / its mean duration, measured with HIP events on the stream
+the kernels run on), and the reference CPU path timed on a bounded sample of
+the same inputs on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--no-cpu]
+Configs: headline (default), c1..c5.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "torch-projectors_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Fourier samples/s + % HBM peak, 3D proj+backproj, 256 box 2x oversampled"
+
+
+# ----------------------------------------------------------------------------- synthetic inputs
+def quat_rotations(P, gen):
+    """Uniform random rotations (normalised Gaussian quaternions) as 3x3, float32."""
+    import torch
+    q = torch.randn(P, 4, generator=gen, dtype=torch.float64)
+    q = q / q.norm(dim=1, keepdim=True)
+    w, x, y, z = q.unbind(1)
+    R = torch.stack([1 - 2 * (y * y + z * z), 2 * (x * y - z * w), 2 * (x * z + y * w),
+                     2 * (x * y + z * w), 1 - 2 * (x * x + z * z), 2 * (y * z - x * w),
+                     2 * (x * z - y * w), 2 * (y * z + x * w), 1 - 2 * (x * x + y * y)], 1)
+    return R.reshape(P, 3, 3).float()
+
+
+def angle_rotations(shape, gen):
+    import torch
+    a = torch.rand(*shape, generator=gen, dtype=torch.float64) * 2 * math.pi
+    c, s = torch.cos(a), torch.sin(a)
+    return torch.stack([c, -s, s, c], -1).reshape(*shape, 2, 2).float()
+
+
+def blob_volume_rfft(size, pad, n_blobs, radius, gen, dev):
+    """Sum of Gaussian blobs on a size^3 grid, zero-padded to pad^3, fftshifted
+    and rfft'd with norm='forward' (the reference's pad_and_fftshift recipe,
+    tests/test_utils.py:174-247) -> [1, pad, pad, pad//2+1] complex64."""
+    import torch
+    u = torch.rand(n_blobs, generator=gen, dtype=torch.float64)
+    d = torch.randn(n_blobs, 3, generator=gen, dtype=torch.float64)
+    d = d / d.norm(dim=1, keepdim=True)
+    mu = size / 2 + radius * u.pow(1 / 3)[:, None] * d
+    sigma = 2 + 4 * torch.rand(n_blobs, generator=gen, dtype=torch.float64)
+    amp = 0.5 + 0.5 * torch.rand(n_blobs, generator=gen, dtype=torch.float64)
+    ax = torch.arange(size, device=dev, dtype=torch.float32)
+    vol = torch.zeros(size, size, size, device=dev, dtype=torch.float32)
+    for k in range(n_blobs):
+        g = [torch.exp(-(ax - float(mu[k, a])) ** 2 / (2 * float(sigma[k]) ** 2)) for a in range(3)]
+        vol += float(amp[k]) * g[0][:, None, None] * g[1][None, :, None] * g[2][None, None, :]
+    lo = (pad - size) // 2
+    padded = torch.nn.functional.pad(vol, (lo, pad - size - lo) * 3)
+    spec = torch.fft.rfftn(torch.fft.fftshift(padded), norm="forward")
+    del vol, padded
+    return spec.to(torch.complex64).unsqueeze(0).contiguous()
+
+
+def noise_image_rfft(B, size, pad, gen, dev):
+    import torch
+    img = torch.randn(B, size, size, generator=gen).to(dev)
+    lo = (pad - size) // 2
+    padded = torch.nn.functional.pad(img, (lo, pad - size - lo) * 2)
+    return torch.fft.rfftn(torch.fft.fftshift(padded, dim=(-2, -1)), dim=(-2, -1), norm="forward").contiguous()
+
+
+def ctf2_weights(B, P, n, gen):
+    """sin^2(k*rho^2), rho = |frequency| / n in cycles/pixel, k ~ U(50, 200) per projection."""
+    import torch
+    i = torch.arange(n, dtype=torch.float64)
+    r = torch.where(i <= n // 2, i, i - n)
+    c = torch.arange(n // 2 + 1, dtype=torch.float64)
+    rho2 = (r[:, None] ** 2 + c[None, :] ** 2) / float(n * n)
+    k = 50 + 150 * torch.rand(B, P, 1, 1, generator=gen, dtype=torch.float64)
+    return torch.sin(k * rho2) ** 2
+
+
+# ----------------------------------------------------------------------------- byte model
+def active_counts(n, cutoff=None):
+    """(total, active forward, active scatter) pixels of one n x (n/2+1) projection
+    (projection_utils.h:61-76; scatters also skip j == 0, i >= n/2)."""
+    radius = cutoff if cutoff is not None else n / 2.0
+    r2 = float(radius) ** 2
+    total = fwd = bwd = 0
+    for i in range(n):
+        r = i if i <= n // 2 else i - n
+        for j in range(n // 2 + 1):
+            total += 1
+            if r * r + j * j > r2:
+                continue
+            fwd += 1
+            if not (j == 0 and i >= n // 2):
+                bwd += 1
+    return total, fwd, bwd
+
+
+def taps(dim, interp):
+    return (4 if interp == "linear" else 16) if dim == 2 else (8 if interp == "linear" else 64)
+
+
+def bytes_forward(npose, n, dim, interp, cutoff=None):
+    total, fwd, _ = active_counts(n, cutoff)
+    return npose * (fwd * (taps(dim, interp) * 8 + 8) + (total - fwd) * 8)
+
+
+def bytes_backproject(npose, n, dim, interp, vol_elems, weights, cutoff=None):
+    _, _, bwd = active_counts(n, cutoff)
+    per = 8 + (4 if weights else 0)
+    return npose * bwd * per * (1 + taps(dim, interp)) + vol_elems * per
+
+
+def bytes_project_back(npose, n, dim, interp, vol_elems, cutoff=None):
+    _, _, bwd = active_counts(n, cutoff)
+    t = taps(dim, interp)
+    return npose * bwd * (8 + t * 8 + t * 8) + vol_elems * 8
+
+
+def bytes_backproject_back(npose, n, dim, interp, weights, cutoff=None):
+    _, _, bwd = active_counts(n, cutoff)
+    lin = taps(dim, "linear")
+    return npose * bwd * (taps(dim, interp) * 8 + 16 + ((4 * lin + 4) if weights else 0))
+
+
+# ----------------------------------------------------------------------------- workloads
+class Workload:
+    """Inputs on the GPU, a step as a list of (op name, callable, bytes, samples)."""
+
+    def __init__(self, name, desc, ops, cpu_sample=None, config=None):
+        self.name, self.desc, self.ops, self.cpu_sample, self.config = name, desc, ops, cpu_sample, config or {}
+
+
+def make_headline(dev, k=0):
+    import torch
+    import torch_projectors as tp
+    gen = torch.Generator().manual_seed(20261201 + 6)
+    P, n, os_ = 2048, 256, 2.0
+    vol = blob_volume_rfft(256, 512, 32, 80.0, gen, dev)
+    rot = quat_rotations(P, gen)[None].to(dev)
+    sh = ((torch.rand(1, P, 2, generator=gen) * 16) - 8).to(dev)
+    w = ctf2_weights(1, P, n, gen).float().to(dev)
+    state = {}
+
+    def fwd():
+        state["proj"] = tp.project_3d_to_2d_forw(vol, rot, sh, output_shape=(n, n), interpolation="linear",
+                                                 oversampling=os_)
+
+    def bp():
+        state["bp"] = tp.backproject_2d_to_3d_forw(state["proj"], rot, weights=w, shifts=sh,
+                                                   interpolation="linear", oversampling=os_)
+
+    V = 512 * 512 * 257
+    samples = P * n * (n // 2 + 1)
+    ops = [("project_3d_to_2d_forw", fwd, bytes_forward(P, n, 3, "linear"), samples, P),
+           ("backproject_2d_to_3d_forw", bp, bytes_backproject(P, n, 3, "linear", V, True), samples, P)]
+
+    def cpu_sample(p_cpu, threads, cpu_ops):
+        """Run the same two ops on the first p_cpu poses on the CPU; returns seconds and samples."""
+        torch.cuda.synchronize()
+        vc, rc, sc, wc = vol.cpu(), rot[:, :p_cpu].cpu(), sh[:, :p_cpu].cpu(), w[:, :p_cpu].cpu()
+        pc = state["proj"][:, :p_cpu].cpu()
+        t0 = time.perf_counter()
+        cpu_ops.project_3d_to_2d_forw(vc, rc, sc, [n, n], "linear", os_, None)
+        t1 = time.perf_counter()
+        cpu_ops.backproject_2d_to_3d_forw(pc, wc, rc, sc, "linear", os_, None)
+        t2 = time.perf_counter()
+        return t2 - t0, 2 * p_cpu * n * (n // 2 + 1), {"fwd_s": t1 - t0, "bp_s": t2 - t1}
+
+    cfg = {"workload": "headline: project_3d_to_2d_forw + backproject_2d_to_3d_forw (weights), linear",
+           "volume": [1, 512, 512, 257], "poses": P, "proj": [n, n // 2 + 1], "oversampling": os_,
+           "interpolation": "linear", "shifts": "U(-8,8)", "weights": "sin^2(k rho^2)"}
+    return Workload("headline", cfg["workload"], ops, cpu_sample, cfg)
+
+
+WORKLOADS = {"headline": make_headline}
+
+
+# ----------------------------------------------------------------------------- CPU baseline
+def cpu_ops_and_kind():
+    from oracle import oracle as O
+    ref = O.ref_ops()
+    if ref is not None:
+        return ref, "reference"
+    return O, "port"
+
+
+def run_cpu_baseline(wl, target_s=12.0):
+    import torch
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    ops, kind = cpu_ops_and_kind()
+    # probe with a small sample, then scale to about target_s of CPU work
+    t, s, _ = wl.cpu_sample(16, threads, ops)
+    p = int(min(2048, max(16, 16 * target_s / max(t, 1e-3))))
+    t, s, parts = wl.cpu_sample(p, threads, ops)
+    return {"value": s / t, "unit": "Fourier samples/s", "cores": threads, "kind": kind,
+            "sample": f"first {p} of the workload's poses, both ops, one run each ({t:.1f} s; "
+                      f"fwd {parts['fwd_s']:.2f} s, bp {parts['bp_s']:.2f} s), {threads} threads"}
+
+
+# ----------------------------------------------------------------------------- main
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="headline", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (--gpus {a.gpus} requested); the multi-GPU "
+              "design (pose sharding + one volume all-reduce) is described in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    dev = torch.device("cuda:0")
+    wl = WORKLOADS[a.config](dev)
+    torch.cuda.synchronize()
+    log(f"inputs ready: {a.config}")
+
+    for _ in range(a.warmup):
+        for _, fn, *_rest in wl.ops:
+            fn()
+    torch.cuda.synchronize()
+
+    nops = len(wl.ops)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(nops + 1)] for _ in range(a.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(a.steps):
+        ev[s][0].record()
+        for k, (_, fn, *_rest) in enumerate(wl.ops):
+            fn()
+            ev[s][k + 1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    log(f"timed {a.steps} steps in {wall:.2f} s")
+    op_ms = [sum(ev[s][k].elapsed_time(ev[s][k + 1]) for s in range(a.steps)) / a.steps for k in range(nops)]
+    ms_step = sum(ev[s][0].elapsed_time(ev[s][nops]) for s in range(a.steps)) / a.steps
+
+    samples_step = sum(op[3] for op in wl.ops)
+    per_op = {}
+    for k, (name, _, nbytes, samples, poses) in enumerate(wl.ops):
+        sec = op_ms[k] / 1e3
+        per_op[name] = {"ms": round(op_ms[k], 4), "samples_per_s": samples / sec, "poses_per_s": poses / sec,
+                        "alg_GB": nbytes / 1e9, "alg_GBps": nbytes / sec / 1e9,
+                        "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS}
+    dom = max(range(nops), key=lambda k: op_ms[k])
+    dname, _, dbytes, _, _ = wl.ops[dom]
+    achieved = dbytes / (op_ms[dom] / 1e3) / 1e9
+    total_bytes = sum(op[2] for op in wl.ops)
+
+    cpu = None
+    if not a.no_cpu and wl.cpu_sample is not None:
+        log("cpu baseline ...")
+        cpu = run_cpu_baseline(wl)
+        log(f"cpu baseline: {cpu['sample']}")
+
+    out = {
+        "metric": METRIC,
+        "value": samples_step / (ms_step / 1e3),
+        "unit": "Fourier samples/s",
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": wl.config,
+        "poses_per_s": wl.ops[0][4] / (ms_step / 1e3),
+        "step_alg_GBps": total_bytes / (ms_step / 1e3) / 1e9,
+        "step_hbm_frac": total_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS,
+        "wall_s": round(wall, 3),
+        "ops": per_op,
+        "roofline": {"bound": "hbm", "kernel": dname, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()
