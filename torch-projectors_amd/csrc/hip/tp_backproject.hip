@@ -16,11 +16,37 @@ namespace {
 
 constexpr double kTwoPi = 6.283185307179586476925286766559;
 
-// One lane per projection pixel: v = proj * conj(phase) is spread over the
-// transposed stencil into the data volume, |tap weight| * w into the weight
-// volume, Friedel-aware, out-of-range taps dropped, and every x = 0 target
-// also feeds its Hermitian partner (projection_utils.h:371-406, 451-493;
-// weight lambdas cpu/3d/backprojection_2d_to_3d_kernels.cpp:245-285).
+// One projection pixel: v = proj * conj(phase) is spread over the transposed
+// stencil into the data volume, |tap weight| * w into the weight volume,
+// Friedel-aware, out-of-range taps dropped, and every x = 0 target also feeds
+// its Hermitian partner (projection_utils.h:371-406, 451-493; weight lambdas
+// cpu/3d/backprojection_2d_to_3d_kernels.cpp:245-285).
+template <int DIM, typename T, bool CUBIC, bool WEIGHTS>
+__device__ __forceinline__ void backproject_pixel(const Geom& g, Cx<T> v, T wpix, const T* __restrict__ R,
+                                                  const T* __restrict__ S, T r, T c, Cx<T>* __restrict__ db,
+                                                  T* __restrict__ wb) {
+    T x[3], sc, sr;
+    rotate<DIM>(R, r, c, g.os, x, sc, sr);
+    if (S) v = cmul(v, cconj(phase<T>(r, c, S[0], S[1], g.phase_k)));
+    const int N = g.N, H = g.H;
+    distribute<DIM, T, CUBIC>(x, [&](int d, int rr, int cc, T wd, T wr, T wc) {
+        bool cj;
+        const int64_t idx = scatter_index<DIM>(N, H, d, rr, cc, cj);
+        if (idx < 0) return;
+        Cx<T> tv = tap_value<DIM, T>(v, wd, wr, wc);
+        if (cj) tv.im = -tv.im;
+        atomic_add_cx(&db[idx], tv);
+        const int64_t m = cc == 0 ? mirror_index<DIM>(N, H, d, rr) : -1;
+        if (m >= 0) atomic_add_cx(&db[m], cconj(tv));
+        if (WEIGHTS) {
+            const T fw = wpix * tap_weight<DIM, T>(wd, wr, wc);
+            atomic_add(&wb[idx], fw);
+            if (m >= 0) atomic_add(&wb[m], fw);
+        }
+    });
+}
+
+// One lane per projection pixel, float atomics into the volumes.
 template <int DIM, typename T, bool CUBIC, bool WEIGHTS>
 __global__ __launch_bounds__(kBlock) void k_backproject_forw(Geom g, const Cx<T>* __restrict__ proj,
                                                              const T* __restrict__ weights,
@@ -37,33 +63,36 @@ __global__ __launch_bounds__(kBlock) void k_backproject_forw(Geom g, const Cx<T>
         const T r = freq_of<T>(i, g.n), c = T(j);
         if (filtered(r, c, cut2) || (j == 0 && i >= g.n / 2)) continue;
         const T* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * RS;
-        T x[3], sc, sr;
-        rotate<DIM>(R, r, c, g.os, x, sc, sr);
+        const T* S = shifts ? shifts + ((g.B_shift == 1 ? 0 : b) * g.P + p) * 2 : nullptr;
         const int64_t pidx = bp * g.npix + pix;
-        Cx<T> v = proj[pidx];
-        if (shifts) {
-            const T* S = shifts + ((g.B_shift == 1 ? 0 : b) * g.P + p) * 2;
-            v = cmul(v, cconj(phase<T>(r, c, S[0], S[1], g.phase_k)));
+        backproject_pixel<DIM, T, CUBIC, WEIGHTS>(g, proj[pidx], WEIGHTS ? weights[pidx] : T(0), R, S, r, c,
+                                                  data + b * g.vol, WEIGHTS ? wrec + b * g.vol : nullptr);
+    }
+}
+
+// The poses of an fp32 3D backprojection that are not rotations (the tiled
+// scatter has accumulated the others).  One block per pose.
+template <bool CUBIC, bool WEIGHTS>
+__global__ __launch_bounds__(kBlock) void k_backproject3_forw_rest(Geom g, const Cx<float>* __restrict__ proj,
+                                                                   const float* __restrict__ weights,
+                                                                   const float* __restrict__ rot,
+                                                                   const float* __restrict__ shifts,
+                                                                   Cx<float>* __restrict__ data,
+                                                                   float* __restrict__ wrec) {
+    const float cut2 = float(g.cut2);
+    for (int64_t bp = blockIdx.x; bp < g.B * g.P; bp += gridDim.x) {
+        const int64_t b = bp / g.P, p = bp - b * g.P;
+        const float* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * 9;
+        if (pose_is_rotation(R)) continue;
+        const float* S = shifts ? shifts + ((g.B_shift == 1 ? 0 : b) * g.P + p) * 2 : nullptr;
+        for (int pix = threadIdx.x; pix < g.npix; pix += kBlock) {
+            const int i = pix / g.hp, j = pix - i * g.hp;
+            const float r = freq_of<float>(i, g.n), c = float(j);
+            if (filtered(r, c, cut2) || (j == 0 && i >= g.n / 2)) continue;
+            const int64_t pidx = bp * g.npix + pix;
+            backproject_pixel<3, float, CUBIC, WEIGHTS>(g, proj[pidx], WEIGHTS ? weights[pidx] : 0.f, R, S, r, c,
+                                                        data + b * g.vol, WEIGHTS ? wrec + b * g.vol : nullptr);
         }
-        const T wpix = WEIGHTS ? weights[pidx] : T(0);
-        Cx<T>* db = data + b * g.vol;
-        T* wb = WEIGHTS ? wrec + b * g.vol : nullptr;
-        const int N = g.N, H = g.H;
-        distribute<DIM, T, CUBIC>(x, [&](int d, int rr, int cc, T wd, T wr, T wc) {
-            bool cj;
-            const int64_t idx = scatter_index<DIM>(N, H, d, rr, cc, cj);
-            if (idx < 0) return;
-            Cx<T> tv = tap_value<DIM, T>(v, wd, wr, wc);
-            if (cj) tv.im = -tv.im;
-            atomic_add_cx(&db[idx], tv);
-            const int64_t m = cc == 0 ? mirror_index<DIM>(N, H, d, rr) : -1;
-            if (m >= 0) atomic_add_cx(&db[m], cconj(tv));
-            if (WEIGHTS) {
-                const T fw = wpix * tap_weight<DIM, T>(wd, wr, wc);
-                atomic_add(&wb[idx], fw);
-                if (m >= 0) atomic_add(&wb[m], fw);
-            }
-        });
     }
 }
 
@@ -154,6 +183,21 @@ hipError_t forw(const Geom& g, const void* proj, const void* weights, const void
     return hipGetLastError();
 }
 
+template <bool CUBIC>
+hipError_t forw_rest(const Geom& g, const void* proj, const void* weights, const void* rot, const void* shifts,
+                     void* data, void* wrec, hipStream_t s) {
+    const unsigned grid = grid_for(g.B * g.P);
+    if (weights)
+        hipLaunchKernelGGL((k_backproject3_forw_rest<CUBIC, true>), dim3(grid), dim3(kBlock), 0, s, g,
+                           (const Cx<float>*)proj, (const float*)weights, (const float*)rot, (const float*)shifts,
+                           (Cx<float>*)data, (float*)wrec);
+    else
+        hipLaunchKernelGGL((k_backproject3_forw_rest<CUBIC, false>), dim3(grid), dim3(kBlock), 0, s, g,
+                           (const Cx<float>*)proj, (const float*)nullptr, (const float*)rot, (const float*)shifts,
+                           (Cx<float>*)data, (float*)nullptr);
+    return hipGetLastError();
+}
+
 template <int DIM, typename T, bool CUBIC, bool WG, bool ROT, bool SHIFT>
 hipError_t back8(const Geom& g, const void* gdata, const void* gw, const void* proj, const void* rot,
                  const void* shifts, void* gproj, void* gweights, void* grot, void* gshift, hipStream_t s) {
@@ -222,7 +266,11 @@ hipError_t launch_zero(void* p, int64_t words, hipStream_t s) {
 }
 
 hipError_t launch_backproject_forw(int dim, int dt, bool cubic, const Geom& g, const void* proj, const void* weights,
-                                   const void* rot, const void* shifts, void* data, void* wrec, hipStream_t s) {
+                                   const void* rot, const void* shifts, void* data, void* wrec, hipStream_t s,
+                                   bool rest_only) {
+    if (rest_only && dim == 3 && dt == 0)
+        return cubic ? forw_rest<true>(g, proj, weights, rot, shifts, data, wrec, s)
+                     : forw_rest<false>(g, proj, weights, rot, shifts, data, wrec, s);
     TP_DISPATCH(dim, dt, cubic, forw, g, proj, weights, rot, shifts, data, wrec, s);
 }
 

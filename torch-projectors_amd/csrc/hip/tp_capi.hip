@@ -85,6 +85,63 @@ int64_t rec_box(int64_t n, double os) {
     return raw + (raw % 2);
 }
 
+// The fp32 3D operators run the tile-owner kernels for rotation poses.
+bool use_tiles(int dim, int dtype, double os) { return dim == 3 && dtype == TP_F32 && os > 0.0 && std::isfinite(os); }
+
+// Poses per wavefront batch: 64 lanes hold one row of the pose's samples
+// each, so a batch takes 64 / rows poses (rows bounded for a box of width w).
+int poses_per_batch(double w, double eps, double os) {
+    // typical |b_c| + |b_r| + |b_d| of a unit column is about 1.5 (at most sqrt(3));
+    // poses with more rows take a second pass over their rows
+    const int rows = int(std::floor(1.5 * (w + 2.0 * eps) / os)) + 2;
+    return rows <= 16 ? 4 : (rows <= 32 ? 2 : 1);
+}
+
+tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
+    constexpr int L = tp::kTileEdge;
+    tp::TileSpec ts{};
+    // radius bound of the active pixels: the cutoff disc, within the pixel grid
+    const double grid_r = std::sqrt(2.0) * double(g.n / 2 + 1);
+    double cutr = g.cut2 >= 0.0 ? std::sqrt(g.cut2) : grid_r;
+    if (!std::isfinite(cutr) || cutr > grid_r) cutr = grid_r;
+    const double rho = g.os * cutr * 1.001 + 1.0;
+    const int half_tiles = int(std::ceil((rho + 2.0) / L));
+    ts.nt = 2 * half_tiles;
+    ts.org = -half_tiles * L;
+    const int half = g.N / 2;
+    ts.ntd = (g.N + tp::kScTD - 1) / tp::kScTD;
+    ts.ntr = (g.N + tp::kScTR - 1) / tp::kScTR;
+    ts.ntc = (g.H + tp::kScTC - 1) / tp::kScTC;
+    // Every random slice plane crosses the tiles around the origin, so those
+    // carry up to P poses each; they are split into pose ranges so that no
+    // single workgroup holds the critical path.  Core = tiles within `rc`
+    // voxels of the origin on every axis.
+    const int rc = 40;
+    ts.fc0 = std::max(0, (-rc - ts.org) / L);
+    ts.fc1 = std::min(ts.nt, (rc - ts.org) / L + 1);
+    ts.sd0 = std::max(0, (-rc + half - 1) / tp::kScTD);
+    ts.sd1 = std::min(ts.ntd, (rc + half - 1) / tp::kScTD + 1);
+    ts.sr0 = std::max(0, (-rc + half - 1) / tp::kScTR);
+    ts.sr1 = std::min(ts.ntr, (rc + half - 1) / tp::kScTR + 1);
+    ts.sc1 = std::min(ts.ntc, rc / tp::kScTC + 1);
+    const int64_t pk = 512;  // poses per range
+    ts.ksplit = int(std::max<int64_t>(1, (g.P + pk - 1) / pk));
+    ts.prange = int((g.P + ts.ksplit - 1) / ts.ksplit);
+    if (ts.ksplit == 1) ts.fc1 = ts.fc0 = ts.sd1 = ts.sd0 = ts.sr1 = ts.sr0 = ts.sc1 = 0;  // nothing to split
+    ts.rho = float(rho);
+    ts.eps = 0.5f;
+    ts.os = float(g.os);
+    ts.inv_os = float(1.0 / g.os);
+    ts.smax = float(g.os * (g.n + 2));
+    ts.kp_forw = poses_per_batch(L, ts.eps, g.os);
+    ts.kp_scatter = poses_per_batch(tp::kScTC + (cubic ? 3 : 1), ts.eps, g.os);
+    const int cl = int(std::floor(cutr)) + 1;
+    ts.cmax = std::min(g.n / 2, cl);
+    ts.rmin = std::max(g.n / 2 + 1 - g.n, -cl);
+    ts.rmax = std::min(g.n / 2, cl);
+    return ts;
+}
+
 int64_t cx_words(int dtype, int64_t elems) { return elems * (dtype == TP_F32 ? 2 : 4); }
 int64_t re_words(int dtype, int64_t elems) { return elems * (dtype == TP_F32 ? 1 : 2); }
 
@@ -122,8 +179,14 @@ int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int6
     TP_TRY(need(rot, "rotations"));
     TP_TRY(need(out, "projections"));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    return launched(tp::launch_project_forw(dim, dtype, interp == TP_CUBIC, g, rec, rot, shifts, out, s),
-                    "projection launch");
+    const bool cubic = interp == TP_CUBIC;
+    if (use_tiles(dim, dtype, os)) {
+        TP_TRY(launched(tp::launch_project3_forw_tiled(cubic, g, tile_spec(g, cubic), rec, rot, shifts, out, s),
+                        "tiled projection launch"));
+        return launched(tp::launch_project_forw(dim, dtype, cubic, g, rec, rot, shifts, out, s, true),
+                        "projection launch");
+    }
+    return launched(tp::launch_project_forw(dim, dtype, cubic, g, rec, rot, shifts, out, s), "projection launch");
 }
 
 int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, int64_t n, int64_t hp, const void* rec,
@@ -140,16 +203,22 @@ int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, in
     set_cut(dtype, has_cut, cut, g);
     g.os = os;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool cubic = interp == TP_CUBIC;
+    const bool tiles = use_tiles(dim, dtype, os) && g.work > 0;
     if (g.B > 0) TP_TRY(need(grec, "grad_reconstruction"));
-    TP_TRY(zero(grec, cx_words(dtype, g.B * g.vol), s));
+    if (!tiles) TP_TRY(zero(grec, cx_words(dtype, g.B * g.vol), s));
     TP_TRY(zero(grot, re_words(dtype, g.B_rot * g.P * dim * dim), s));
     TP_TRY(zero(gshift, re_words(dtype, g.B_shift * g.P * 2), s));
     if (g.work == 0) return TP_OK;
     TP_TRY(need(gproj, "grad_projections"));
     TP_TRY(need(rec, "reconstruction"));
     TP_TRY(need(rot, "rotations"));
-    return launched(tp::launch_project_back(dim, dtype, interp == TP_CUBIC, g, gproj, rec, rot, shifts, grec, grot,
-                                            gshift, s),
+    if (tiles)
+        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 1, g, tile_spec(g, cubic), gproj, nullptr, rot, shifts, grec,
+                                                  nullptr, s),
+                        "tiled reconstruction-gradient launch"));
+    return launched(tp::launch_project_back(dim, dtype, cubic, g, gproj, rec, rot, shifts, grec, grot, gshift, s,
+                                            tiles),
                     "projection backward launch");
 }
 
@@ -167,14 +236,22 @@ int backproject_forw(int dim, int dtype, const void* proj, int64_t B, int64_t P,
     set_cut(dtype, has_cut, cut, g);
     g.os = os;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool cubic = interp == TP_CUBIC;
+    const bool tiles = use_tiles(dim, dtype, os) && g.work > 0;
     if (g.B > 0) TP_TRY(need(data, "data_reconstruction"));
-    TP_TRY(zero(data, cx_words(dtype, g.B * g.vol), s));
-    TP_TRY(zero(wrec, re_words(dtype, g.B * g.vol), s));
+    if (!tiles) {
+        TP_TRY(zero(data, cx_words(dtype, g.B * g.vol), s));
+        TP_TRY(zero(wrec, re_words(dtype, g.B * g.vol), s));
+    }
     if (g.work == 0) return TP_OK;
     TP_TRY(need(proj, "projections"));
     TP_TRY(need(rot, "rotations"));
+    if (tiles)
+        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 0, g, tile_spec(g, cubic), proj, weights, rot, shifts, data, wrec,
+                                                  s),
+                        "tiled backprojection launch"));
     return launched(
-        tp::launch_backproject_forw(dim, dtype, interp == TP_CUBIC, g, proj, weights, rot, shifts, data, wrec, s),
+        tp::launch_backproject_forw(dim, dtype, cubic, g, proj, weights, rot, shifts, data, wrec, s, tiles),
         "backprojection launch");
 }
 

@@ -161,14 +161,16 @@ __device__ __forceinline__ Interp<T> interp2_cubic(const Cx<T>* __restrict__ rec
 }
 
 // Trilinear (interpolation_kernels.h:140-228): lerp along c, then r, then d.
-template <typename T, bool GRADS>
-__device__ __forceinline__ Interp<T> interp3_linear(const Cx<T>* __restrict__ rec, int N, int H, T d, T r, T c) {
+// `fetch(d, r, c)` returns the tap value the reference's sampler would return
+// for integer coordinates (global fetch3, or a staged copy of it in LDS).
+template <typename T, bool GRADS, typename F>
+__device__ __forceinline__ Interp<T> lerp3(F&& fetch, T d, T r, T c) {
     T dx, rx, cx;
     const int df = split(d, dx), rf = split(r, rx), cf = split(c, cx);
-    const Cx<T> p000 = fetch3(rec, N, H, df, rf, cf), p001 = fetch3(rec, N, H, df, rf, cf + 1);
-    const Cx<T> p010 = fetch3(rec, N, H, df, rf + 1, cf), p011 = fetch3(rec, N, H, df, rf + 1, cf + 1);
-    const Cx<T> p100 = fetch3(rec, N, H, df + 1, rf, cf), p101 = fetch3(rec, N, H, df + 1, rf, cf + 1);
-    const Cx<T> p110 = fetch3(rec, N, H, df + 1, rf + 1, cf), p111 = fetch3(rec, N, H, df + 1, rf + 1, cf + 1);
+    const Cx<T> p000 = fetch(df, rf, cf), p001 = fetch(df, rf, cf + 1);
+    const Cx<T> p010 = fetch(df, rf + 1, cf), p011 = fetch(df, rf + 1, cf + 1);
+    const Cx<T> p100 = fetch(df + 1, rf, cf), p101 = fetch(df + 1, rf, cf + 1);
+    const Cx<T> p110 = fetch(df + 1, rf + 1, cf), p111 = fetch(df + 1, rf + 1, cf + 1);
     const Cx<T> p00 = cadd(p000, cscale(csub(p001, p000), cx));
     const Cx<T> p01 = cadd(p010, cscale(csub(p011, p010), cx));
     const Cx<T> p10 = cadd(p100, cscale(csub(p101, p100), cx));
@@ -187,10 +189,15 @@ __device__ __forceinline__ Interp<T> interp3_linear(const Cx<T>* __restrict__ re
     }
     return o;
 }
+template <typename T, bool GRADS>
+__device__ __forceinline__ Interp<T> interp3_linear(const Cx<T>* __restrict__ rec, int N, int H, T d, T r, T c) {
+    return lerp3<T, GRADS>([&](int dd, int rr, int cc) { return fetch3(rec, N, H, dd, rr, cc); }, d, r, c);
+}
 
 // Tricubic (interpolation_kernels.h:345-425): sum over d, r, c of ((s*wd)*wr)*wc.
-template <typename T, bool GRADS>
-__device__ __forceinline__ Interp<T> interp3_cubic(const Cx<T>* __restrict__ rec, int N, int H, T d, T r, T c) {
+// `fetch` returns the pre-clamped tap of fetch3_cubic.
+template <typename T, bool GRADS, typename F>
+__device__ __forceinline__ Interp<T> cubic3(F&& fetch, T d, T r, T c) {
     T dx, rx, cx;
     const int df = split(d, dx), rf = split(r, rx), cf = split(c, cx);
     T wc[4], dwc[4], wr[4], dwr[4];
@@ -214,7 +221,7 @@ __device__ __forceinline__ Interp<T> interp3_cubic(const Cx<T>* __restrict__ rec
         for (int i = 0; i < 4; ++i) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const Cx<T> s = fetch3_cubic(rec, N, H, df + k - 1, rf + i - 1, cf + j - 1);
+                const Cx<T> s = fetch(df + k - 1, rf + i - 1, cf + j - 1);
                 o.v = cadd(o.v, cscale(cscale(cscale(s, wd), wr[i]), wc[j]));
                 if (GRADS) {
                     o.g[2] = cadd(o.g[2], cscale(cscale(cscale(s, dwd), wr[i]), wc[j]));
@@ -225,6 +232,10 @@ __device__ __forceinline__ Interp<T> interp3_cubic(const Cx<T>* __restrict__ rec
         }
     }
     return o;
+}
+template <typename T, bool GRADS>
+__device__ __forceinline__ Interp<T> interp3_cubic(const Cx<T>* __restrict__ rec, int N, int H, T d, T r, T c) {
+    return cubic3<T, GRADS>([&](int dd, int rr, int cc) { return fetch3_cubic(rec, N, H, dd, rr, cc); }, d, r, c);
 }
 
 template <int DIM, typename T, bool CUBIC, bool GRADS>
@@ -429,6 +440,18 @@ template <typename T> __device__ __forceinline__ Cx<T> phase(T r, T c, T s0, T s
     Cx<T> f;
     sin_cos(ph, &f.im, &f.re);
     return f;
+}
+
+// ---------------------------------------------------------------- pose classes
+// The tiled 3D kernels enumerate the samples of a pose through its slice
+// plane, which needs the first two rotation columns orthonormal (every
+// rotation matrix).  Other matrices (scaled, sheared, degenerate) take the
+// per-pixel kernels.  Both sides evaluate this same predicate.
+__device__ __forceinline__ bool pose_is_rotation(const float* __restrict__ R) {
+    const float aa = R[0] * R[0] + R[3] * R[3] + R[6] * R[6];
+    const float bb = R[1] * R[1] + R[4] * R[4] + R[7] * R[7];
+    const float ab = R[0] * R[1] + R[3] * R[4] + R[6] * R[7];
+    return fabsf(aa - 1.0f) <= 1e-4f && fabsf(bb - 1.0f) <= 1e-4f && fabsf(ab) <= 1e-4f;
 }
 
 // ---------------------------------------------------------------- atomics

@@ -22,6 +22,23 @@ struct Geom {
     int64_t work;                  // B*P*chunks
 };
 
+// Tile-owner enumeration parameters of the fp32 3D kernels (tp_tiled3d.hip).
+constexpr int kTileEdge = 16;                          // forward tiles: 16^3 voxels
+constexpr int kScTC = 16, kScTR = 16, kScTD = 8;        // scatter tiles (c, r, d): fp64 accumulators
+struct TileSpec {
+    int nt, org;              // forward: tiles per axis and signed origin of the tile grid
+    int fc0, fc1;             // forward core tiles (split by pose range): [fc0, fc1) on every axis
+    int ntd, ntr, ntc;        // scatter: tiles along d, r, c of the stored half volume
+    int sd0, sd1, sr0, sr1, sc1;  // scatter core tiles: [sd0, sd1) x [sr0, sr1) x [0, sc1)
+    int ksplit, prange;       // pose ranges per core tile, poses per range
+    float rho;                // bound on |x| of every active sample of a rotation pose
+    float eps;                // slack (voxels) added to every enumeration box
+    float os, inv_os;         // oversampling and its inverse
+    float smax;               // bound on |c*os| over the pixel grid
+    int cmax, rmin, rmax;     // pixel-grid limits of c and r (grid and cutoff)
+    int kp_forw, kp_scatter;  // poses per wavefront batch (1, 2 or 4)
+};
+
 constexpr int kBlock = 256;
 constexpr int64_t kMaxGrid = int64_t(1) << 22;
 
@@ -31,13 +48,28 @@ inline unsigned grid_for(int64_t work) { return unsigned(work < kMaxGrid ? work 
 hipError_t launch_zero(void* p, int64_t words, hipStream_t s);
 
 // Kernel launchers; `dim` is 2 or 3, `dt` 0 (fp32) or 1 (fp64).
+// `rest_only` (fp32 3D): only masked pixels and poses that are not rotations.
 hipError_t launch_project_forw(int dim, int dt, bool cubic, const Geom& g, const void* rec, const void* rot,
-                               const void* shifts, void* out, hipStream_t s);
+                               const void* shifts, void* out, hipStream_t s, bool rest_only = false);
+// `rest_only` (fp32 3D): the reconstruction-gradient scatter only for poses
+// that are not rotations; rotation/shift gradients for all poses.
 hipError_t launch_project_back(int dim, int dt, bool cubic, const Geom& g, const void* gproj, const void* rec,
                                const void* rot, const void* shifts, void* grec, void* grot, void* gshift,
-                               hipStream_t s);
+                               hipStream_t s, bool rest_only = false);
+// `rest_only` (fp32 3D): only poses that are not rotations.
 hipError_t launch_backproject_forw(int dim, int dt, bool cubic, const Geom& g, const void* proj, const void* weights,
-                                   const void* rot, const void* shifts, void* data, void* wrec, hipStream_t s);
+                                   const void* rot, const void* shifts, void* data, void* wrec, hipStream_t s,
+                                   bool rest_only = false);
+// fp32 3D tile-owner paths (rotation poses only; the per-pixel kernels with
+// `rest_only` complete the other poses and the masked pixels).
+hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* rec,
+                                      const void* rot, const void* shifts, void* out, hipStream_t s);
+// mode 0: backprojection into data (+ weights), with the x = 0 Hermitian completion;
+// mode 1: reconstruction gradient of the projection.
+hipError_t launch_scatter3_tiled(bool cubic, int mode, const Geom& g, const TileSpec& ts, const void* src,
+                                 const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
+                                 hipStream_t s);
+
 hipError_t launch_backproject_back(int dim, int dt, bool cubic, const Geom& g, const void* gdata, const void* gw,
                                    const void* proj, const void* rot, const void* shifts, void* gproj,
                                    void* gweights, void* grot, void* gshift, hipStream_t s);

@@ -21,6 +21,17 @@ namespace {
 
 constexpr double kTwoPi = 6.283185307179586476925286766559;
 
+// Value of one active pixel (frequency r, c) of one pose.
+template <int DIM, typename T, bool CUBIC>
+__device__ __forceinline__ Cx<T> project_pixel(const Geom& g, const Cx<T>* __restrict__ recb, const T* __restrict__ R,
+                                               const T* __restrict__ S, T r, T c) {
+    T x[3], sc, sr;
+    rotate<DIM>(R, r, c, g.os, x, sc, sr);
+    Cx<T> v = interpolate<DIM, T, CUBIC, false>(recb, g.N, g.H, x).v;
+    if (S) v = cmul(v, phase<T>(r, c, S[0], S[1], g.phase_k));
+    return v;
+}
+
 template <int DIM, typename T, bool CUBIC>
 __global__ __launch_bounds__(kBlock) void k_project_forw(Geom g, const Cx<T>* __restrict__ rec,
                                                          const T* __restrict__ rot, const T* __restrict__ shifts,
@@ -37,15 +48,34 @@ __global__ __launch_bounds__(kBlock) void k_project_forw(Geom g, const Cx<T>* __
         Cx<T> v = {0, 0};
         if (!filtered(r, c, cut2)) {
             const T* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * RS;
-            T x[3], sc, sr;
-            rotate<DIM>(R, r, c, g.os, x, sc, sr);
-            v = interpolate<DIM, T, CUBIC, false>(rec + b * g.vol, g.N, g.H, x).v;
-            if (shifts) {
-                const T* S = shifts + ((g.B_shift == 1 ? 0 : b) * g.P + p) * 2;
-                v = cmul(v, phase<T>(r, c, S[0], S[1], g.phase_k));
-            }
+            const T* S = shifts ? shifts + ((g.B_shift == 1 ? 0 : b) * g.P + p) * 2 : nullptr;
+            v = project_pixel<DIM, T, CUBIC>(g, rec + b * g.vol, R, S, r, c);
         }
         out[bp * g.npix + pix] = v;
+    }
+}
+
+// Completes the fp32 3D forward after the tiled kernel, which has written the
+// active pixels of rotation poses: zeros on masked pixels, and every pixel of
+// the other poses.  One block per pose.
+template <bool CUBIC>
+__global__ __launch_bounds__(kBlock) void k_project3_forw_rest(Geom g, const Cx<float>* __restrict__ rec,
+                                                               const float* __restrict__ rot,
+                                                               const float* __restrict__ shifts,
+                                                               Cx<float>* __restrict__ out) {
+    const float cut2 = float(g.cut2);
+    for (int64_t bp = blockIdx.x; bp < g.B * g.P; bp += gridDim.x) {
+        const int64_t b = bp / g.P, p = bp - b * g.P;
+        const float* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * 9;
+        const float* S = shifts ? shifts + ((g.B_shift == 1 ? 0 : b) * g.P + p) * 2 : nullptr;
+        const bool tiled = pose_is_rotation(R);
+        Cx<float>* outp = out + bp * g.npix;
+        for (int pix = threadIdx.x; pix < g.npix; pix += kBlock) {
+            const int i = pix / g.hp, j = pix - i * g.hp;
+            const float r = freq_of<float>(i, g.n), c = float(j);
+            if (filtered(r, c, cut2)) outp[pix] = Cx<float>{0.f, 0.f};
+            else if (!tiled) outp[pix] = project_pixel<3, float, CUBIC>(g, rec + b * g.vol, R, S, r, c);
+        }
     }
 }
 
@@ -54,7 +84,9 @@ __global__ __launch_bounds__(kBlock) void k_project_forw(Geom g, const Cx<T>* __
 // with out-of-range taps dropped and no x = 0 mirror
 // (projection_utils.h:336-362, 414-443).  Rotation and shift gradients are
 // per-pose sums, reduced across the block before one atomic per component.
-template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT>
+// REST (fp32 3D): the reconstruction gradient of rotation poses comes from
+// the tiled scatter; only the other poses are scattered here.
+template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT, bool REST>
 __global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __restrict__ gproj,
                                                          const Cx<T>* __restrict__ rec, const T* __restrict__ rot,
                                                          const T* __restrict__ shifts, Cx<T>* __restrict__ grec,
@@ -68,6 +100,11 @@ __global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __
         const int pix = int(w - bp * g.chunks) * kBlock + int(threadIdx.x);
         const int64_t b = bp / g.P, p = bp - b * g.P;
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
+        bool scatter = true;
+        if constexpr (REST) {
+            scatter = !pose_is_rotation(rot + (rb * g.P + p) * RS);
+            if (!scatter && !ROT && !SHIFT) continue;  // block-uniform
+        }
         T acc[K];
 #pragma unroll
         for (int k = 0; k < K; ++k) acc[k] = T(0);
@@ -84,14 +121,15 @@ __global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __
                 const Cx<T> gg = S ? cmul(g0, phase<T>(-r, -c, S[0], S[1], g.phase_k)) : g0;
                 Cx<T>* gb = grec + b * g.vol;
                 const int N = g.N, H = g.H;
-                distribute<DIM, T, CUBIC>(x, [&](int d, int rr, int cc, T wd, T wr, T wc) {
-                    bool cj;
-                    const int64_t idx = scatter_index<DIM>(N, H, d, rr, cc, cj);
-                    if (idx < 0) return;
-                    Cx<T> v = tap_value<DIM, T>(gg, wd, wr, wc);
-                    if (cj) v.im = -v.im;
-                    atomic_add_cx(&gb[idx], v);
-                });
+                if (scatter)
+                    distribute<DIM, T, CUBIC>(x, [&](int d, int rr, int cc, T wd, T wr, T wc) {
+                        bool cj;
+                        const int64_t idx = scatter_index<DIM>(N, H, d, rr, cc, cj);
+                        if (idx < 0) return;
+                        Cx<T> v = tap_value<DIM, T>(gg, wd, wr, wc);
+                        if (cj) v.im = -v.im;
+                        atomic_add_cx(&gb[idx], v);
+                    });
                 if (ROT || SHIFT) {
                     const Interp<T> it = interpolate<DIM, T, CUBIC, ROT>(rec + b * g.vol, N, H, x);
                     if (ROT) {
@@ -131,22 +169,30 @@ hipError_t forw(const Geom& g, const void* rec, const void* rot, const void* shi
     return hipGetLastError();
 }
 
-template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT>
+template <bool CUBIC>
+hipError_t forw_rest(const Geom& g, const void* rec, const void* rot, const void* shifts, void* out, hipStream_t s) {
+    hipLaunchKernelGGL(k_project3_forw_rest<CUBIC>, dim3(grid_for(g.B * g.P)), dim3(kBlock), 0, s, g,
+                       (const Cx<float>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
+    return hipGetLastError();
+}
+
+template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT, bool REST>
 hipError_t back4(const Geom& g, const void* gproj, const void* rec, const void* rot, const void* shifts, void* grec,
                  void* grot, void* gshift, hipStream_t s) {
-    hipLaunchKernelGGL((k_project_back<DIM, T, CUBIC, ROT, SHIFT>), dim3(grid_for(g.work)), dim3(kBlock), 0, s, g,
-                       (const Cx<T>*)gproj, (const Cx<T>*)rec, (const T*)rot, (const T*)shifts, (Cx<T>*)grec,
+    hipLaunchKernelGGL((k_project_back<DIM, T, CUBIC, ROT, SHIFT, REST>), dim3(grid_for(g.work)), dim3(kBlock), 0,
+                       s, g, (const Cx<T>*)gproj, (const Cx<T>*)rec, (const T*)rot, (const T*)shifts, (Cx<T>*)grec,
                        (T*)grot, (T*)gshift);
     return hipGetLastError();
 }
 
-template <int DIM, typename T, bool CUBIC>
+template <int DIM, typename T, bool CUBIC, bool REST = false>
 hipError_t back(const Geom& g, const void* gproj, const void* rec, const void* rot, const void* shifts, void* grec,
                 void* grot, void* gshift, hipStream_t s) {
-    if (grot && gshift) return back4<DIM, T, CUBIC, true, true>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
-    if (grot) return back4<DIM, T, CUBIC, true, false>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
-    if (gshift) return back4<DIM, T, CUBIC, false, true>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
-    return back4<DIM, T, CUBIC, false, false>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+    if (grot && gshift)
+        return back4<DIM, T, CUBIC, true, true, REST>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+    if (grot) return back4<DIM, T, CUBIC, true, false, REST>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+    if (gshift) return back4<DIM, T, CUBIC, false, true, REST>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+    return back4<DIM, T, CUBIC, false, false, REST>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
 }
 
 #define TP_DISPATCH(dim, dt, cubic, FN, ...)                                                  \
@@ -162,13 +208,18 @@ hipError_t back(const Geom& g, const void* gproj, const void* rec, const void* r
 }  // namespace
 
 hipError_t launch_project_forw(int dim, int dt, bool cubic, const Geom& g, const void* rec, const void* rot,
-                               const void* shifts, void* out, hipStream_t s) {
+                               const void* shifts, void* out, hipStream_t s, bool rest_only) {
+    if (rest_only && dim == 3 && dt == 0)
+        return cubic ? forw_rest<true>(g, rec, rot, shifts, out, s) : forw_rest<false>(g, rec, rot, shifts, out, s);
     TP_DISPATCH(dim, dt, cubic, forw, g, rec, rot, shifts, out, s);
 }
 
 hipError_t launch_project_back(int dim, int dt, bool cubic, const Geom& g, const void* gproj, const void* rec,
                                const void* rot, const void* shifts, void* grec, void* grot, void* gshift,
-                               hipStream_t s) {
+                               hipStream_t s, bool rest_only) {
+    if (rest_only && dim == 3 && dt == 0)
+        return cubic ? back<3, float, true, true>(g, gproj, rec, rot, shifts, grec, grot, gshift, s)
+                     : back<3, float, false, true>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
     TP_DISPATCH(dim, dt, cubic, back, g, gproj, rec, rot, shifts, grec, grot, gshift, s);
 }
 

@@ -1,0 +1,705 @@
+// Tile-owner kernels for the 3D operators (fp32).
+//
+// The reference walks poses and pixels and gathers/scatters each sample's
+// stencil straight from/to memory (cpu/3d/projection_3d_to_2d_kernels.cpp:156-209,
+// cpu/3d/backprojection_2d_to_3d_kernels.cpp:182-292).  At 2x oversampling
+// neighbouring samples are two voxels apart, so every sample touches ~4 fresh
+// cache lines, and the scatter is two float atomics per tap into HBM.
+//
+// Here a workgroup owns a tile of the volume held in LDS and inverts the
+// loop: it culls the poses whose slice plane crosses the tile, and for each
+// such pose enumerates exactly the grid samples whose stencil reaches the
+// tile (one lane per (pose, row) computes the row's column interval, a wave
+// prefix sum packs the samples of several poses densely onto the lanes).
+// The tiles around the origin are crossed by nearly every pose; they are
+// split into pose ranges ("core" work items) that are dispatched first.
+//
+//   k_forw3_tiled     forward projection.  The tile plus its stencil halo is
+//                     staged in LDS holding exactly the value the reference's
+//                     sampler returns for each integer coordinate (Friedel
+//                     conjugation, clamping and wrapping applied), over the
+//                     full signed frequency range, so the interpolation is
+//                     bit-identical.  A sample is computed by the one tile
+//                     that contains floor(x).
+//   k_scatter3_tiled  backprojection (data + weights) and the reconstruction
+//                     gradient of the projection backward.  Contributions are
+//                     accumulated in fp64 LDS (gfx950's LDS fp32 atomic add
+//                     runs at ~0.3 lanes/clk/CU, fp64 at ~2.6) and every
+//                     stored cell of the tile is written once with a plain
+//                     store: no zero fill and no global atomics, except for
+//                     the split core tiles, which add their partial tiles
+//                     into a zeroed region.  The Hermitian x = 0 mirror of
+//                     the backprojection is applied afterwards by k_mirror_x0.
+//
+// Only poses whose first two rotation columns are orthonormal take this path
+// (pose_is_rotation); the per-pixel kernels handle the others and write the
+// masked pixels of the forward.
+#include "tp_device.hh"
+#include "tp_launch.hh"
+
+namespace tp {
+
+namespace {
+
+constexpr int L = kTileEdge;  // forward tile edge (voxels)
+constexpr int SC = kScTC, SR = kScTR, SD = kScTD, S3 = SC * SR * SD;  // scatter tile
+constexpr int NW = kBlock / 64;
+
+__device__ __forceinline__ int to_int_clamped(float v) {
+    v = fminf(fmaxf(v, -1.0e8f), 1.0e8f);
+    return int(v);
+}
+
+// Does the slice plane (through the origin, spanned by columns 0 and 1 of R)
+// pass within the box [lo, hi] (x-order c, r, d)?
+__device__ __forceinline__ bool plane_hits(const float* R, const float* lo, const float* hi) {
+    const float n0 = R[3] * R[7] - R[6] * R[4];
+    const float n1 = R[6] * R[1] - R[0] * R[7];
+    const float n2 = R[0] * R[4] - R[3] * R[1];
+    const float m0 = 0.5f * (lo[0] + hi[0]), m1 = 0.5f * (lo[1] + hi[1]), m2 = 0.5f * (lo[2] + hi[2]);
+    const float h0 = 0.5f * (hi[0] - lo[0]), h1 = 0.5f * (hi[1] - lo[1]), h2 = 0.5f * (hi[2] - lo[2]);
+    return fabsf(n0 * m0 + n1 * m1 + n2 * m2) <= fabsf(n0) * h0 + fabsf(n1) * h1 + fabsf(n2) * h2;
+}
+
+// Range of sc = a.x (column 0) over the box; samples have sc >= 0.
+__device__ __forceinline__ bool half_plane_hits(const float* R, const float* hi, const float* lo) {
+    float uhi = 0.f;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const float a = R[3 * k];
+        uhi += a >= 0.f ? a * hi[k] : a * lo[k];
+    }
+    return uhi >= 0.f;
+}
+
+__device__ __forceinline__ bool pose_hits(const float* R, const float* lo, const float* hi) {
+    return pose_is_rotation(R) && plane_hits(R, lo, hi) && half_plane_hits(R, hi, lo);
+}
+
+// Rows r (sr = r*os = b.x, b = column 1) whose samples can lie in the box.
+__device__ __forceinline__ void box_rows(const float* R, const float* lo, const float* hi, const TileSpec& ts,
+                                         int& r0, int& r1) {
+    float vlo = 0.f, vhi = 0.f;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const float b = R[3 * k + 1];
+        vlo += b >= 0.f ? b * lo[k] : b * hi[k];
+        vhi += b >= 0.f ? b * hi[k] : b * lo[k];
+    }
+    r0 = max(ts.rmin, to_int_clamped(ceilf(vlo * ts.inv_os)));
+    r1 = min(ts.rmax, to_int_clamped(floorf(vhi * ts.inv_os)));
+}
+
+// Columns c of row r whose sample x = c*os*a + r*os*b lies in the box (the
+// box already carries the slack that covers rounding), within the pixel grid
+// and (up to one column) the cutoff disc.
+__device__ __forceinline__ void row_span(const float* R, int r, const float* lo, const float* hi, const TileSpec& ts,
+                                         float cut2, int& c0, int& c1) {
+    const float ros = float(r) * ts.os;
+    float l = -3.0e38f, h = 3.0e38f;
+    bool empty = false;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const float a = R[3 * k], base = ros * R[3 * k + 1];
+        const float lk = lo[k] - base, hk = hi[k] - base;  // need a*sc in [lk, hk]
+        if (fabsf(a) > 1e-6f) {
+            const float ia = __builtin_amdgcn_rcpf(a);
+            const float u0 = lk * ia, u1 = hk * ia;
+            l = fmaxf(l, a > 0.f ? u0 : u1);
+            h = fminf(h, a > 0.f ? u1 : u0);
+        } else {
+            const float tol = fabsf(a) * ts.smax;
+            empty |= lk > tol || hk < -tol;
+        }
+    }
+    c0 = max(0, to_int_clamped(ceilf(l * ts.inv_os - 1e-3f)));
+    c1 = min(ts.cmax, to_int_clamped(floorf(h * ts.inv_os + 1e-3f)));
+    const float rem = cut2 - float(r) * float(r);
+    if (empty || rem < 0.f) c1 = -1;
+    else c1 = min(c1, int(sqrtf(rem)) + 1);
+}
+
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(v, off, 64);
+        if (lane >= off) v += t;
+    }
+    return v;
+}
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
+    return v;
+}
+// Lane owning flattened index e: the first lane whose inclusive count exceeds e.
+__device__ __forceinline__ int owner_lane(int incl, int e) {
+    int lw = 0;
+#pragma unroll
+    for (int step = 32; step >= 1; step >>= 1)
+        if (__shfl(incl, lw + step - 1, 64) <= e) lw += step;
+    return lw;
+}
+
+// Per-wave copy of the poses of one batch.
+struct Slot {
+    float R[9];
+    float s0, s1;
+    int p;
+    int r0a, r1a;  // scatter: rows of box 1 (pass-2 de-duplication)
+};
+
+__device__ __forceinline__ void load_rot(const float* __restrict__ Rg, float* R) {
+#pragma unroll
+    for (int e = 0; e < 9; ++e) R[e] = Rg[e];
+}
+
+// Work items: first the core tiles, one item per (batch, tile, pose range),
+// then every tile of every batch with all poses (core tiles skipped there).
+struct Item {
+    int64_t b;
+    int kd, kr, kc;
+    int p0, p1;
+    bool core, skip;
+};
+__device__ __forceinline__ Item item_of(int64_t w, int64_t B, int P, int nd, int nr, int nc, int d0, int d1, int r0,
+                                        int r1, int c0, int c1, int ksplit, int prange) {
+    Item it;
+    const int cd = d1 - d0, cr = r1 - r0, cc = c1 - c0;
+    const int64_t ncore = int64_t(cd) * cr * cc * ksplit;
+    it.skip = false;
+    if (w < B * ncore) {
+        it.core = true;
+        it.b = w / ncore;
+        int64_t q = w - it.b * ncore;
+        const int j = int(q % ksplit);
+        q /= ksplit;
+        it.kc = c0 + int(q % cc);
+        it.kr = r0 + int((q / cc) % cr);
+        it.kd = d0 + int(q / (int64_t(cc) * cr));
+        it.p0 = j * prange;
+        it.p1 = min(P, it.p0 + prange);
+    } else {
+        it.core = false;
+        const int64_t per_b = int64_t(nd) * nr * nc;
+        const int64_t q = w - B * ncore;
+        it.b = q / per_b;
+        const int t = int(q - it.b * per_b);
+        it.kc = t % nc;
+        it.kr = (t / nc) % nr;
+        it.kd = t / (nc * nr);
+        it.p0 = 0;
+        it.p1 = P;
+        it.skip = ksplit > 1 && it.kd >= d0 && it.kd < d1 && it.kr >= r0 && it.kr < r1 && it.kc >= c0 && it.kc < c1;
+    }
+    return it;
+}
+
+// Poses culled per phase: each lane tests 4, the survivors' indices (relative
+// to the phase) go to an LDS list.
+constexpr int kCullPerLane = 4;
+constexpr int kCullInFlight = 2;  // rotations loaded together per lane
+constexpr int kChunk = kBlock * kCullPerLane;
+
+// Cull poses [pbase, pbase + kChunk) against up to two boxes; returns the count.
+template <bool TWO>
+__device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pend, int pbase, const float* lo1,
+                                          const float* hi1, const float* lo2, const float* hi2,
+                                          unsigned short* plist, int* pcount) {
+    __syncthreads();  // every lane has read the previous count and list
+    if (threadIdx.x == 0) *pcount = 0;
+    __syncthreads();
+#pragma unroll 1
+    for (int q0 = 0; q0 < kCullPerLane; q0 += kCullInFlight) {
+        float R[kCullInFlight][9];
+#pragma unroll
+        for (int q = 0; q < kCullInFlight; ++q) {
+            const int p = min(pbase + int(threadIdx.x) + (q0 + q) * kBlock, pend - 1);
+            load_rot(rotb + int64_t(p) * 9, R[q]);
+        }
+#pragma unroll
+        for (int q = 0; q < kCullInFlight; ++q) {
+            const int p = pbase + int(threadIdx.x) + (q0 + q) * kBlock;
+            if (p >= pend) continue;
+            const bool hit = pose_hits(R[q], lo1, hi1) || (TWO && pose_hits(R[q], lo2, hi2));
+            if (hit) plist[atomicAdd(pcount, 1)] = (unsigned short)(p - pbase);
+        }
+    }
+    __syncthreads();
+    const int np = *pcount;
+    return np;
+}
+
+// ----------------------------------------------------------------------------- forward
+template <bool CUBIC, int KP>
+__global__ __launch_bounds__(kBlock) void k_forw3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ rec,
+                                                        const float* __restrict__ rot,
+                                                        const float* __restrict__ shifts,
+                                                        Cx<float>* __restrict__ out) {
+    constexpr int LO = CUBIC ? 1 : 0, HI = CUBIC ? 2 : 1, W = L + LO + HI, W3 = W * W * W;
+    constexpr int RPS = 64 / KP;
+    constexpr int LOADS = (W3 + kBlock - 1) / kBlock;
+    __shared__ Cx<float> vt[W3];
+    __shared__ unsigned short plist[kChunk];
+    __shared__ int pcount;
+    __shared__ Slot slots[NW][KP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int slot = lane / RPS, jrow = lane % RPS;
+    const int nt = ts.nt;
+    const int64_t items = g.B * (int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * ts.ksplit +
+                                 int64_t(nt) * nt * nt);
+    const float cut2 = float(g.cut2);
+    const float rho2 = ts.rho * ts.rho;
+    const int N = g.N, H = g.H;
+    for (int64_t w = blockIdx.x; w < items; w += gridDim.x) {
+        const Item it = item_of(w, g.B, int(g.P), nt, nt, nt, ts.fc0, ts.fc1, ts.fc0, ts.fc1, ts.fc0, ts.fc1,
+                                ts.ksplit, ts.prange);
+        if (it.skip) continue;
+        const int64_t b = it.b;
+        const int tc = ts.org + it.kc * L, tr = ts.org + it.kr * L, td = ts.org + it.kd * L;
+        // samples owned by this tile: floor(x) in [t, t + L) on every axis (+ slack)
+        const float lo[3] = {float(tc) - ts.eps, float(tr) - ts.eps, float(td) - ts.eps};
+        const float hi[3] = {float(tc + L) + ts.eps, float(tr + L) + ts.eps, float(td + L) + ts.eps};
+        float dist2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const float q = lo[k] > 0.f ? lo[k] : (hi[k] < 0.f ? -hi[k] : 0.f);
+            dist2 += q * q;
+        }
+        if (dist2 > rho2) continue;
+        const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
+        const float* rotb = rot + rb * g.P * 9;
+        const Cx<float>* recb = rec + b * g.vol;
+        auto lds = [&](int d, int r, int c) {
+            return vt[((d - (td - LO)) * W + (r - (tr - LO))) * W + (c - (tc - LO))];
+        };
+        bool loaded = false;
+        for (int pbase = it.p0; pbase < it.p1; pbase += kChunk) {
+            const int np = cull_chunk<false>(rotb, it.p1, pbase, lo, hi, lo, hi, plist, &pcount);
+            if (np == 0) continue;
+            if (!loaded) {
+                // stage the tile and its halo, STAGE loads in flight per lane
+                constexpr int STAGE = 8;
+#pragma unroll 1
+                for (int q0 = 0; q0 < LOADS; q0 += STAGE) {
+                    Cx<float> v[STAGE];
+#pragma unroll
+                    for (int q = 0; q < STAGE; ++q) {
+                        const int cell = min(tid + (q0 + q) * kBlock, W3 - 1);
+                        const int lc = cell % W, lr = (cell / W) % W, ld = cell / (W * W);
+                        const int d = td - LO + ld, r = tr - LO + lr, c = tc - LO + lc;
+                        v[q] = CUBIC ? fetch3_cubic(recb, N, H, d, r, c) : fetch3(recb, N, H, d, r, c);
+                    }
+#pragma unroll
+                    for (int q = 0; q < STAGE; ++q)
+                        if (tid + (q0 + q) * kBlock < W3) vt[tid + (q0 + q) * kBlock] = v[q];
+                }
+                __syncthreads();
+                loaded = true;
+            }
+            // wave batches of KP poses; the next batch's rotations load during this one
+            int base = wave * KP;
+            float Rn[9];
+            load_rot(rotb + int64_t(pbase + plist[min(base + slot, np - 1)]) * 9, Rn);
+            for (; base < np; base += NW * KP) {
+                const bool sv = base + slot < np;
+                const int pp = pbase + plist[min(base + slot, np - 1)];
+                float R[9];
+#pragma unroll
+                for (int e = 0; e < 9; ++e) R[e] = Rn[e];
+                if (base + NW * KP < np)
+                    load_rot(rotb + int64_t(pbase + plist[min(base + NW * KP + slot, np - 1)]) * 9, Rn);
+                if (jrow == 0 && sv) {
+                    Slot& sd = slots[wave][slot];
+#pragma unroll
+                    for (int e = 0; e < 9; ++e) sd.R[e] = R[e];
+                    const float* S = shifts ? shifts + (sb * g.P + pp) * 2 : nullptr;
+                    sd.s0 = S ? S[0] : 0.f;
+                    sd.s1 = S ? S[1] : 0.f;
+                    sd.p = pp;
+                }
+                __builtin_amdgcn_wave_barrier();
+                int r0, r1;
+                box_rows(R, lo, hi, ts, r0, r1);
+                const int nr = sv ? max(0, r1 - r0 + 1) : 0;
+                const int maxnr = wave_max(nr);
+                for (int rbase = 0; rbase < maxnr; rbase += RPS) {
+                    const int jr = rbase + jrow;
+                    const int r = r0 + jr;
+                    int c0 = 0, cnt = 0;
+                    if (jr < nr) {
+                        int c1;
+                        row_span(R, r, lo, hi, ts, cut2, c0, c1);
+                        cnt = max(0, c1 - c0 + 1);
+                    }
+                    const int incl = wave_incl_scan(cnt);
+                    const int excl = incl - cnt;
+                    const int total = __shfl(incl, 63, 64);
+                    for (int e0 = 0; e0 < total; e0 += 64) {
+                        const int e = e0 + lane;
+                        const int es = min(e, total - 1);
+                        const int lw = owner_lane(incl, es);
+                        const int rr = __shfl(r, lw, 64);
+                        const int cc = __shfl(c0, lw, 64) + (es - __shfl(excl, lw, 64));
+                        if (e >= total) continue;
+                        const Slot& sd = slots[wave][lw / RPS];
+                        const float fr = float(rr), fc = float(cc);
+                        if (filtered(fr, fc, cut2)) continue;
+                        float x[3], sc, sr;
+                        rotate<3>(sd.R, fr, fc, g.os, x, sc, sr);
+                        const int fxc = int(floorf(x[0])), fxr = int(floorf(x[1])), fxd = int(floorf(x[2]));
+                        if (fxc < tc || fxc >= tc + L || fxr < tr || fxr >= tr + L || fxd < td || fxd >= td + L)
+                            continue;
+                        Cx<float> v = CUBIC ? cubic3<float, false>(lds, x[2], x[1], x[0]).v
+                                            : lerp3<float, false>(lds, x[2], x[1], x[0]).v;
+                        if (shifts) v = cmul(v, phase<float>(fr, fc, sd.s0, sd.s1, g.phase_k));
+                        const int i = rr >= 0 ? rr : rr + g.n;
+                        out[(b * g.P + sd.p) * int64_t(g.npix) + i * g.hp + cc] = v;
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+            __syncthreads();
+        }
+        if (loaded) __syncthreads();
+    }
+}
+
+// ----------------------------------------------------------------------------- scatter
+// Per-sample work of the scatter: value and weight of a projection pixel,
+// spread over the stencil taps that land in the tile (LDS float atomics).
+template <bool CUBIC, int MODE, bool WEIGHTS>
+__device__ __forceinline__ void scatter_sample(const Geom& g, const Slot& sd, int rr, int cc, Cx<float> v, float wpix,
+                                               bool shifted, int tc, int tr, int td, double* acc_re, double* acc_im,
+                                               double* acc_w) {
+    const int H = g.H, half = g.N / 2;
+    const float fr = float(rr), fc = float(cc);
+    float x[3], sc, sr;
+    rotate<3>(sd.R, fr, fc, g.os, x, sc, sr);
+    if (shifted) {
+        if (MODE == 0) v = cmul(v, cconj(phase<float>(fr, fc, sd.s0, sd.s1, g.phase_k)));
+        else v = cmul(v, phase<float>(-fr, -fc, sd.s0, sd.s1, g.phase_k));
+    }
+    distribute<3, float, CUBIC>(x, [&](int d, int tr2, int tc2, float wd, float wr, float wc) {
+        const bool cj = tc2 < 0;
+        if (cj) {
+            tc2 = -tc2;
+            tr2 = -tr2;
+            d = -d;
+        }
+        // dropped taps (projection_utils.h:431-438) never fall in a stored tile
+        const int lc = tc2 - tc, lr = tr2 - tr, ld = d - td;
+        if ((unsigned)lc >= (unsigned)SC || (unsigned)lr >= (unsigned)SR || (unsigned)ld >= (unsigned)SD) return;
+        if (tc2 >= H || tr2 > half || d > half) return;
+        Cx<float> tv = tap_value<3, float>(v, wd, wr, wc);
+        if (cj) tv.im = -tv.im;
+        const int li = (ld * SR + lr) * SC + lc;
+        atomicAdd(&acc_re[li], double(tv.re));
+        atomicAdd(&acc_im[li], double(tv.im));
+        if (WEIGHTS) atomicAdd(&acc_w[li], double(wpix * tap_weight<3, float>(wd, wr, wc)));
+    });
+}
+
+// MODE 0: backprojection, v = proj * conj(phase(r, c)), optional weights.
+// MODE 1: reconstruction gradient of the projection, v = g * phase(-r, -c).
+template <bool CUBIC, int MODE, bool WEIGHTS, int KP>
+__global__ __launch_bounds__(kBlock) void k_scatter3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ src,
+                                                           const float* __restrict__ weights,
+                                                           const float* __restrict__ rot,
+                                                           const float* __restrict__ shifts,
+                                                           Cx<float>* __restrict__ dst, float* __restrict__ wdst) {
+    constexpr int SL = CUBIC ? 2 : 1, SH = CUBIC ? 1 : 0;  // stencil reach below / above floor(x)
+    constexpr int RPS = 64 / KP;
+    __shared__ double acc_re[S3], acc_im[S3];
+    __shared__ double acc_w[WEIGHTS ? S3 : 1];
+    __shared__ unsigned short plist[kChunk];
+    __shared__ int pcount;
+    __shared__ Slot slots[NW][KP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int slot = lane / RPS, jrow = lane % RPS;
+    const int N = g.N, H = g.H, half = N / 2;
+    const int64_t items = g.B * (int64_t(ts.sd1 - ts.sd0) * (ts.sr1 - ts.sr0) * ts.sc1 * ts.ksplit +
+                                 int64_t(ts.ntd) * ts.ntr * ts.ntc);
+    const float cut2 = float(g.cut2);
+    for (int64_t w = blockIdx.x; w < items; w += gridDim.x) {
+        const Item it = item_of(w, g.B, int(g.P), ts.ntd, ts.ntr, ts.ntc, ts.sd0, ts.sd1, ts.sr0, ts.sr1, 0, ts.sc1,
+                                ts.ksplit, ts.prange);
+        if (it.skip) continue;
+        const int64_t b = it.b;
+        // stored cells of this tile, signed coordinates: d, r in [-N/2+1, N/2], c in [0, N/2]
+        const int tc = it.kc * SC, tr = -half + 1 + it.kr * SR, td = -half + 1 + it.kd * SD;
+        // direct taps land here when x is in box 1 (the tile dilated by the stencil);
+        // flipped (c < 0) taps when x is in box 2 (the same around the negated tile)
+        const int fc0 = -tc - SC + 1, fr0 = -tr - SR + 1, fd0 = -td - SD + 1;
+        const float lo1[3] = {float(tc - SL) - ts.eps, float(tr - SL) - ts.eps, float(td - SL) - ts.eps};
+        const float hi1[3] = {float(tc + SC + SH) + ts.eps, float(tr + SR + SH) + ts.eps,
+                              float(td + SD + SH) + ts.eps};
+        const float lo2[3] = {float(fc0 - SL) - ts.eps, float(fr0 - SL) - ts.eps, float(fd0 - SL) - ts.eps};
+        const float hi2[3] = {float(fc0 + SC + SH) + ts.eps, float(fr0 + SR + SH) + ts.eps,
+                              float(fd0 + SD + SH) + ts.eps};
+        for (int e = tid; e < S3; e += kBlock) {
+            acc_re[e] = 0.0;
+            acc_im[e] = 0.0;
+            if (WEIGHTS) acc_w[e] = 0.0;
+        }
+        const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
+        const float* rotb = rot + rb * g.P * 9;
+        const int64_t pose0 = b * g.P;
+
+        for (int pbase = it.p0; pbase < it.p1; pbase += kChunk) {
+            const int np = cull_chunk<true>(rotb, it.p1, pbase, lo1, hi1, lo2, hi2, plist, &pcount);
+            int base = wave * KP;
+            float Rn[9];
+            if (base < np) load_rot(rotb + int64_t(pbase + plist[min(base + slot, np - 1)]) * 9, Rn);
+            for (; base < np; base += NW * KP) {
+                const bool sv = base + slot < np;
+                const int pp = pbase + plist[min(base + slot, np - 1)];
+                float R[9];
+#pragma unroll
+                for (int e = 0; e < 9; ++e) R[e] = Rn[e];
+                if (base + NW * KP < np)
+                    load_rot(rotb + int64_t(pbase + plist[min(base + NW * KP + slot, np - 1)]) * 9, Rn);
+                int ra0, ra1;
+                box_rows(R, lo1, hi1, ts, ra0, ra1);
+                if (jrow == 0 && sv) {
+                    Slot& sd = slots[wave][slot];
+#pragma unroll
+                    for (int e = 0; e < 9; ++e) sd.R[e] = R[e];
+                    const float* S = shifts ? shifts + (sb * g.P + pp) * 2 : nullptr;
+                    sd.s0 = S ? S[0] : 0.f;
+                    sd.s1 = S ? S[1] : 0.f;
+                    sd.p = pp;
+                    sd.r0a = ra0;
+                    sd.r1a = ra1;
+                }
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll 1
+                for (int pass = 0; pass < 2; ++pass) {
+                    float lo[3], hi[3];
+#pragma unroll
+                    for (int k = 0; k < 3; ++k) {
+                        lo[k] = pass == 0 ? lo1[k] : lo2[k];
+                        hi[k] = pass == 0 ? hi1[k] : hi2[k];
+                    }
+                    int r0, r1;
+                    if (pass == 0) {
+                        r0 = ra0;
+                        r1 = ra1;
+                    } else {
+                        box_rows(R, lo, hi, ts, r0, r1);
+                    }
+                    const int nr = sv ? max(0, r1 - r0 + 1) : 0;
+                    const int maxnr = wave_max(nr);
+                    for (int rbase = 0; rbase < maxnr; rbase += RPS) {
+                        const int jr = rbase + jrow;
+                        const int r = r0 + jr;
+                        int c0 = 0, cnt = 0;
+                        if (jr < nr) {
+                            int c1;
+                            row_span(R, r, lo, hi, ts, cut2, c0, c1);
+                            cnt = max(0, c1 - c0 + 1);
+                        }
+                        const int incl = wave_incl_scan(cnt);
+                        const int excl = incl - cnt;
+                        const int total = __shfl(incl, 63, 64);
+                        // sample e of this row block: owner lane, pixel, validity, and its loads
+                        auto fetch_sample = [&](int e, int& rr, int& cc, int& sl, bool& ok, Cx<float>& v,
+                                                float& wv) {
+                            const int es = min(e, total - 1);
+                            const int lw = owner_lane(incl, es);
+                            rr = __shfl(r, lw, 64);
+                            cc = __shfl(c0, lw, 64) + (es - __shfl(excl, lw, 64));
+                            sl = lw / RPS;
+                            ok = e < total;
+                            const Slot& sd = slots[wave][sl];
+                            if (ok && pass == 1 && rr >= sd.r0a && rr <= sd.r1a) {
+                                int a0, a1;  // already enumerated by box 1?
+                                row_span(sd.R, rr, lo1, hi1, ts, cut2, a0, a1);
+                                ok = cc < a0 || cc > a1;
+                            }
+                            ok = ok && !filtered(float(rr), float(cc), cut2) &&
+                                 !(cc == 0 && (rr == g.n / 2 || rr < 0));  // Friedel half of x = 0
+                            const int i = rr >= 0 ? rr : rr + g.n;
+                            const int64_t pidx = (pose0 + sd.p) * int64_t(g.npix) + i * g.hp + cc;
+                            v = ok ? src[pidx] : Cx<float>{0.f, 0.f};
+                            wv = (WEIGHTS && ok) ? weights[pidx] : 0.f;
+                        };
+                        int rr, cc, sl;
+                        bool ok;
+                        Cx<float> v;
+                        float wv;
+                        fetch_sample(lane, rr, cc, sl, ok, v, wv);
+                        for (int e0 = 0; e0 < total; e0 += 64) {
+                            // the next sample's loads are in flight while this one is spread
+                            int rr2 = 0, cc2 = 0, sl2 = 0;
+                            bool ok2 = false;
+                            Cx<float> v2 = {0.f, 0.f};
+                            float wv2 = 0.f;
+                            if (e0 + 64 < total) fetch_sample(e0 + 64 + lane, rr2, cc2, sl2, ok2, v2, wv2);
+                            if (ok)
+                                scatter_sample<CUBIC, MODE, WEIGHTS>(g, slots[wave][sl], rr, cc, v, wv,
+                                                                     shifts != nullptr, tc, tr, td, acc_re, acc_im,
+                                                                     acc_w);
+                            rr = rr2;
+                            cc = cc2;
+                            sl = sl2;
+                            ok = ok2;
+                            v = v2;
+                            wv = wv2;
+                        }
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+            __syncthreads();
+        }
+
+        // write every stored cell of the tile once (core pieces add into a zeroed region)
+        __syncthreads();
+        for (int e = tid; e < S3; e += kBlock) {
+            const int lc = e % SC, lr = (e / SC) % SR, ld = e / (SC * SR);
+            const int c = tc + lc, r = tr + lr, d = td + ld;
+            if (c >= H || r > half || d > half) continue;
+            const int re = r < 0 ? r + N : r, de = d < 0 ? d + N : d;
+            const int64_t idx = b * g.vol + (int64_t(de) * N + re) * H + c;
+            if (it.core) {
+                atomic_add(&dst[idx].re, float(acc_re[e]));
+                atomic_add(&dst[idx].im, float(acc_im[e]));
+                if (WEIGHTS) atomic_add(&wdst[idx], float(acc_w[e]));
+            } else {
+                dst[idx] = Cx<float>{float(acc_re[e]), float(acc_im[e])};
+                if (WEIGHTS) wdst[idx] = float(acc_w[e]);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Hermitian completion of the x = 0 plane after an unmirrored accumulation:
+// every x = 0 contribution v of the reference is also added, conjugated, at
+// the partner cell (-d, -r) (projection_utils.h:481-492), so the final value
+// of a cell is A(X) + conj(A(mirror X)) (weights: A_w(X) + A_w(mirror X)).
+// One lane per unordered pair {X, mirror X}; self-partnered cells are kept.
+template <bool WEIGHTS>
+__global__ __launch_bounds__(kBlock) void k_mirror_x0(Geom g, Cx<float>* __restrict__ dst,
+                                                      float* __restrict__ wdst) {
+    const int N = g.N, H = g.H;
+    const int64_t plane = int64_t(N) * N;
+    for (int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x; e < g.B * plane;
+         e += int64_t(gridDim.x) * kBlock) {
+        const int64_t b = e / plane;
+        const int q = int(e - b * plane);
+        const int de = q / N, re = q - de * N;
+        const int dm = de == 0 ? 0 : N - de, rm = re == 0 ? 0 : N - re;
+        const int qm = dm * N + rm;
+        if (qm <= q) continue;  // self-partnered, or handled by the partner's lane
+        const int64_t i0 = b * g.vol + int64_t(q) * H, i1 = b * g.vol + int64_t(qm) * H;
+        const Cx<float> a = dst[i0], m = dst[i1];
+        dst[i0] = Cx<float>{a.re + m.re, a.im - m.im};
+        dst[i1] = Cx<float>{m.re + a.re, m.im - a.im};
+        if (WEIGHTS) {
+            const float wa = wdst[i0], wm = wdst[i1];
+            wdst[i0] = wa + wm;
+            wdst[i1] = wm + wa;
+        }
+    }
+}
+
+// Zero the stored cells of the scatter core tiles, which their pose-range
+// pieces then accumulate into with atomics.
+template <bool WEIGHTS>
+__global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<float>* __restrict__ dst,
+                                                      float* __restrict__ wdst) {
+    const int N = g.N, H = g.H, half = N / 2;
+    const int dd = (ts.sd1 - ts.sd0) * SD, rr = (ts.sr1 - ts.sr0) * SR, cc = ts.sc1 * SC;
+    const int64_t cells = int64_t(dd) * rr * cc;
+    for (int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x; e < g.B * cells; e += int64_t(gridDim.x) * kBlock) {
+        const int64_t b = e / cells;
+        const int64_t q = e - b * cells;
+        const int c = int(q % cc), r = -half + 1 + ts.sr0 * SR + int((q / cc) % rr),
+                  d = -half + 1 + ts.sd0 * SD + int(q / (int64_t(cc) * rr));
+        if (c >= H || r > half || d > half) continue;
+        const int re = r < 0 ? r + N : r, de = d < 0 ? d + N : d;
+        const int64_t idx = b * g.vol + (int64_t(de) * N + re) * H + c;
+        dst[idx] = Cx<float>{0.f, 0.f};
+        if (WEIGHTS) wdst[idx] = 0.f;
+    }
+}
+
+template <bool CUBIC, int KP>
+hipError_t forw_launch(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts,
+                       void* out, hipStream_t s) {
+    const int64_t fcore = int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * ts.ksplit;
+    const int64_t work = g.B * (fcore + int64_t(ts.nt) * ts.nt * ts.nt);
+    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP>), dim3(grid_for(work)), dim3(kBlock), 0, s, g, ts,
+                       (const Cx<float>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
+    return hipGetLastError();
+}
+
+template <bool CUBIC, int MODE, bool WEIGHTS, int KP>
+hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
+                          const void* shifts, void* dst, void* wdst, hipStream_t s) {
+    const int64_t score = int64_t(ts.sd1 - ts.sd0) * (ts.sr1 - ts.sr0) * ts.sc1 * ts.ksplit;
+    if (score > 0) {
+        const int64_t cells = g.B * int64_t((ts.sd1 - ts.sd0) * SD) * ((ts.sr1 - ts.sr0) * SR) * (ts.sc1 * SC);
+        int64_t blocks = (cells + kBlock - 1) / kBlock;
+        if (blocks > 65536) blocks = 65536;
+        hipLaunchKernelGGL(k_zero_core<WEIGHTS>, dim3(unsigned(blocks)), dim3(kBlock), 0, s, g, ts, (Cx<float>*)dst,
+                           (float*)wdst);
+        const hipError_t ez = hipGetLastError();
+        if (ez != hipSuccess) return ez;
+    }
+    const int64_t work = g.B * (score + int64_t(ts.ntd) * ts.ntr * ts.ntc);
+    hipLaunchKernelGGL((k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP>), dim3(grid_for(work)), dim3(kBlock), 0, s, g,
+                       ts, (const Cx<float>*)src, (const float*)weights, (const float*)rot, (const float*)shifts,
+                       (Cx<float>*)dst, (float*)wdst);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || MODE != 0) return e;
+    const int64_t pairs = g.B * int64_t(g.N) * g.N;
+    int64_t blocks = (pairs + kBlock - 1) / kBlock;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(k_mirror_x0<WEIGHTS>, dim3(unsigned(blocks)), dim3(kBlock), 0, s, g, (Cx<float>*)dst,
+                       (float*)wdst);
+    return hipGetLastError();
+}
+
+template <bool CUBIC, int MODE, bool WEIGHTS>
+hipError_t scatter_kp(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
+                      const void* shifts, void* dst, void* wdst, hipStream_t s) {
+    if (ts.kp_scatter >= 4)
+        return scatter_launch<CUBIC, MODE, WEIGHTS, 4>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    if (ts.kp_scatter == 2)
+        return scatter_launch<CUBIC, MODE, WEIGHTS, 2>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    return scatter_launch<CUBIC, MODE, WEIGHTS, 1>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+}
+
+}  // namespace
+
+hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* rec,
+                                      const void* rot, const void* shifts, void* out, hipStream_t s) {
+    if (cubic) {
+        if (ts.kp_forw >= 4) return forw_launch<true, 4>(g, ts, rec, rot, shifts, out, s);
+        if (ts.kp_forw == 2) return forw_launch<true, 2>(g, ts, rec, rot, shifts, out, s);
+        return forw_launch<true, 1>(g, ts, rec, rot, shifts, out, s);
+    }
+    if (ts.kp_forw >= 4) return forw_launch<false, 4>(g, ts, rec, rot, shifts, out, s);
+    if (ts.kp_forw == 2) return forw_launch<false, 2>(g, ts, rec, rot, shifts, out, s);
+    return forw_launch<false, 1>(g, ts, rec, rot, shifts, out, s);
+}
+
+hipError_t launch_scatter3_tiled(bool cubic, int mode, const Geom& g, const TileSpec& ts, const void* src,
+                                 const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
+                                 hipStream_t s) {
+    if (mode == 0) {
+        if (weights)
+            return cubic ? scatter_kp<true, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s)
+                         : scatter_kp<false, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+        return cubic ? scatter_kp<true, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
+                     : scatter_kp<false, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
+    }
+    return cubic ? scatter_kp<true, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
+                 : scatter_kp<false, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
+}
+
+}  // namespace tp
