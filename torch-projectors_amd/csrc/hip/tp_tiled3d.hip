@@ -119,27 +119,44 @@ __device__ __forceinline__ void row_span(const float* R, int r, const float* lo,
     else c1 = min(c1, int(sqrtf(rem)) + 1);
 }
 
-__device__ __forceinline__ int wave_incl_scan(int v) {
+// Wave-wide inclusive prefix sum / max with DPP row shifts and broadcasts
+// (register-to-register inside the SIMD, no LDS round trip).  Call with
+// every lane active.
+__device__ __forceinline__ int dpp_scan_add(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return v;
+}
+// Values must be >= 0 (0 is the identity).
+__device__ __forceinline__ int dpp_scan_max(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false));
+    return v;
+}
+__device__ __forceinline__ int wave_max(int v) { return __builtin_amdgcn_readlane(dpp_scan_max(max(v, 0)), 63); }
+
+// Row lanes hold `cnt` samples starting at flattened index `excl`.  For the
+// window [e0, e0 + 64) every lane gets the row lane owning index e0 + lane:
+// rows mark their first index in a per-wave LDS array, a prefix max carries
+// the marks forward, and `carry` brings the owner across windows.
+__device__ __forceinline__ int window_owner(int cnt, int excl, int e0, int& carry, int* marks) {
     const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int t = __shfl_up(v, off, 64);
-        if (lane >= off) v += t;
-    }
-    return v;
-}
-__device__ __forceinline__ int wave_max(int v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
-    return v;
-}
-// Lane owning flattened index e: the first lane whose inclusive count exceeds e.
-__device__ __forceinline__ int owner_lane(int incl, int e) {
-    int lw = 0;
-#pragma unroll
-    for (int step = 32; step >= 1; step >>= 1)
-        if (__shfl(incl, lw + step - 1, 64) <= e) lw += step;
-    return lw;
+    marks[lane] = 0;
+    __builtin_amdgcn_wave_barrier();
+    if (cnt > 0 && excl >= e0 && excl < e0 + 64) marks[excl - e0] = lane + 1;
+    __builtin_amdgcn_wave_barrier();
+    const int m = max(dpp_scan_max(marks[lane]), carry);
+    carry = __builtin_amdgcn_readlane(m, 63);
+    __builtin_amdgcn_wave_barrier();
+    return m - 1;
 }
 
 // Per-wave copy of the poses of one batch.
@@ -153,6 +170,13 @@ struct Slot {
 __device__ __forceinline__ void load_rot(const float* __restrict__ Rg, float* R) {
 #pragma unroll
     for (int e = 0; e < 9; ++e) R[e] = Rg[e];
+}
+// Rotation and shift of pose p (shifts may be absent: zeros).
+__device__ __forceinline__ void load_pose(const float* __restrict__ rotb, const float* __restrict__ shb, int p,
+                                          float* R, float* S) {
+    load_rot(rotb + int64_t(p) * 9, R);
+    S[0] = shb ? shb[2 * int64_t(p)] : 0.f;
+    S[1] = shb ? shb[2 * int64_t(p) + 1] : 0.f;
 }
 
 // Work items: first the core tiles, one item per (batch, tile, pose range),
@@ -202,7 +226,11 @@ constexpr int kCullPerLane = 4;
 constexpr int kCullInFlight = 2;  // rotations loaded together per lane
 constexpr int kChunk = kBlock * kCullPerLane;
 
-// Cull poses [pbase, pbase + kChunk) against up to two boxes; returns the count.
+// List entries: pose index relative to the phase, plus which boxes it crosses.
+constexpr unsigned kHit1 = 1u << 14, kHit2 = 1u << 15, kPoseMask = kHit1 - 1;
+static_assert(kChunk <= int(kPoseMask) + 1, "pose index must fit below the flag bits");
+
+// Cull poses [pbase, pend) (at most kChunk) against up to two boxes; returns the count.
 template <bool TWO>
 __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pend, int pbase, const float* lo1,
                                           const float* hi1, const float* lo2, const float* hi2,
@@ -222,8 +250,8 @@ __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pe
         for (int q = 0; q < kCullInFlight; ++q) {
             const int p = pbase + int(threadIdx.x) + (q0 + q) * kBlock;
             if (p >= pend) continue;
-            const bool hit = pose_hits(R[q], lo1, hi1) || (TWO && pose_hits(R[q], lo2, hi2));
-            if (hit) plist[atomicAdd(pcount, 1)] = (unsigned short)(p - pbase);
+                const bool h1 = pose_hits(R[q], lo1, hi1), h2 = TWO && pose_hits(R[q], lo2, hi2);
+            if (h1 || h2) plist[atomicAdd(pcount, 1)] = (unsigned short)((p - pbase) | (h1 ? kHit1 : 0) | (h2 ? kHit2 : 0));
         }
     }
     __syncthreads();
@@ -244,6 +272,7 @@ __global__ __launch_bounds__(kBlock) void k_forw3_tiled(Geom g, TileSpec ts, con
     __shared__ unsigned short plist[kChunk];
     __shared__ int pcount;
     __shared__ Slot slots[NW][KP];
+    __shared__ int marks[NW][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slot = lane / RPS, jrow = lane % RPS;
     const int nt = ts.nt;
@@ -298,25 +327,28 @@ __global__ __launch_bounds__(kBlock) void k_forw3_tiled(Geom g, TileSpec ts, con
                 __syncthreads();
                 loaded = true;
             }
-            // wave batches of KP poses; the next batch's rotations load during this one
+            // wave batches of KP poses; the next batch's rotation and shift load during this one
             int base = wave * KP;
-            float Rn[9];
-            load_rot(rotb + int64_t(pbase + plist[min(base + slot, np - 1)]) * 9, Rn);
+            float Rn[9], Sn[2];
+            load_pose(rotb, shifts ? shifts + sb * g.P * 2 : nullptr, pbase + (plist[min(base + slot, np - 1)] & kPoseMask),
+                      Rn, Sn);
             for (; base < np; base += NW * KP) {
                 const bool sv = base + slot < np;
-                const int pp = pbase + plist[min(base + slot, np - 1)];
-                float R[9];
+                const int pp = pbase + (plist[min(base + slot, np - 1)] & kPoseMask);
+                float R[9], Sh[2];
 #pragma unroll
                 for (int e = 0; e < 9; ++e) R[e] = Rn[e];
+                Sh[0] = Sn[0];
+                Sh[1] = Sn[1];
                 if (base + NW * KP < np)
-                    load_rot(rotb + int64_t(pbase + plist[min(base + NW * KP + slot, np - 1)]) * 9, Rn);
+                    load_pose(rotb, shifts ? shifts + sb * g.P * 2 : nullptr,
+                              pbase + (plist[min(base + NW * KP + slot, np - 1)] & kPoseMask), Rn, Sn);
                 if (jrow == 0 && sv) {
                     Slot& sd = slots[wave][slot];
 #pragma unroll
                     for (int e = 0; e < 9; ++e) sd.R[e] = R[e];
-                    const float* S = shifts ? shifts + (sb * g.P + pp) * 2 : nullptr;
-                    sd.s0 = S ? S[0] : 0.f;
-                    sd.s1 = S ? S[1] : 0.f;
+                    sd.s0 = Sh[0];
+                    sd.s1 = Sh[1];
                     sd.p = pp;
                 }
                 __builtin_amdgcn_wave_barrier();
@@ -333,15 +365,15 @@ __global__ __launch_bounds__(kBlock) void k_forw3_tiled(Geom g, TileSpec ts, con
                         row_span(R, r, lo, hi, ts, cut2, c0, c1);
                         cnt = max(0, c1 - c0 + 1);
                     }
-                    const int incl = wave_incl_scan(cnt);
+                    const int incl = dpp_scan_add(cnt);
                     const int excl = incl - cnt;
-                    const int total = __shfl(incl, 63, 64);
+                    const int total = __builtin_amdgcn_readlane(incl, 63);
+                    int carry = 0;
                     for (int e0 = 0; e0 < total; e0 += 64) {
                         const int e = e0 + lane;
-                        const int es = min(e, total - 1);
-                        const int lw = owner_lane(incl, es);
+                        const int lw = window_owner(cnt, excl, e0, carry, marks[wave]);
                         const int rr = __shfl(r, lw, 64);
-                        const int cc = __shfl(c0, lw, 64) + (es - __shfl(excl, lw, 64));
+                        const int cc = __shfl(c0, lw, 64) + (e - __shfl(excl, lw, 64));
                         if (e >= total) continue;
                         const Slot& sd = slots[wave][lw / RPS];
                         const float fr = float(rr), fc = float(cc);
@@ -404,7 +436,7 @@ __device__ __forceinline__ void scatter_sample(const Geom& g, const Slot& sd, in
 // MODE 0: backprojection, v = proj * conj(phase(r, c)), optional weights.
 // MODE 1: reconstruction gradient of the projection, v = g * phase(-r, -c).
 template <bool CUBIC, int MODE, bool WEIGHTS, int KP>
-__global__ __launch_bounds__(kBlock) void k_scatter3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ src,
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) void k_scatter3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ src,
                                                            const float* __restrict__ weights,
                                                            const float* __restrict__ rot,
                                                            const float* __restrict__ shifts,
@@ -416,6 +448,7 @@ __global__ __launch_bounds__(kBlock) void k_scatter3_tiled(Geom g, TileSpec ts, 
     __shared__ unsigned short plist[kChunk];
     __shared__ int pcount;
     __shared__ Slot slots[NW][KP];
+    __shared__ int marks[NW][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slot = lane / RPS, jrow = lane % RPS;
     const int N = g.N, H = g.H, half = N / 2;
@@ -446,32 +479,43 @@ __global__ __launch_bounds__(kBlock) void k_scatter3_tiled(Geom g, TileSpec ts, 
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
         const float* rotb = rot + rb * g.P * 9;
         const int64_t pose0 = b * g.P;
+        // samples lie within |x| <= rho; box 2 is box 1 mirrored, so one test serves both
+        float dist2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const float q = lo1[k] > 0.f ? lo1[k] : (hi1[k] < 0.f ? -hi1[k] : 0.f);
+            dist2 += q * q;
+        }
+        const int pend = dist2 > ts.rho * ts.rho ? it.p0 : it.p1;
 
-        for (int pbase = it.p0; pbase < it.p1; pbase += kChunk) {
-            const int np = cull_chunk<true>(rotb, it.p1, pbase, lo1, hi1, lo2, hi2, plist, &pcount);
+        for (int pbase = it.p0; pbase < pend; pbase += kChunk) {
+            const int np = cull_chunk<true>(rotb, pend, pbase, lo1, hi1, lo2, hi2, plist, &pcount);
             int base = wave * KP;
-            float Rn[9];
-            if (base < np) load_rot(rotb + int64_t(pbase + plist[min(base + slot, np - 1)]) * 9, Rn);
+            float Rn[9], Sn[2];
+            const float* shb = shifts ? shifts + sb * g.P * 2 : nullptr;
+            if (base < np) load_pose(rotb, shb, pbase + (plist[min(base + slot, np - 1)] & kPoseMask), Rn, Sn);
             for (; base < np; base += NW * KP) {
                 const bool sv = base + slot < np;
-                const int pp = pbase + plist[min(base + slot, np - 1)];
-                float R[9];
+                const unsigned entry = plist[min(base + slot, np - 1)];
+                const int pp = pbase + int(entry & kPoseMask);
+                float R[9], Sh[2];
 #pragma unroll
                 for (int e = 0; e < 9; ++e) R[e] = Rn[e];
+                Sh[0] = Sn[0];
+                Sh[1] = Sn[1];
                 if (base + NW * KP < np)
-                    load_rot(rotb + int64_t(pbase + plist[min(base + NW * KP + slot, np - 1)]) * 9, Rn);
+                    load_pose(rotb, shb, pbase + (plist[min(base + NW * KP + slot, np - 1)] & kPoseMask), Rn, Sn);
                 int ra0, ra1;
                 box_rows(R, lo1, hi1, ts, ra0, ra1);
                 if (jrow == 0 && sv) {
                     Slot& sd = slots[wave][slot];
 #pragma unroll
                     for (int e = 0; e < 9; ++e) sd.R[e] = R[e];
-                    const float* S = shifts ? shifts + (sb * g.P + pp) * 2 : nullptr;
-                    sd.s0 = S ? S[0] : 0.f;
-                    sd.s1 = S ? S[1] : 0.f;
+                    sd.s0 = Sh[0];
+                    sd.s1 = Sh[1];
                     sd.p = pp;
-                    sd.r0a = ra0;
-                    sd.r1a = ra1;
+                    sd.r0a = (entry & kHit1) ? ra0 : 1;
+                    sd.r1a = (entry & kHit1) ? ra1 : 0;
                 }
                 __builtin_amdgcn_wave_barrier();
 #pragma unroll 1
@@ -482,6 +526,8 @@ __global__ __launch_bounds__(kBlock) void k_scatter3_tiled(Geom g, TileSpec ts, 
                         lo[k] = pass == 0 ? lo1[k] : lo2[k];
                         hi[k] = pass == 0 ? hi1[k] : hi2[k];
                     }
+                    const bool crosses = sv && (entry & (pass == 0 ? kHit1 : kHit2));
+                    if (!__any(crosses)) continue;
                     int r0, r1;
                     if (pass == 0) {
                         r0 = ra0;
@@ -489,7 +535,7 @@ __global__ __launch_bounds__(kBlock) void k_scatter3_tiled(Geom g, TileSpec ts, 
                     } else {
                         box_rows(R, lo, hi, ts, r0, r1);
                     }
-                    const int nr = sv ? max(0, r1 - r0 + 1) : 0;
+                    const int nr = crosses ? max(0, r1 - r0 + 1) : 0;
                     const int maxnr = wave_max(nr);
                     for (int rbase = 0; rbase < maxnr; rbase += RPS) {
                         const int jr = rbase + jrow;
@@ -500,16 +546,17 @@ __global__ __launch_bounds__(kBlock) void k_scatter3_tiled(Geom g, TileSpec ts, 
                             row_span(R, r, lo, hi, ts, cut2, c0, c1);
                             cnt = max(0, c1 - c0 + 1);
                         }
-                        const int incl = wave_incl_scan(cnt);
+                        const int incl = dpp_scan_add(cnt);
                         const int excl = incl - cnt;
-                        const int total = __shfl(incl, 63, 64);
-                        // sample e of this row block: owner lane, pixel, validity, and its loads
-                        auto fetch_sample = [&](int e, int& rr, int& cc, int& sl, bool& ok, Cx<float>& v,
+                        const int total = __builtin_amdgcn_readlane(incl, 63);
+                        int carry = 0;
+                        // sample e0 + lane of this row block: owner lane, pixel, validity, and its loads
+                        auto fetch_sample = [&](int e0, int& rr, int& cc, int& sl, bool& ok, Cx<float>& v,
                                                 float& wv) {
-                            const int es = min(e, total - 1);
-                            const int lw = owner_lane(incl, es);
+                            const int e = e0 + lane;
+                            const int lw = window_owner(cnt, excl, e0, carry, marks[wave]);
                             rr = __shfl(r, lw, 64);
-                            cc = __shfl(c0, lw, 64) + (es - __shfl(excl, lw, 64));
+                            cc = __shfl(c0, lw, 64) + (e - __shfl(excl, lw, 64));
                             sl = lw / RPS;
                             ok = e < total;
                             const Slot& sd = slots[wave][sl];
@@ -529,14 +576,14 @@ __global__ __launch_bounds__(kBlock) void k_scatter3_tiled(Geom g, TileSpec ts, 
                         bool ok;
                         Cx<float> v;
                         float wv;
-                        fetch_sample(lane, rr, cc, sl, ok, v, wv);
+                        fetch_sample(0, rr, cc, sl, ok, v, wv);
                         for (int e0 = 0; e0 < total; e0 += 64) {
                             // the next sample's loads are in flight while this one is spread
                             int rr2 = 0, cc2 = 0, sl2 = 0;
                             bool ok2 = false;
                             Cx<float> v2 = {0.f, 0.f};
                             float wv2 = 0.f;
-                            if (e0 + 64 < total) fetch_sample(e0 + 64 + lane, rr2, cc2, sl2, ok2, v2, wv2);
+                            if (e0 + 64 < total) fetch_sample(e0 + 64, rr2, cc2, sl2, ok2, v2, wv2);
                             if (ok)
                                 scatter_sample<CUBIC, MODE, WEIGHTS>(g, slots[wave][sl], rr, cc, v, wv,
                                                                      shifts != nullptr, tc, tr, td, acc_re, acc_im,
