@@ -43,7 +43,8 @@ namespace {
 
 constexpr int L = kTileEdge;  // forward tile edge (voxels)
 constexpr int SC = kScTC, SR = kScTR, SD = kScTD, S3 = SC * SR * SD;  // scatter tile
-constexpr int NW = kBlock / 64;
+constexpr int kForwThreads = 256;     // forward workgroup
+constexpr int kScatterThreads = 256;  // scatter workgroup
 
 __device__ __forceinline__ int to_int_clamped(float v) {
     v = fminf(fmaxf(v, -1.0e8f), 1.0e8f);
@@ -220,18 +221,18 @@ __device__ __forceinline__ Item item_of(int64_t w, int64_t B, int P, int nd, int
     return it;
 }
 
-// Poses culled per phase: each lane tests 4, the survivors' indices (relative
-// to the phase) go to an LDS list.
-constexpr int kCullPerLane = 4;
+// Poses culled per phase: each lane tests kChunk / NT of them, the survivors'
+// indices (relative to the phase) go to an LDS list.
 constexpr int kCullInFlight = 2;  // rotations loaded together per lane
-constexpr int kChunk = kBlock * kCullPerLane;
+constexpr int kChunk = 1024;      // poses culled per phase
 
 // List entries: pose index relative to the phase, plus which boxes it crosses.
 constexpr unsigned kHit1 = 1u << 14, kHit2 = 1u << 15, kPoseMask = kHit1 - 1;
 static_assert(kChunk <= int(kPoseMask) + 1, "pose index must fit below the flag bits");
 
-// Cull poses [pbase, pend) (at most kChunk) against up to two boxes; returns the count.
-template <bool TWO>
+// Cull poses [pbase, pend) (at most kChunk) against up to two boxes with a
+// workgroup of NT lanes; returns the count.
+template <int NT, bool TWO>
 __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pend, int pbase, const float* lo1,
                                           const float* hi1, const float* lo2, const float* hi2,
                                           unsigned short* plist, int* pcount) {
@@ -239,16 +240,16 @@ __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pe
     if (threadIdx.x == 0) *pcount = 0;
     __syncthreads();
 #pragma unroll 1
-    for (int q0 = 0; q0 < kCullPerLane; q0 += kCullInFlight) {
+    for (int q0 = 0; q0 < kChunk / NT; q0 += kCullInFlight) {
         float R[kCullInFlight][9];
 #pragma unroll
         for (int q = 0; q < kCullInFlight; ++q) {
-            const int p = min(pbase + int(threadIdx.x) + (q0 + q) * kBlock, pend - 1);
+            const int p = min(pbase + int(threadIdx.x) + (q0 + q) * NT, pend - 1);
             load_rot(rotb + int64_t(p) * 9, R[q]);
         }
 #pragma unroll
         for (int q = 0; q < kCullInFlight; ++q) {
-            const int p = pbase + int(threadIdx.x) + (q0 + q) * kBlock;
+            const int p = pbase + int(threadIdx.x) + (q0 + q) * NT;
             if (p >= pend) continue;
                 const bool h1 = pose_hits(R[q], lo1, hi1), h2 = TWO && pose_hits(R[q], lo2, hi2);
             if (h1 || h2) plist[atomicAdd(pcount, 1)] = (unsigned short)((p - pbase) | (h1 ? kHit1 : 0) | (h2 ? kHit2 : 0));
@@ -261,13 +262,14 @@ __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pe
 
 // ----------------------------------------------------------------------------- forward
 template <bool CUBIC, int KP>
-__global__ __launch_bounds__(kBlock) void k_forw3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ rec,
+__global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ rec,
                                                         const float* __restrict__ rot,
                                                         const float* __restrict__ shifts,
                                                         Cx<float>* __restrict__ out) {
     constexpr int LO = CUBIC ? 1 : 0, HI = CUBIC ? 2 : 1, W = L + LO + HI, W3 = W * W * W;
     constexpr int RPS = 64 / KP;
-    constexpr int LOADS = (W3 + kBlock - 1) / kBlock;
+    constexpr int NT = kForwThreads, NW = NT / 64;
+    constexpr int LOADS = (W3 + NT - 1) / NT;
     __shared__ Cx<float> vt[W3];
     __shared__ unsigned short plist[kChunk];
     __shared__ int pcount;
@@ -305,7 +307,7 @@ __global__ __launch_bounds__(kBlock) void k_forw3_tiled(Geom g, TileSpec ts, con
         };
         bool loaded = false;
         for (int pbase = it.p0; pbase < it.p1; pbase += kChunk) {
-            const int np = cull_chunk<false>(rotb, it.p1, pbase, lo, hi, lo, hi, plist, &pcount);
+            const int np = cull_chunk<NT, false>(rotb, it.p1, pbase, lo, hi, lo, hi, plist, &pcount);
             if (np == 0) continue;
             if (!loaded) {
                 // stage the tile and its halo, STAGE loads in flight per lane
@@ -315,14 +317,14 @@ __global__ __launch_bounds__(kBlock) void k_forw3_tiled(Geom g, TileSpec ts, con
                     Cx<float> v[STAGE];
 #pragma unroll
                     for (int q = 0; q < STAGE; ++q) {
-                        const int cell = min(tid + (q0 + q) * kBlock, W3 - 1);
+                        const int cell = min(tid + (q0 + q) * NT, W3 - 1);
                         const int lc = cell % W, lr = (cell / W) % W, ld = cell / (W * W);
                         const int d = td - LO + ld, r = tr - LO + lr, c = tc - LO + lc;
                         v[q] = CUBIC ? fetch3_cubic(recb, N, H, d, r, c) : fetch3(recb, N, H, d, r, c);
                     }
 #pragma unroll
                     for (int q = 0; q < STAGE; ++q)
-                        if (tid + (q0 + q) * kBlock < W3) vt[tid + (q0 + q) * kBlock] = v[q];
+                        if (tid + (q0 + q) * NT < W3) vt[tid + (q0 + q) * NT] = v[q];
                 }
                 __syncthreads();
                 loaded = true;
@@ -436,13 +438,14 @@ __device__ __forceinline__ void scatter_sample(const Geom& g, const Slot& sd, in
 // MODE 0: backprojection, v = proj * conj(phase(r, c)), optional weights.
 // MODE 1: reconstruction gradient of the projection, v = g * phase(-r, -c).
 template <bool CUBIC, int MODE, bool WEIGHTS, int KP>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) void k_scatter3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ src,
+__global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu(3))) void k_scatter3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ src,
                                                            const float* __restrict__ weights,
                                                            const float* __restrict__ rot,
                                                            const float* __restrict__ shifts,
                                                            Cx<float>* __restrict__ dst, float* __restrict__ wdst) {
     constexpr int SL = CUBIC ? 2 : 1, SH = CUBIC ? 1 : 0;  // stencil reach below / above floor(x)
     constexpr int RPS = 64 / KP;
+    constexpr int NT = kScatterThreads, NW = NT / 64;
     __shared__ double acc_re[S3], acc_im[S3];
     __shared__ double acc_w[WEIGHTS ? S3 : 1];
     __shared__ unsigned short plist[kChunk];
@@ -471,7 +474,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
         const float lo2[3] = {float(fc0 - SL) - ts.eps, float(fr0 - SL) - ts.eps, float(fd0 - SL) - ts.eps};
         const float hi2[3] = {float(fc0 + SC + SH) + ts.eps, float(fr0 + SR + SH) + ts.eps,
                               float(fd0 + SD + SH) + ts.eps};
-        for (int e = tid; e < S3; e += kBlock) {
+        for (int e = tid; e < S3; e += NT) {
             acc_re[e] = 0.0;
             acc_im[e] = 0.0;
             if (WEIGHTS) acc_w[e] = 0.0;
@@ -489,7 +492,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
         const int pend = dist2 > ts.rho * ts.rho ? it.p0 : it.p1;
 
         for (int pbase = it.p0; pbase < pend; pbase += kChunk) {
-            const int np = cull_chunk<true>(rotb, pend, pbase, lo1, hi1, lo2, hi2, plist, &pcount);
+            const int np = cull_chunk<NT, true>(rotb, pend, pbase, lo1, hi1, lo2, hi2, plist, &pcount);
             int base = wave * KP;
             float Rn[9], Sn[2];
             const float* shb = shifts ? shifts + sb * g.P * 2 : nullptr;
@@ -604,7 +607,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
 
         // write every stored cell of the tile once (core pieces add into a zeroed region)
         __syncthreads();
-        for (int e = tid; e < S3; e += kBlock) {
+        for (int e = tid; e < S3; e += NT) {
             const int lc = e % SC, lr = (e / SC) % SR, ld = e / (SC * SR);
             const int c = tc + lc, r = tr + lr, d = td + ld;
             if (c >= H || r > half || d > half) continue;
@@ -679,7 +682,7 @@ hipError_t forw_launch(const Geom& g, const TileSpec& ts, const void* rec, const
                        void* out, hipStream_t s) {
     const int64_t fcore = int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * ts.ksplit;
     const int64_t work = g.B * (fcore + int64_t(ts.nt) * ts.nt * ts.nt);
-    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP>), dim3(grid_for(work)), dim3(kBlock), 0, s, g, ts,
+    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP>), dim3(grid_for(work)), dim3(kForwThreads), 0, s, g, ts,
                        (const Cx<float>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
     return hipGetLastError();
 }
@@ -698,7 +701,7 @@ hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, co
         if (ez != hipSuccess) return ez;
     }
     const int64_t work = g.B * (score + int64_t(ts.ntd) * ts.ntr * ts.ntc);
-    hipLaunchKernelGGL((k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP>), dim3(grid_for(work)), dim3(kBlock), 0, s, g,
+    hipLaunchKernelGGL((k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP>), dim3(grid_for(work)), dim3(kScatterThreads), 0, s, g,
                        ts, (const Cx<float>*)src, (const float*)weights, (const float*)rot, (const float*)shifts,
                        (Cx<float>*)dst, (float*)wdst);
     hipError_t e = hipGetLastError();
