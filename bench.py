@@ -215,6 +215,25 @@ def run_cpu_baseline(wl, target_s=12.0):
                       f"fwd {parts['fwd_s']:.2f} s, bp {parts['bp_s']:.2f} s), {threads} threads"}
 
 
+# ----------------------------------------------------------------------------- HBM traffic
+def measured_traffic(workload, op):
+    """HBM bytes per call of `op`, from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary.
+
+    The counters cannot be read from inside a run, so the figure comes from the
+    summary profiles/hbm_traffic_<workload>.md (copy-kernel-scaled, read + write,
+    summed over the op's kernels); None when there is none for this workload.
+    """
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"hbm_traffic_{workload}.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_call:"):
+                    return json.loads(line.split(":", 1)[1]).get(op)
+    except OSError:
+        pass
+    return None
+
+
 # ----------------------------------------------------------------------------- main
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -227,6 +246,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="headline", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 1 GiB copy kernel 5 times (calibrates HBM byte counters)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {a.gpus} requested); the multi-GPU "
@@ -235,6 +256,15 @@ def main():
 
     import torch
     dev = torch.device("cuda:0")
+    if a.copy_probe:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):  # an elementwise kernel (not a runtime blit) so counters see it
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_read": src.numel() * 4, "copy_probe_bytes_written": dst.numel() * 4,
+                          "calls": 5}))
+        return
     wl = WORKLOADS[a.config](dev)
     torch.cuda.synchronize()
     log(f"inputs ready: {a.config}")
@@ -292,7 +322,7 @@ def main():
         "wall_s": round(wall, 3),
         "ops": per_op,
         "roofline": {"bound": "hbm", "kernel": dname, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic(a.config, dname)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
