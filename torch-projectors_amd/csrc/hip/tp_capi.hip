@@ -129,10 +129,13 @@ tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
     ts.prange = int((g.P + ts.ksplit - 1) / ts.ksplit);
     if (ts.ksplit == 1) ts.fc1 = ts.fc0 = ts.sd1 = ts.sd0 = ts.sr1 = ts.sr0 = ts.sc1 = 0;  // nothing to split
     ts.rho = float(rho);
-    ts.eps = 0.5f;
     ts.os = float(g.os);
     ts.inv_os = float(1.0 / g.os);
     ts.smax = float(g.os * (g.n + 2));
+    // Slack of the sample boxes: the row and half-plane bounds use the
+    // rotation's orthonormality (off by at most kRotationTol * |sc, sr| each),
+    // plus fp32 rounding of the bounds themselves.
+    ts.eps = 0.01f + 2.0f * tp::kRotationTol * ts.smax;
     ts.kp_forw = poses_per_batch(L, ts.eps, g.os);
     ts.kp_scatter = poses_per_batch(tp::kScTC + (cubic ? 3 : 1), ts.eps, g.os);
     const int cl = int(std::floor(cutr)) + 1;

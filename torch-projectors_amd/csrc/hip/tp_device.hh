@@ -13,6 +13,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "tp_launch.hh"
+
 namespace tp {
 
 template <typename T>
@@ -38,6 +40,13 @@ template <typename T> __device__ __forceinline__ int split(T x, T& frac) {
     frac = x - f;
     const T lim = T(16777216.0);
     return (int)(f < -lim ? -lim : (f > lim ? lim : f));
+}
+// The same without the clamp, for callers whose |x| is bounded by the box.
+template <bool CLAMP, typename T> __device__ __forceinline__ int split_as(T x, T& frac) {
+    if (CLAMP) return split(x, frac);
+    const T f = floor(x);
+    frac = x - f;
+    return (int)f;
 }
 
 // ---------------------------------------------------------------- cubic weights
@@ -163,10 +172,10 @@ __device__ __forceinline__ Interp<T> interp2_cubic(const Cx<T>* __restrict__ rec
 // Trilinear (interpolation_kernels.h:140-228): lerp along c, then r, then d.
 // `fetch(d, r, c)` returns the tap value the reference's sampler would return
 // for integer coordinates (global fetch3, or a staged copy of it in LDS).
-template <typename T, bool GRADS, typename F>
+template <typename T, bool GRADS, bool CLAMP = true, typename F>
 __device__ __forceinline__ Interp<T> lerp3(F&& fetch, T d, T r, T c) {
     T dx, rx, cx;
-    const int df = split(d, dx), rf = split(r, rx), cf = split(c, cx);
+    const int df = split_as<CLAMP>(d, dx), rf = split_as<CLAMP>(r, rx), cf = split_as<CLAMP>(c, cx);
     const Cx<T> p000 = fetch(df, rf, cf), p001 = fetch(df, rf, cf + 1);
     const Cx<T> p010 = fetch(df, rf + 1, cf), p011 = fetch(df, rf + 1, cf + 1);
     const Cx<T> p100 = fetch(df + 1, rf, cf), p101 = fetch(df + 1, rf, cf + 1);
@@ -196,10 +205,10 @@ __device__ __forceinline__ Interp<T> interp3_linear(const Cx<T>* __restrict__ re
 
 // Tricubic (interpolation_kernels.h:345-425): sum over d, r, c of ((s*wd)*wr)*wc.
 // `fetch` returns the pre-clamped tap of fetch3_cubic.
-template <typename T, bool GRADS, typename F>
+template <typename T, bool GRADS, bool CLAMP = true, typename F>
 __device__ __forceinline__ Interp<T> cubic3(F&& fetch, T d, T r, T c) {
     T dx, rx, cx;
-    const int df = split(d, dx), rf = split(r, rx), cf = split(c, cx);
+    const int df = split_as<CLAMP>(d, dx), rf = split_as<CLAMP>(r, rx), cf = split_as<CLAMP>(c, cx);
     T wc[4], dwc[4], wr[4], dwr[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -442,16 +451,35 @@ template <typename T> __device__ __forceinline__ Cx<T> phase(T r, T c, T s0, T s
     return f;
 }
 
+// The same phase angle, evaluated with the hardware sine/cosine: the angle is
+// turned into revolutions with an error-free product split (1/2pi = C1 + C2),
+// reduced to [-1/2, 1/2] exactly, and fed to v_sin/v_cos.  Differs from the
+// library sincosf by the hardware units' few-ulp error only.
+__device__ __forceinline__ Cx<float> phase_hw(float r, float c, float s0, float s1, double k) {
+    float ph = 0.0f;
+    ph += r * s0;
+    ph += c * s1;
+    ph = float(double(ph) * k);
+    constexpr float C1 = 0.15915493667125702f;       // fl(1 / 2pi)
+    constexpr float C2 = 6.4206382433e-09f;          // 1 / 2pi - C1
+    const float h = ph * C1;
+    const float e = fmaf(ph, C1, -h) + ph * C2;      // low part of ph / 2pi
+    const float t = (h - rintf(h)) + e;
+    return {__builtin_amdgcn_cosf(t), __builtin_amdgcn_sinf(t)};
+}
+
 // ---------------------------------------------------------------- pose classes
 // The tiled 3D kernels enumerate the samples of a pose through its slice
 // plane, which needs the first two rotation columns orthonormal (every
 // rotation matrix).  Other matrices (scaled, sheared, degenerate) take the
-// per-pixel kernels.  Both sides evaluate this same predicate.
+// per-pixel kernels.  Both sides evaluate this same predicate.  Rotations
+// stored in fp32 are orthonormal to a few 1e-7; the tiled kernels' sample
+// bounds allow for kRotationTol (tp_launch.hh).
 __device__ __forceinline__ bool pose_is_rotation(const float* __restrict__ R) {
     const float aa = R[0] * R[0] + R[3] * R[3] + R[6] * R[6];
     const float bb = R[1] * R[1] + R[4] * R[4] + R[7] * R[7];
     const float ab = R[0] * R[1] + R[3] * R[4] + R[6] * R[7];
-    return fabsf(aa - 1.0f) <= 1e-4f && fabsf(bb - 1.0f) <= 1e-4f && fabsf(ab) <= 1e-4f;
+    return fabsf(aa - 1.0f) <= kRotationTol && fabsf(bb - 1.0f) <= kRotationTol && fabsf(ab) <= kRotationTol;
 }
 
 // ---------------------------------------------------------------- atomics

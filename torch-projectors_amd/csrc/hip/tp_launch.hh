@@ -22,6 +22,10 @@ struct Geom {
     int64_t work;                  // B*P*chunks
 };
 
+// A pose matrix counts as a rotation (and takes the tiled kernels) when its
+// first two columns are orthonormal to this tolerance.
+constexpr float kRotationTol = 1e-5f;
+
 // Tile-owner enumeration parameters of the fp32 3D kernels (tp_tiled3d.hip).
 constexpr int kTileEdge = 16;                          // forward tiles: 16^3 voxels
 constexpr int kScTC = 16, kScTR = 16, kScTD = 8;        // scatter tiles (c, r, d): fp64 accumulators

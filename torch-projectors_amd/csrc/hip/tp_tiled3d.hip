@@ -165,7 +165,6 @@ struct Slot {
     float R[9];
     float s0, s1;
     int p;
-    int r0a, r1a;  // scatter: rows of box 1 (pass-2 de-duplication)
 };
 
 __device__ __forceinline__ void load_rot(const float* __restrict__ Rg, float* R) {
@@ -385,9 +384,9 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                         const int fxc = int(floorf(x[0])), fxr = int(floorf(x[1])), fxd = int(floorf(x[2]));
                         if (fxc < tc || fxc >= tc + L || fxr < tr || fxr >= tr + L || fxd < td || fxd >= td + L)
                             continue;
-                        Cx<float> v = CUBIC ? cubic3<float, false>(lds, x[2], x[1], x[0]).v
-                                            : lerp3<float, false>(lds, x[2], x[1], x[0]).v;
-                        if (shifts) v = cmul(v, phase<float>(fr, fc, sd.s0, sd.s1, g.phase_k));
+                        Cx<float> v = CUBIC ? cubic3<float, false, false>(lds, x[2], x[1], x[0]).v
+                                            : lerp3<float, false, false>(lds, x[2], x[1], x[0]).v;
+                        if (shifts) v = cmul(v, phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k));
                         const int i = rr >= 0 ? rr : rr + g.n;
                         out[(b * g.P + sd.p) * int64_t(g.npix) + i * g.hp + cc] = v;
                     }
@@ -401,38 +400,73 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
 }
 
 // ----------------------------------------------------------------------------- scatter
-// Per-sample work of the scatter: value and weight of a projection pixel,
-// spread over the stencil taps that land in the tile (LDS float atomics).
+// Per-sample work of the scatter: one class of the sample's stencil taps,
+// spread over the tile's fp64 LDS accumulators.  flip = false takes the direct
+// taps (c >= 0), flip = true the taps with c < 0, which the reference moves to
+// (-c, -r, -d) and conjugates (projection_utils.h:414-443, 451-493); every
+// (sample, tap) pair is thus deposited by exactly one pass.  Taps outside the
+// reference's range [-N/2+1, N/2] are dropped there; here they fall outside
+// the tile or on cells past the volume edge, which are never written out.
+// Per-pass constants: local cell of tap j on axis a is sgn * floor(x_a) + off[a] + sgn * j
+// (sgn = -1 for the flipped taps), valid in [lmin[a], S_a).
+struct TapMap {
+    int sgn;
+    int off[3];
+    int lmin[3];
+};
+
 template <bool CUBIC, int MODE, bool WEIGHTS>
 __device__ __forceinline__ void scatter_sample(const Geom& g, const Slot& sd, int rr, int cc, Cx<float> v, float wpix,
-                                               bool shifted, int tc, int tr, int td, double* acc_re, double* acc_im,
-                                               double* acc_w) {
-    const int H = g.H, half = g.N / 2;
+                                               bool shifted, bool flip, const TapMap& tm, double* acc_re,
+                                               double* acc_im, double* acc_w) {
+    constexpr int K = CUBIC ? 4 : 2, LOW = CUBIC ? 1 : 0;  // taps at floor(x) - LOW + j, j < K
     const float fr = float(rr), fc = float(cc);
     float x[3], sc, sr;
     rotate<3>(sd.R, fr, fc, g.os, x, sc, sr);
     if (shifted) {
-        if (MODE == 0) v = cmul(v, cconj(phase<float>(fr, fc, sd.s0, sd.s1, g.phase_k)));
-        else v = cmul(v, phase<float>(-fr, -fc, sd.s0, sd.s1, g.phase_k));
+        if (MODE == 0) v = cmul(v, cconj(phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k)));
+        else v = cmul(v, phase_hw(-fr, -fc, sd.s0, sd.s1, g.phase_k));
     }
-    distribute<3, float, CUBIC>(x, [&](int d, int tr2, int tc2, float wd, float wr, float wc) {
-        const bool cj = tc2 < 0;
-        if (cj) {
-            tc2 = -tc2;
-            tr2 = -tr2;
-            d = -d;
+    // per axis: local cell of each tap position (or -1 outside the tile) and its weight
+    constexpr int S[3] = {SC, SR, SD};
+    int loc[3][K];
+    double wt[3][K];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        float f;
+        const int fl = split_as<false>(x[a], f);
+        const int l0 = (flip ? -fl : fl) + tm.off[a];
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            const int l = l0 + tm.sgn * j;
+            loc[a][j] = (unsigned)(l - tm.lmin[a]) < (unsigned)(S[a] - tm.lmin[a]) ? l : -1;
+            if (CUBIC) wt[a][j] = double(cubic_w<float>(f - float(j - LOW)));
         }
-        // dropped taps (projection_utils.h:431-438) never fall in a stored tile
-        const int lc = tc2 - tc, lr = tr2 - tr, ld = d - td;
-        if ((unsigned)lc >= (unsigned)SC || (unsigned)lr >= (unsigned)SR || (unsigned)ld >= (unsigned)SD) return;
-        if (tc2 >= H || tr2 > half || d > half) return;
-        Cx<float> tv = tap_value<3, float>(v, wd, wr, wc);
-        if (cj) tv.im = -tv.im;
-        const int li = (ld * SR + lr) * SC + lc;
-        atomicAdd(&acc_re[li], double(tv.re));
-        atomicAdd(&acc_im[li], double(tv.im));
-        if (WEIGHTS) atomicAdd(&acc_w[li], double(wpix * tap_weight<3, float>(wd, wr, wc)));
-    });
+        if (!CUBIC) {
+            wt[a][1] = double(f);
+            wt[a][0] = 1.0 - wt[a][1];
+        }
+    }
+    const double vre = double(v.re), vim = flip ? -double(v.im) : double(v.im), wp = double(wpix);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        if (loc[2][k] < 0) continue;
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+            if (loc[1][i] < 0) continue;
+            const double wdr = wt[2][k] * wt[1][i];
+            const int row = (loc[2][k] * SR + loc[1][i]) * SC;
+#pragma unroll
+            for (int j = 0; j < K; ++j) {
+                if (loc[0][j] < 0) continue;
+                const double w = wdr * wt[0][j];
+                const int li = row + loc[0][j];
+                atomicAdd(&acc_re[li], vre * w);
+                atomicAdd(&acc_im[li], vim * w);
+                if (WEIGHTS) atomicAdd(&acc_w[li], wp * (CUBIC ? fabs(w) : w));
+            }
+        }
+    }
 }
 
 // MODE 0: backprojection, v = proj * conj(phase(r, c)), optional weights.
@@ -444,6 +478,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                                                            const float* __restrict__ shifts,
                                                            Cx<float>* __restrict__ dst, float* __restrict__ wdst) {
     constexpr int SL = CUBIC ? 2 : 1, SH = CUBIC ? 1 : 0;  // stencil reach below / above floor(x)
+    constexpr int SLOW = CUBIC ? 1 : 0;                    // first tap at floor(x) - SLOW
     constexpr int RPS = 64 / KP;
     constexpr int NT = kScatterThreads, NW = NT / 64;
     __shared__ double acc_re[S3], acc_im[S3];
@@ -508,8 +543,6 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                 Sh[1] = Sn[1];
                 if (base + NW * KP < np)
                     load_pose(rotb, shb, pbase + (plist[min(base + NW * KP + slot, np - 1)] & kPoseMask), Rn, Sn);
-                int ra0, ra1;
-                box_rows(R, lo1, hi1, ts, ra0, ra1);
                 if (jrow == 0 && sv) {
                     Slot& sd = slots[wave][slot];
 #pragma unroll
@@ -517,8 +550,6 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                     sd.s0 = Sh[0];
                     sd.s1 = Sh[1];
                     sd.p = pp;
-                    sd.r0a = (entry & kHit1) ? ra0 : 1;
-                    sd.r1a = (entry & kHit1) ? ra1 : 0;
                 }
                 __builtin_amdgcn_wave_barrier();
 #pragma unroll 1
@@ -529,15 +560,19 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                         lo[k] = pass == 0 ? lo1[k] : lo2[k];
                         hi[k] = pass == 0 ? hi1[k] : hi2[k];
                     }
+                    // direct taps: l = floor(x) - LOW + j - t; flipped: l = -(floor(x) - LOW + j) - t,
+                    // and at c = 0 a flipped tap must have c < 0 (l >= 1 when t_c = 0)
+                    TapMap tm;
+                    tm.sgn = pass == 0 ? 1 : -1;
+                    tm.off[0] = pass == 0 ? -SLOW - tc : SLOW - tc;
+                    tm.off[1] = pass == 0 ? -SLOW - tr : SLOW - tr;
+                    tm.off[2] = pass == 0 ? -SLOW - td : SLOW - td;
+                    tm.lmin[0] = (pass == 1 && tc == 0) ? 1 : 0;
+                    tm.lmin[1] = tm.lmin[2] = 0;
                     const bool crosses = sv && (entry & (pass == 0 ? kHit1 : kHit2));
                     if (!__any(crosses)) continue;
                     int r0, r1;
-                    if (pass == 0) {
-                        r0 = ra0;
-                        r1 = ra1;
-                    } else {
-                        box_rows(R, lo, hi, ts, r0, r1);
-                    }
+                    box_rows(R, lo, hi, ts, r0, r1);
                     const int nr = crosses ? max(0, r1 - r0 + 1) : 0;
                     const int maxnr = wave_max(nr);
                     for (int rbase = 0; rbase < maxnr; rbase += RPS) {
@@ -563,11 +598,6 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                             sl = lw / RPS;
                             ok = e < total;
                             const Slot& sd = slots[wave][sl];
-                            if (ok && pass == 1 && rr >= sd.r0a && rr <= sd.r1a) {
-                                int a0, a1;  // already enumerated by box 1?
-                                row_span(sd.R, rr, lo1, hi1, ts, cut2, a0, a1);
-                                ok = cc < a0 || cc > a1;
-                            }
                             ok = ok && !filtered(float(rr), float(cc), cut2) &&
                                  !(cc == 0 && (rr == g.n / 2 || rr < 0));  // Friedel half of x = 0
                             const int i = rr >= 0 ? rr : rr + g.n;
@@ -589,8 +619,8 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                             if (e0 + 64 < total) fetch_sample(e0 + 64, rr2, cc2, sl2, ok2, v2, wv2);
                             if (ok)
                                 scatter_sample<CUBIC, MODE, WEIGHTS>(g, slots[wave][sl], rr, cc, v, wv,
-                                                                     shifts != nullptr, tc, tr, td, acc_re, acc_im,
-                                                                     acc_w);
+                                                                     shifts != nullptr, pass == 1, tm, acc_re,
+                                                                     acc_im, acc_w);
                             rr = rr2;
                             cc = cc2;
                             sl = sl2;
