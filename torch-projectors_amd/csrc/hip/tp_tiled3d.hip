@@ -407,6 +407,14 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
 // (sample, tap) pair is thus deposited by exactly one pass.  Taps outside the
 // reference's range [-N/2+1, N/2] are dropped there; here they fall outside
 // the tile or on cells past the volume edge, which are never written out.
+// LDS layout of the scatter accumulators: cell (lc, lr, ld) sits at
+// (ld * SR + lr) * SC + ((lc + acc_swizzle(lr, ld)) mod SC).  Rotating each
+// row by an amount that changes with lr / 2 and ld spreads the taps of
+// samples stepping along r or d over different banks (an fp64 cell spans two
+// of the 64 four-byte banks, so without it every cell of a column shares one).
+static_assert((SC & (SC - 1)) == 0, "scatter tile width must be a power of two");
+__device__ __forceinline__ int acc_swizzle(int lr, int ld) { return ((lr >> 1) + 3 * ld) & (SC - 1); }
+
 // Per-pass constants: local cell of tap j on axis a is sgn * floor(x_a) + off[a] + sgn * j
 // (sgn = -1 for the flipped taps), valid in [lmin[a], S_a).
 struct TapMap {
@@ -455,12 +463,12 @@ __device__ __forceinline__ void scatter_sample(const Geom& g, const Slot& sd, in
         for (int i = 0; i < K; ++i) {
             if (loc[1][i] < 0) continue;
             const double wdr = wt[2][k] * wt[1][i];
-            const int row = (loc[2][k] * SR + loc[1][i]) * SC;
+            const int row = (loc[2][k] * SR + loc[1][i]) * SC, rot = acc_swizzle(loc[1][i], loc[2][k]);
 #pragma unroll
             for (int j = 0; j < K; ++j) {
                 if (loc[0][j] < 0) continue;
                 const double w = wdr * wt[0][j];
-                const int li = row + loc[0][j];
+                const int li = row + ((loc[0][j] + rot) & (SC - 1));
                 atomicAdd(&acc_re[li], vre * w);
                 atomicAdd(&acc_im[li], vim * w);
                 if (WEIGHTS) atomicAdd(&acc_w[li], wp * (CUBIC ? fabs(w) : w));
@@ -643,13 +651,14 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
             if (c >= H || r > half || d > half) continue;
             const int re = r < 0 ? r + N : r, de = d < 0 ? d + N : d;
             const int64_t idx = b * g.vol + (int64_t(de) * N + re) * H + c;
+            const int a = (e - lc) + ((lc + acc_swizzle(lr, ld)) & (SC - 1));
             if (it.core) {
-                atomic_add(&dst[idx].re, float(acc_re[e]));
-                atomic_add(&dst[idx].im, float(acc_im[e]));
-                if (WEIGHTS) atomic_add(&wdst[idx], float(acc_w[e]));
+                atomic_add(&dst[idx].re, float(acc_re[a]));
+                atomic_add(&dst[idx].im, float(acc_im[a]));
+                if (WEIGHTS) atomic_add(&wdst[idx], float(acc_w[a]));
             } else {
-                dst[idx] = Cx<float>{float(acc_re[e]), float(acc_im[e])};
-                if (WEIGHTS) wdst[idx] = float(acc_w[e]);
+                dst[idx] = Cx<float>{float(acc_re[a]), float(acc_im[a])};
+                if (WEIGHTS) wdst[idx] = float(acc_w[a]);
             }
         }
         __syncthreads();
