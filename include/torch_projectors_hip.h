@@ -12,7 +12,8 @@
  *   - complex arrays are interleaved (re, im) pairs of the real type chosen
  *     by `dtype` (TP_F32: complex64 / float32, TP_F64: complex128 / float64);
  *     rotations, shifts and weights use that same real type;
- *   - an optional input is passed as NULL when absent;
+ *   - an optional input is passed as NULL when absent; an array with no
+ *     elements may be passed as NULL too;
  *   - an optional gradient output is passed as NULL when it is not wanted
  *     (the reference decides this from `requires_grad`, projection_utils.h:112-113);
  *   - every output element is written by the call (no pre-zeroing needed);
@@ -87,7 +88,9 @@ int tp_project_2d_back(int dtype,
 
 /* Replaces backproject_2d_forw_cuda (cuda/2d/backprojection_2d_kernels.cu:827-977).
  * Outputs have shape [B, N, N/2+1] with N = tp_backproject_rec_boxsize(n, os);
- * weight_reconstruction must be non-NULL exactly when weights is. */
+ * weight_reconstruction must be non-NULL exactly when weights is (when
+ * B * P == 0, weights may be NULL with weight_reconstruction given: it is
+ * zero-filled). */
 int tp_backproject_2d_forw(int dtype,
                            const void* projections, int64_t B, int64_t P, int64_t proj_boxsize, int64_t proj_boxsize_half,
                            const void* weights,
@@ -134,7 +137,8 @@ int tp_project_3d_to_2d_back(int dtype,
                              void* stream);
 
 /* Replaces backproject_2d_to_3d_forw_cuda (cuda/3d/backprojection_2d_to_3d_kernels.cu:1001-1188).
- * Outputs have shape [B, N, N, N/2+1] with N = tp_backproject_rec_boxsize(n, os). */
+ * Outputs have shape [B, N, N, N/2+1] with N = tp_backproject_rec_boxsize(n, os);
+ * weights and weight_reconstruction pair as for tp_backproject_2d_forw. */
 int tp_backproject_2d_to_3d_forw(int dtype,
                                  const void* projections, int64_t B, int64_t P, int64_t proj_boxsize, int64_t proj_boxsize_half,
                                  const void* weights,

@@ -1,0 +1,200 @@
+"""The BASELINE configurations at their full sizes, through the dispatcher ops.
+
+The oracle cannot redo whole full-size runs in seconds, so these tests use
+properties that hold at any size:
+
+* poses are independent: the GPU result of a sampled pose (its projection,
+  its gradient rows, its grad_projections) equals the oracle's run on that
+  pose alone;
+* batch items are independent: a sampled item's volume sums equal the
+  oracle's on that item's poses;
+* a volume sum over every pose is compared whole where the oracle finishes
+  in seconds (the headline backprojection).
+
+Inputs follow bench.py's synthetic recipes (seeded).  Bars as tests/parity.py:
+gathers bit-identical without shifts, else relative L2 1e-5; scatters and
+pose gradients relative L2 1e-4.
+"""
+import pytest
+import torch
+
+import bench
+from tests.parity import GATHER_TOL, SCATTER_TOL, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+F32 = torch.float32
+
+
+@pytest.fixture(scope="module")
+def ops(gpu):
+    import torch_projectors  # noqa: F401  (registers the dispatcher ops; fails without the HIP library)
+    return torch.ops.torch_projectors
+
+
+@pytest.fixture(scope="module")
+def O():
+    from oracle import oracle
+    return oracle
+
+
+def say(msg):
+    print(f"[fullsize] {msg}", flush=True)
+
+
+def close(got, exp, tol, what):
+    err = rel_l2(got, exp)
+    say(f"{what}: rel L2 {err:.2e}")
+    assert err <= tol, f"{what}: relative L2 {err:.3e} > {tol:.0e}"
+
+
+# ----------------------------------------------------------------------------- headline (3D linear)
+@pytest.fixture(scope="module")
+def headline(gpu):
+    gen = torch.Generator().manual_seed(20261201 + 6)
+    vol = bench.blob_volume_rfft(256, 512, 32, 80.0, gen, gpu)
+    rot = bench.quat_rotations(2048, gen)[None].to(gpu)
+    sh = ((torch.rand(1, 2048, 2, generator=gen) * 16) - 8).to(gpu)
+    w = bench.ctf2_weights(1, 2048, 256, gen).float().to(gpu)
+    return vol, rot, sh, w
+
+
+POSES = [0, 1, 1031, 2047]
+
+
+def test_headline_forward_sampled_poses(headline, ops, O):
+    vol, rot, sh, _ = headline
+    say("headline forward, 2048 poses")
+    vol_c = vol.cpu()
+    proj = ops.project_3d_to_2d_forw(vol, rot, sh, [256, 256], "linear", 2.0, None)
+    assert proj.shape == (1, 2048, 256, 129)
+    exp = O.project_3d_to_2d_forw(vol_c, rot[:, POSES].cpu(), sh[:, POSES].cpu(), [256, 256], "linear", 2.0, None)
+    close(proj[:, POSES].cpu(), exp, GATHER_TOL[F32], "forward with shifts, sampled poses")
+    proj0 = ops.project_3d_to_2d_forw(vol, rot, None, [256, 256], "linear", 2.0, None)
+    exp0 = O.project_3d_to_2d_forw(vol_c, rot[:, POSES].cpu(), None, [256, 256], "linear", 2.0, None)
+    assert torch.equal(proj0[:, POSES].cpu(), exp0), "forward without shifts must be bit-identical"
+
+
+def test_headline_backprojection_whole(headline, ops, O):
+    vol, rot, sh, w = headline
+    say("headline backprojection, 2048 poses, whole volume against the oracle")
+    proj = ops.project_3d_to_2d_forw(vol, rot, sh, [256, 256], "linear", 2.0, None)
+    data, wrec = ops.backproject_2d_to_3d_forw(proj, w, rot, sh, "linear", 2.0, None)
+    assert data.shape == (1, 512, 512, 257) and wrec.shape == (1, 512, 512, 257)
+    ed, ew = O.backproject_2d_to_3d_forw(proj.cpu(), w.cpu(), rot.cpu(), sh.cpu(), "linear", 2.0, None)
+    close(data.cpu(), ed, SCATTER_TOL[F32], "backprojection data")
+    close(wrec.cpu(), ew, SCATTER_TOL[F32], "backprojection weights")
+
+
+# ----------------------------------------------------------------------------- c4 (3D cubic, forward + backward)
+@pytest.fixture(scope="module")
+def c4(gpu):
+    gen = torch.Generator().manual_seed(20261201 + 4)
+    vol = bench.blob_volume_rfft(256, 512, 32, 80.0, gen, gpu)
+    rot = bench.quat_rotations(2048, gen)[None].to(gpu)
+    sh = ((torch.rand(1, 2048, 2, generator=gen) * 16) - 8).to(gpu)
+    g = torch.randn(1, 2048, 256, 129, generator=gen, dtype=torch.complex64).to(gpu)
+    return vol, rot, sh, g
+
+
+def test_c4_cubic_forward_sampled_poses(c4, ops, O):
+    vol, rot, sh, _ = c4
+    say("c4 cubic forward, 2048 poses")
+    proj = ops.project_3d_to_2d_forw(vol, rot, sh, [256, 256], "cubic", 2.0, None)
+    exp = O.project_3d_to_2d_forw(vol.cpu(), rot[:, POSES].cpu(), sh[:, POSES].cpu(), [256, 256], "cubic", 2.0, None)
+    close(proj[:, POSES].cpu(), exp, GATHER_TOL[F32], "cubic forward, sampled poses")
+
+
+def test_c4_cubic_backward(c4, ops, O):
+    vol, rot, sh, g = c4
+    say("c4 cubic backward, 2048 poses; pose gradients of sampled poses")
+    rg, sg = rot.clone().requires_grad_(True), sh.clone().requires_grad_(True)
+    grec, grot, gsh = ops.project_3d_to_2d_back(g, vol, rg, sg, "cubic", 2.0, None)
+    assert grec.shape == vol.shape and grot.shape == rot.shape and gsh.shape == sh.shape
+    vol_c = vol.cpu()
+    r_c = rot[:, POSES].cpu().requires_grad_(True)
+    s_c = sh[:, POSES].cpu().requires_grad_(True)
+    _, er, es = O.project_3d_to_2d_back(g[:, POSES].cpu(), vol_c, r_c, s_c, "cubic", 2.0, None)
+    close(grot[:, POSES].cpu(), er, SCATTER_TOL[F32], "rotation gradients, sampled poses")
+    close(gsh[:, POSES].cpu(), es, SCATTER_TOL[F32], "shift gradients, sampled poses")
+    say("c4 reconstruction gradient over the first 48 poses, whole volume")
+    sub = slice(0, 48)
+    grec_s, _, _ = ops.project_3d_to_2d_back(g[:, sub].contiguous(), vol, rot[:, sub].contiguous(),
+                                             sh[:, sub].contiguous(), "cubic", 2.0, None)
+    eg, _, _ = O.project_3d_to_2d_back(g[:, sub].cpu(), vol_c, rot[:, sub].cpu(), sh[:, sub].cpu(), "cubic", 2.0,
+                                       None)
+    close(grec_s.cpu(), eg, SCATTER_TOL[F32], "reconstruction gradient")
+
+
+# ----------------------------------------------------------------------------- c5 (batched 2D cubic)
+@pytest.fixture(scope="module")
+def c5(gpu):
+    gen = torch.Generator().manual_seed(20261201 + 5)
+    rec = bench.noise_image_rfft(16, 256, 512, gen, gpu).to(torch.complex64)
+    rot = bench.angle_rotations((16, 4096), gen).to(gpu)
+    sh = (3 * torch.randn(16, 4096, 2, generator=gen)).to(gpu)
+    return rec, rot, sh
+
+
+ITEMS = [0, 15]
+PAIRS = [(0, 0), (0, 4095), (15, 2048), (15, 7)]
+
+
+def test_c5_batched_2d_cubic(c5, ops, O):
+    rec, rot, sh = c5
+    say("c5 forward: 16 x 4096 projections (2.16e9 complex elements)")
+    proj = ops.project_2d_forw(rec, rot, sh, [256, 256], "cubic", 2.0, 64.0)
+    assert proj.shape == (16, 4096, 256, 129) and proj.numel() > 2 ** 31
+    rec_c = rec.cpu()
+    for b, p in PAIRS:
+        exp = O.project_2d_forw(rec_c[b:b + 1], rot[b:b + 1, p:p + 1].cpu(), sh[b:b + 1, p:p + 1].cpu(), [256, 256],
+                                "cubic", 2.0, 64.0)
+        close(proj[b:b + 1, p:p + 1].cpu(), exp, GATHER_TOL[F32], f"forward (item {b}, pose {p})")
+
+    say("c5 backprojection with unit weights")
+    ones = torch.ones(16, 4096, 256, 129, device=proj.device, dtype=F32)
+    data, wrec = ops.backproject_2d_forw(proj, ones, rot, sh, "cubic", 2.0, 64.0)
+    assert data.shape == (16, 512, 257)
+    for b in ITEMS:
+        ed, ew = O.backproject_2d_forw(proj[b:b + 1].cpu(), ones[b:b + 1].cpu(), rot[b:b + 1].cpu(),
+                                       sh[b:b + 1].cpu(), "cubic", 2.0, 64.0)
+        close(data[b:b + 1].cpu(), ed, SCATTER_TOL[F32], f"backprojection data (item {b})")
+        close(wrec[b:b + 1].cpu(), ew, SCATTER_TOL[F32], f"backprojection weights (item {b})")
+
+    say("c5 backward of a loss on (data, weight)")
+    gen = torch.Generator().manual_seed(20261201 + 55)
+    gd = torch.randn(16, 512, 257, generator=gen, dtype=torch.complex64).to(proj.device)
+    gw = torch.randn(16, 512, 257, generator=gen).to(proj.device)
+    rg, sg = rot.clone().requires_grad_(True), sh.clone().requires_grad_(True)
+    gproj, gwts, grot, gsh = ops.backproject_2d_back(gd, gw, proj, ones, rg, sg, "cubic", 2.0, 64.0)
+    assert gproj.shape == proj.shape and gwts.shape == ones.shape
+    for b, p in PAIRS:
+        r_c = rot[b:b + 1, p:p + 1].cpu().requires_grad_(True)
+        s_c = sh[b:b + 1, p:p + 1].cpu().requires_grad_(True)
+        e = O.backproject_2d_back(gd[b:b + 1].cpu(), gw[b:b + 1].cpu(), proj[b:b + 1, p:p + 1].cpu(),
+                                  ones[b:b + 1, p:p + 1].cpu(), r_c, s_c, "cubic", 2.0, 64.0)
+        close(gproj[b:b + 1, p:p + 1].cpu(), e[0], GATHER_TOL[F32], f"grad_projections (item {b}, pose {p})")
+        close(gwts[b:b + 1, p:p + 1].cpu(), e[1], GATHER_TOL[F32], f"grad_weights (item {b}, pose {p})")
+        close(grot[b:b + 1, p:p + 1].cpu(), e[2], SCATTER_TOL[F32], f"grad_rotations (item {b}, pose {p})")
+        close(gsh[b:b + 1, p:p + 1].cpu(), e[3], SCATTER_TOL[F32], f"grad_shifts (item {b}, pose {p})")
+    del ones, gwts
+
+    say("c5 reconstruction gradient (project_2d_back), item 0 over all its poses")
+    grec, _, _ = ops.project_2d_back(gproj, rec, rot, sh, "cubic", 2.0, 64.0)
+    assert grec.shape == rec.shape
+    eg, _, _ = O.project_2d_back(gproj[0:1].cpu(), rec_c[0:1], rot[0:1].cpu(), sh[0:1].cpu(), "cubic", 2.0, 64.0)
+    close(grec[0:1].cpu(), eg, SCATTER_TOL[F32], "reconstruction gradient (item 0)")
+
+
+# ----------------------------------------------------------------------------- empty inputs
+def test_zero_poses(ops, gpu):
+    vol = torch.randn(1, 32, 32, 17, dtype=torch.complex64, device=gpu)
+    rot = torch.empty(1, 0, 3, 3, device=gpu)
+    proj = ops.project_3d_to_2d_forw(vol, rot, None, [32, 32], "linear", 1.0, None)
+    assert proj.shape == (1, 0, 32, 17)
+    data, wrec = ops.backproject_2d_to_3d_forw(proj, torch.empty(1, 0, 32, 17, device=gpu), rot, None, "linear",
+                                               2.0, None)
+    torch.cuda.synchronize()
+    assert data.shape == (1, 64, 64, 33) and torch.count_nonzero(data) == 0 and torch.count_nonzero(wrec) == 0
+    grec, grot, gsh = ops.project_3d_to_2d_back(proj, vol, rot, None, "cubic", 1.0, None)
+    assert grec.shape == vol.shape and torch.count_nonzero(grec) == 0

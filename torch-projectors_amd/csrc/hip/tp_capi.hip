@@ -231,7 +231,8 @@ int backproject_forw(int dim, int dtype, const void* proj, int64_t B, int64_t P,
     tp::Geom g{};
     TP_TRY(check_common(dtype, interp, B, P, B_rot, shifts, B_shift, g));
     if (hp != n / 2 + 1) return fail("projections last dimension must be boxsize/2+1");
-    if ((weights == nullptr) != (wrec == nullptr))
+    // with no samples (B * P == 0) an empty weights array may come as NULL; its volume is still zeroed
+    if ((weights == nullptr) != (wrec == nullptr) && !(weights == nullptr && B * P == 0))
         return fail("weight_reconstruction must be given exactly when weights are");
     const int64_t N = rec_box(n, os);
     TP_TRY(set_rec(dim, N, N / 2 + 1, g));
