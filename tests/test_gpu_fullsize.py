@@ -86,6 +86,47 @@ def test_headline_backprojection_whole(headline, ops, O):
     close(wrec.cpu(), ew, SCATTER_TOL[F32], "backprojection weights")
 
 
+# ----------------------------------------------------------------------------- c1 - c3
+def test_c1_2d_linear_whole(ops, O, gpu):
+    gen = torch.Generator().manual_seed(20261201 + 1)
+    rec = bench.noise_image_rfft(1, 64, 128, gen, gpu).to(torch.complex64)
+    rot = bench.angle_rotations((1, 256), gen).to(gpu)
+    sh = (2 * torch.randn(1, 256, 2, generator=gen)).to(gpu)
+    say("c1 2D linear forward and backprojection, 256 poses")
+    proj = ops.project_2d_forw(rec, rot, sh, [64, 64], "linear", 2.0, None)
+    exp = O.project_2d_forw(rec.cpu(), rot.cpu(), sh.cpu(), [64, 64], "linear", 2.0, None)
+    close(proj.cpu(), exp, GATHER_TOL[F32], "c1 forward")
+    data, _ = ops.backproject_2d_forw(proj, None, rot, sh, "linear", 2.0, None)
+    ed, _ = O.backproject_2d_forw(proj.cpu(), None, rot.cpu(), sh.cpu(), "linear", 2.0, None)
+    close(data.cpu(), ed, SCATTER_TOL[F32], "c1 backprojection")
+
+
+def test_c2_forward_sampled_poses(ops, O, gpu):
+    gen = torch.Generator().manual_seed(20261201 + 2)
+    vol = bench.blob_volume_rfft(128, 256, 32, 40.0, gen, gpu)
+    rot = bench.quat_rotations(4096, gen)[None].to(gpu)
+    sh = ((torch.rand(1, 4096, 2, generator=gen) * 10) - 5).to(gpu)
+    say("c2 forward, 4096 poses of a 256^3 volume")
+    proj = ops.project_3d_to_2d_forw(vol, rot, sh, [128, 128], "linear", 2.0, None)
+    idx = [0, 2049, 4095]
+    exp = O.project_3d_to_2d_forw(vol.cpu(), rot[:, idx].cpu(), sh[:, idx].cpu(), [128, 128], "linear", 2.0, None)
+    close(proj[:, idx].cpu(), exp, GATHER_TOL[F32], "c2 forward, sampled poses")
+
+
+def test_c3_backprojection_whole(ops, O, gpu):
+    gen = torch.Generator().manual_seed(20261201 + 3)
+    proj = torch.randn(1, 8192, 128, 65, generator=gen, dtype=torch.complex64).to(gpu)
+    w = bench.ctf2_weights(1, 8192, 128, gen).float().to(gpu)
+    rot = bench.quat_rotations(8192, gen)[None].to(gpu)
+    sh = ((torch.rand(1, 8192, 2, generator=gen) * 10) - 5).to(gpu)
+    say("c3 backprojection, 8192 poses, whole volume against the oracle")
+    data, wrec = ops.backproject_2d_to_3d_forw(proj, w, rot, sh, "linear", 2.0, None)
+    assert data.shape == (1, 256, 256, 129)
+    ed, ew = O.backproject_2d_to_3d_forw(proj.cpu(), w.cpu(), rot.cpu(), sh.cpu(), "linear", 2.0, None)
+    close(data.cpu(), ed, SCATTER_TOL[F32], "c3 backprojection data")
+    close(wrec.cpu(), ew, SCATTER_TOL[F32], "c3 backprojection weights")
+
+
 # ----------------------------------------------------------------------------- c4 (3D cubic, forward + backward)
 @pytest.fixture(scope="module")
 def c4(gpu):
