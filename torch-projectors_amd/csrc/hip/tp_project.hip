@@ -70,11 +70,15 @@ __global__ __launch_bounds__(kBlock) void k_project3_forw_rest(Geom g, const Cx<
         const float* S = shifts ? shifts + ((g.B_shift == 1 ? 0 : b) * g.P + p) * 2 : nullptr;
         const bool tiled = pose_is_rotation(R);
         Cx<float>* outp = out + bp * g.npix;
-        for (int pix = threadIdx.x; pix < g.npix; pix += kBlock) {
-            const int i = pix / g.hp, j = pix - i * g.hp;
-            const float r = freq_of<float>(i, g.n), c = float(j);
-            if (filtered(r, c, cut2)) outp[pix] = Cx<float>{0.f, 0.f};
-            else if (!tiled) outp[pix] = project_pixel<3, float, CUBIC>(g, rec + b * g.vol, R, S, r, c);
+        // one row per wave, lanes along the row (no per-pixel division)
+        for (int i = threadIdx.x / 64; i < g.n; i += kBlock / 64) {
+            const float r = freq_of<float>(i, g.n);
+            Cx<float>* row = outp + int64_t(i) * g.hp;
+            for (int j = threadIdx.x % 64; j < g.hp; j += 64) {
+                const float c = float(j);
+                if (filtered(r, c, cut2)) row[j] = Cx<float>{0.f, 0.f};
+                else if (!tiled) row[j] = project_pixel<3, float, CUBIC>(g, rec + b * g.vol, R, S, r, c);
+            }
         }
     }
 }

@@ -160,6 +160,16 @@ __device__ __forceinline__ int window_owner(int cnt, int excl, int e0, int& carr
     return m - 1;
 }
 
+// Sample position of pixel (r, c): rotate<3> without its R[k][2] * 0 terms.
+// Adding that signed zero to the other two terms can only flip the sign of a
+// zero coordinate, which floors to the same cell with the same fraction.
+__device__ __forceinline__ void rotate_slice(const float* __restrict__ R, float r, float c, double os, float* x) {
+    const float sc = float(double(c) * os), sr = float(double(r) * os);
+    x[0] = R[0] * sc + R[1] * sr;
+    x[1] = R[3] * sc + R[4] * sr;
+    x[2] = R[6] * sc + R[7] * sr;
+}
+
 // Per-wave copy of the poses of one batch.
 struct Slot {
     float R[9];
@@ -379,8 +389,8 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                         const Slot& sd = slots[wave][lw / RPS];
                         const float fr = float(rr), fc = float(cc);
                         if (filtered(fr, fc, cut2)) continue;
-                        float x[3], sc, sr;
-                        rotate<3>(sd.R, fr, fc, g.os, x, sc, sr);
+                        float x[3];
+                        rotate_slice(sd.R, fr, fc, g.os, x);
                         const int fxc = int(floorf(x[0])), fxr = int(floorf(x[1])), fxd = int(floorf(x[2]));
                         if (fxc < tc || fxc >= tc + L || fxr < tr || fxr >= tr + L || fxd < td || fxd >= td + L)
                             continue;
@@ -429,8 +439,8 @@ __device__ __forceinline__ void scatter_sample(const Geom& g, const Slot& sd, in
                                                double* acc_im, double* acc_w) {
     constexpr int K = CUBIC ? 4 : 2, LOW = CUBIC ? 1 : 0;  // taps at floor(x) - LOW + j, j < K
     const float fr = float(rr), fc = float(cc);
-    float x[3], sc, sr;
-    rotate<3>(sd.R, fr, fc, g.os, x, sc, sr);
+    float x[3];
+    rotate_slice(sd.R, fr, fc, g.os, x);
     if (shifted) {
         if (MODE == 0) v = cmul(v, cconj(phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k)));
         else v = cmul(v, phase_hw(-fr, -fc, sd.s0, sd.s1, g.phase_k));
