@@ -269,6 +269,43 @@ __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pe
     return np;
 }
 
+// Scatter culling: poses [pbase, pend) (at most kChunkSc) against box 1 and
+// box 2 separately.  Box-1 survivors fill plist from the front, box-2
+// survivors from the back (kChunk entries hold both lists), so each pass
+// batches only poses that cross its box.
+constexpr int kChunkSc = kChunk / 2;
+template <int NT>
+__device__ __forceinline__ void cull_chunk_boxes(const float* __restrict__ rotb, int pend, int pbase,
+                                                 const float* lo1, const float* hi1, const float* lo2,
+                                                 const float* hi2, unsigned short* plist, int* pcnt, int& n1,
+                                                 int& n2) {
+    static_assert(kChunkSc % NT == 0 && (kChunkSc / NT) % kCullInFlight == 0, "cull shape");
+    __syncthreads();  // every lane has read the previous counts and lists
+    if (threadIdx.x == 0) pcnt[0] = pcnt[1] = 0;
+    __syncthreads();
+#pragma unroll 1
+    for (int q0 = 0; q0 < kChunkSc / NT; q0 += kCullInFlight) {
+        float R[kCullInFlight][9];
+#pragma unroll
+        for (int q = 0; q < kCullInFlight; ++q) {
+            const int p = min(pbase + int(threadIdx.x) + (q0 + q) * NT, pend - 1);
+            load_rot(rotb + int64_t(p) * 9, R[q]);
+        }
+#pragma unroll
+        for (int q = 0; q < kCullInFlight; ++q) {
+            const int p = pbase + int(threadIdx.x) + (q0 + q) * NT;
+            if (p >= pend || !pose_is_rotation(R[q])) continue;
+            if (plane_hits(R[q], lo1, hi1) && half_plane_hits(R[q], hi1, lo1))
+                plist[atomicAdd(&pcnt[0], 1)] = (unsigned short)(p - pbase);
+            if (plane_hits(R[q], lo2, hi2) && half_plane_hits(R[q], hi2, lo2))
+                plist[kChunk - 1 - atomicAdd(&pcnt[1], 1)] = (unsigned short)(p - pbase);
+        }
+    }
+    __syncthreads();
+    n1 = pcnt[0];
+    n2 = pcnt[1];
+}
+
 // ----------------------------------------------------------------------------- forward
 template <bool CUBIC, int KP>
 __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ rec,
@@ -502,7 +539,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
     __shared__ double acc_re[S3], acc_im[S3];
     __shared__ double acc_w[WEIGHTS ? S3 : 1];
     __shared__ unsigned short plist[kChunk];
-    __shared__ int pcount;
+    __shared__ int pcnt[2];
     __shared__ Slot slots[NW][KP];
     __shared__ int marks[NW][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -544,54 +581,55 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
         }
         const int pend = dist2 > ts.rho * ts.rho ? it.p0 : it.p1;
 
-        for (int pbase = it.p0; pbase < pend; pbase += kChunk) {
-            const int np = cull_chunk<NT, true>(rotb, pend, pbase, lo1, hi1, lo2, hi2, plist, &pcount);
-            int base = wave * KP;
-            float Rn[9], Sn[2];
-            const float* shb = shifts ? shifts + sb * g.P * 2 : nullptr;
-            if (base < np) load_pose(rotb, shb, pbase + (plist[min(base + slot, np - 1)] & kPoseMask), Rn, Sn);
-            for (; base < np; base += NW * KP) {
-                const bool sv = base + slot < np;
-                const unsigned entry = plist[min(base + slot, np - 1)];
-                const int pp = pbase + int(entry & kPoseMask);
-                float R[9], Sh[2];
-#pragma unroll
-                for (int e = 0; e < 9; ++e) R[e] = Rn[e];
-                Sh[0] = Sn[0];
-                Sh[1] = Sn[1];
-                if (base + NW * KP < np)
-                    load_pose(rotb, shb, pbase + (plist[min(base + NW * KP + slot, np - 1)] & kPoseMask), Rn, Sn);
-                if (jrow == 0 && sv) {
-                    Slot& sd = slots[wave][slot];
-#pragma unroll
-                    for (int e = 0; e < 9; ++e) sd.R[e] = R[e];
-                    sd.s0 = Sh[0];
-                    sd.s1 = Sh[1];
-                    sd.p = pp;
-                }
-                __builtin_amdgcn_wave_barrier();
+        const float* shb = shifts ? shifts + sb * g.P * 2 : nullptr;
+        for (int pbase = it.p0; pbase < pend; pbase += kChunkSc) {
+            int n1, n2;
+            cull_chunk_boxes<NT>(rotb, pend, pbase, lo1, hi1, lo2, hi2, plist, pcnt, n1, n2);
 #pragma unroll 1
-                for (int pass = 0; pass < 2; ++pass) {
-                    float lo[3], hi[3];
+            for (int pass = 0; pass < 2; ++pass) {
+                const int np = pass == 0 ? n1 : n2;
+                // pose of list entry k of this pass (box-2 entries are stored from the back)
+                auto pose_at = [&](int k) { return pbase + int(plist[pass == 0 ? k : kChunk - 1 - k]); };
+                float lo[3], hi[3];
 #pragma unroll
-                    for (int k = 0; k < 3; ++k) {
-                        lo[k] = pass == 0 ? lo1[k] : lo2[k];
-                        hi[k] = pass == 0 ? hi1[k] : hi2[k];
+                for (int k = 0; k < 3; ++k) {
+                    lo[k] = pass == 0 ? lo1[k] : lo2[k];
+                    hi[k] = pass == 0 ? hi1[k] : hi2[k];
+                }
+                // direct taps: l = floor(x) - LOW + j - t; flipped: l = -(floor(x) - LOW + j) - t,
+                // and at c = 0 a flipped tap must have c < 0 (l >= 1 when t_c = 0)
+                TapMap tm;
+                tm.sgn = pass == 0 ? 1 : -1;
+                tm.off[0] = pass == 0 ? -SLOW - tc : SLOW - tc;
+                tm.off[1] = pass == 0 ? -SLOW - tr : SLOW - tr;
+                tm.off[2] = pass == 0 ? -SLOW - td : SLOW - td;
+                tm.lmin[0] = (pass == 1 && tc == 0) ? 1 : 0;
+                tm.lmin[1] = tm.lmin[2] = 0;
+                int base = wave * KP;
+                float Rn[9], Sn[2];
+                if (base < np) load_pose(rotb, shb, pose_at(min(base + slot, np - 1)), Rn, Sn);
+                for (; base < np; base += NW * KP) {
+                    const bool sv = base + slot < np;
+                    const int pp = pose_at(min(base + slot, np - 1));
+                    float R[9], Sh[2];
+#pragma unroll
+                    for (int e = 0; e < 9; ++e) R[e] = Rn[e];
+                    Sh[0] = Sn[0];
+                    Sh[1] = Sn[1];
+                    if (base + NW * KP < np) load_pose(rotb, shb, pose_at(min(base + NW * KP + slot, np - 1)), Rn, Sn);
+                    if (jrow == 0 && sv) {
+                        Slot& sd = slots[wave][slot];
+#pragma unroll
+                        for (int e = 0; e < 9; ++e) sd.R[e] = R[e];
+                        sd.s0 = Sh[0];
+                        sd.s1 = Sh[1];
+                        sd.p = pp;
                     }
-                    // direct taps: l = floor(x) - LOW + j - t; flipped: l = -(floor(x) - LOW + j) - t,
-                    // and at c = 0 a flipped tap must have c < 0 (l >= 1 when t_c = 0)
-                    TapMap tm;
-                    tm.sgn = pass == 0 ? 1 : -1;
-                    tm.off[0] = pass == 0 ? -SLOW - tc : SLOW - tc;
-                    tm.off[1] = pass == 0 ? -SLOW - tr : SLOW - tr;
-                    tm.off[2] = pass == 0 ? -SLOW - td : SLOW - td;
-                    tm.lmin[0] = (pass == 1 && tc == 0) ? 1 : 0;
-                    tm.lmin[1] = tm.lmin[2] = 0;
-                    const bool crosses = sv && (entry & (pass == 0 ? kHit1 : kHit2));
-                    if (!__any(crosses)) continue;
+                    __builtin_amdgcn_wave_barrier();
+                    {
                     int r0, r1;
                     box_rows(R, lo, hi, ts, r0, r1);
-                    const int nr = crosses ? max(0, r1 - r0 + 1) : 0;
+                    const int nr = sv ? max(0, r1 - r0 + 1) : 0;
                     const int maxnr = wave_max(nr);
                     for (int rbase = 0; rbase < maxnr; rbase += RPS) {
                         const int jr = rbase + jrow;
@@ -647,8 +685,9 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                             wv = wv2;
                         }
                     }
+                    }
+                    __builtin_amdgcn_wave_barrier();
                 }
-                __builtin_amdgcn_wave_barrier();
             }
             __syncthreads();
         }
