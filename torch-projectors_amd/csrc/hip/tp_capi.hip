@@ -86,7 +86,10 @@ int64_t rec_box(int64_t n, double os) {
 }
 
 // The fp32 3D operators run the tile-owner kernels for rotation poses.
-bool use_tiles(int dim, int dtype, double os) { return dim == 3 && dtype == TP_F32 && os > 0.0 && std::isfinite(os); }
+// (Their per-wave sample queues pack a column index into 14 bits: n <= 32766.)
+bool use_tiles(int dim, int dtype, double os, int64_t n) {
+    return dim == 3 && dtype == TP_F32 && os > 0.0 && std::isfinite(os) && n <= 32766;
+}
 
 // Poses per wavefront batch: 64 lanes hold one row of the pose's samples
 // each, so a batch takes 64 / rows poses (rows bounded for a box of width w).
@@ -183,7 +186,7 @@ int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int6
     TP_TRY(need(out, "projections"));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool cubic = interp == TP_CUBIC;
-    if (use_tiles(dim, dtype, os)) {
+    if (use_tiles(dim, dtype, os, n)) {
         TP_TRY(launched(tp::launch_project3_forw_tiled(cubic, g, tile_spec(g, cubic), rec, rot, shifts, out, s),
                         "tiled projection launch"));
         return launched(tp::launch_project_forw(dim, dtype, cubic, g, rec, rot, shifts, out, s, true),
@@ -207,7 +210,7 @@ int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, in
     g.os = os;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool cubic = interp == TP_CUBIC;
-    const bool tiles = use_tiles(dim, dtype, os) && g.work > 0;
+    const bool tiles = use_tiles(dim, dtype, os, n) && g.work > 0;
     if (g.B > 0) TP_TRY(need(grec, "grad_reconstruction"));
     if (!tiles) TP_TRY(zero(grec, cx_words(dtype, g.B * g.vol), s));
     TP_TRY(zero(grot, re_words(dtype, g.B_rot * g.P * dim * dim), s));
@@ -241,7 +244,7 @@ int backproject_forw(int dim, int dtype, const void* proj, int64_t B, int64_t P,
     g.os = os;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool cubic = interp == TP_CUBIC;
-    const bool tiles = use_tiles(dim, dtype, os) && g.work > 0;
+    const bool tiles = use_tiles(dim, dtype, os, n) && g.work > 0;
     if (g.B > 0) TP_TRY(need(data, "data_reconstruction"));
     if (!tiles) {
         TP_TRY(zero(data, cx_words(dtype, g.B * g.vol), s));

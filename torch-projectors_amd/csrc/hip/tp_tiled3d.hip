@@ -170,6 +170,27 @@ __device__ __forceinline__ void rotate_slice(const float* __restrict__ R, float 
     x[2] = R[6] * sc + R[7] * sr;
 }
 
+// Per-wave sample queue.  A row block's samples are written once, in
+// flattened order, as packed (slot, c, r) entries; windows of 64 lanes then
+// read their samples straight from the queue.  Rows hold `cnt` samples from
+// column c0 at flattened index `excl`; entries [q0, q0 + QCAP) are written.
+constexpr unsigned kQRowBias = 0x8000u;  // r + bias in bits 0-15, c in bits 16-29, slot in 30-31
+__device__ __forceinline__ unsigned q_pack(int r, int c, int slot) {
+    return (unsigned(r) + kQRowBias) & 0xffffu | (unsigned(c) << 16) | (unsigned(slot) << 30);
+}
+__device__ __forceinline__ void q_unpack(unsigned e, int& r, int& c, int& slot) {
+    r = int(e & 0xffffu) - int(kQRowBias);
+    c = int((e >> 16) & 0x3fffu);
+    slot = int(e >> 30);
+}
+template <int QCAP>
+__device__ __forceinline__ void q_fill(unsigned* q, int r, int c0, int cnt, int excl, int slot, int q0) {
+    __builtin_amdgcn_wave_barrier();  // the previous entries have been read
+    const int lo = max(excl, q0), hi = min(excl + cnt, q0 + QCAP);
+    for (int e = lo; e < hi; ++e) q[e - q0] = q_pack(r, c0 + (e - excl), slot);
+    __builtin_amdgcn_wave_barrier();
+}
+
 // Per-wave copy of the poses of one batch.
 struct Slot {
     float R[9];
@@ -319,8 +340,9 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
     __shared__ Cx<float> vt[W3];
     __shared__ unsigned short plist[kChunk];
     __shared__ int pcount;
+    constexpr int QCAP = 256;
     __shared__ Slot slots[NW][KP];
-    __shared__ int marks[NW][64];
+    __shared__ unsigned queue[NW][QCAP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slot = lane / RPS, jrow = lane % RPS;
     const int nt = ts.nt;
@@ -356,7 +378,17 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
             const int np = cull_chunk<NT, false>(rotb, it.p1, pbase, lo, hi, lo, hi, plist, &pcount);
             if (np == 0) continue;
             if (!loaded) {
-                // stage the tile and its halo, STAGE loads in flight per lane
+                // stage the tile and its halo, STAGE loads in flight per lane.  When the staged
+                // box lies on one side of c = 0 and needs no clamping, a cell is a plain wrapped
+                // load (conjugated from the mirrored cell on the c < 0 side).
+                const int c_lo = tc - LO, c_hi = tc - LO + W - 1, r_lo = tr - LO, r_hi = tr - LO + W - 1,
+                          d_lo = td - LO, d_hi = td - LO + W - 1, hn = N / 2;
+                const bool plain_pos = c_lo >= 0 && c_hi <= H - 1 && r_lo >= -hn + 1 && r_hi <= hn &&
+                                       d_lo >= -hn + 1 && d_hi <= hn;
+                const bool plain_neg = c_hi < 0 && -c_lo <= H - 1 && r_lo >= -hn + 1 && r_hi <= hn - 1 &&
+                                       d_lo >= -hn + 1 && d_hi <= hn - 1;
+                const bool plain = plain_pos || plain_neg;
+                const int sg = plain_neg ? -1 : 1;
                 constexpr int STAGE = 8;
 #pragma unroll 1
                 for (int q0 = 0; q0 < LOADS; q0 += STAGE) {
@@ -366,7 +398,13 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                         const int cell = min(tid + (q0 + q) * NT, W3 - 1);
                         const int lc = cell % W, lr = (cell / W) % W, ld = cell / (W * W);
                         const int d = td - LO + ld, r = tr - LO + lr, c = tc - LO + lc;
-                        v[q] = CUBIC ? fetch3_cubic(recb, N, H, d, r, c) : fetch3(recb, N, H, d, r, c);
+                        if (plain) {
+                            const int dd = sg * d, rr = sg * r;
+                            v[q] = recb[(int64_t(dd < 0 ? dd + N : dd) * N + (rr < 0 ? rr + N : rr)) * H + sg * c];
+                            if (plain_neg) v[q].im = -v[q].im;
+                        } else {
+                            v[q] = CUBIC ? fetch3_cubic(recb, N, H, d, r, c) : fetch3(recb, N, H, d, r, c);
+                        }
                     }
 #pragma unroll
                     for (int q = 0; q < STAGE; ++q)
@@ -416,14 +454,14 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                     const int incl = dpp_scan_add(cnt);
                     const int excl = incl - cnt;
                     const int total = __builtin_amdgcn_readlane(incl, 63);
-                    int carry = 0;
-                    for (int e0 = 0; e0 < total; e0 += 64) {
-                        const int e = e0 + lane;
-                        const int lw = window_owner(cnt, excl, e0, carry, marks[wave]);
-                        const int rr = __shfl(r, lw, 64);
-                        const int cc = __shfl(c0, lw, 64) + (e - __shfl(excl, lw, 64));
-                        if (e >= total) continue;
-                        const Slot& sd = slots[wave][lw / RPS];
+                    for (int q0 = 0; q0 < total; q0 += QCAP) {
+                      q_fill<QCAP>(queue[wave], r, c0, cnt, excl, slot, q0);
+                      const int m = min(QCAP, total - q0);
+                      for (int e0 = 0; e0 < m; e0 += 64) {
+                        if (e0 + lane >= m) continue;
+                        int rr, cc, sl;
+                        q_unpack(queue[wave][e0 + lane], rr, cc, sl);
+                        const Slot& sd = slots[wave][sl];
                         const float fr = float(rr), fc = float(cc);
                         if (filtered(fr, fc, cut2)) continue;
                         float x[3];
@@ -436,6 +474,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                         if (shifts) v = cmul(v, phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k));
                         const int i = rr >= 0 ? rr : rr + g.n;
                         out[(b * g.P + sd.p) * int64_t(g.npix) + i * g.hp + cc] = v;
+                      }
                     }
                 }
                 __builtin_amdgcn_wave_barrier();
