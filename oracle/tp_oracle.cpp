@@ -538,7 +538,7 @@ void backproject_forw(const Common& cm, const Cx<T>* proj, int64_t B, int64_t P,
                 // weight lambda (cpu/2d/backprojection_2d_kernels.cpp:236-264,
                 // cpu/3d/backprojection_2d_to_3d_kernels.cpp:245-285): |tap weight|
                 // times the pixel weight, same flip (no conj) and mirror.
-                if (wb) {
+                if (wb && weights) {
                     const T w = weights[pix];
                     distribute<DIM, T>(x, cm.cubic, [&](int64_t d, int64_t rr, int64_t cc, T wd, T wr, T wc) {
                         const T fw = w * std::abs(tap_value<DIM, T>(Cx<T>{T(1.0), T(0.0)}, wd, wr, wc).re);
@@ -751,7 +751,7 @@ int tpo_backproject_2d_forw(int dtype, const void* proj, int64_t B, int64_t P, i
     const Common cm{interp == 1, os, has_cut, cut};
     DISPATCH_T(dtype, backproject_forw<2, T>(cm, (const Cx<T>*)proj, B, P, n, hp, (const T*)weights, (const T*)rot,
                                              B_rot, (const T*)shifts, B_shift, (Cx<T>*)data,
-                                             weights ? (T*)wrec : nullptr, nthreads));
+                                             (T*)wrec, nthreads));
     return 0;
 }
 
@@ -763,7 +763,7 @@ int tpo_backproject_2d_to_3d_forw(int dtype, const void* proj, int64_t B, int64_
     const Common cm{interp == 1, os, has_cut, cut};
     DISPATCH_T(dtype, backproject_forw<3, T>(cm, (const Cx<T>*)proj, B, P, n, hp, (const T*)weights, (const T*)rot,
                                              B_rot, (const T*)shifts, B_shift, (Cx<T>*)data,
-                                             weights ? (T*)wrec : nullptr, nthreads));
+                                             (T*)wrec, nthreads));
     return 0;
 }
 

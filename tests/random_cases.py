@@ -1,0 +1,49 @@
+"""Seeded random configurations across the argument space of the eight ops.
+
+Each case is a tests/golden/cases.py case dict (so `make_inputs` builds its
+tensors): odd oversampling factors including < 1, cutoffs from 0 to beyond
+the box, reconstruction boxes other than the backprojection size, batch and
+pose broadcasting, absent shifts / weights / gradient inputs, both dtypes and
+interpolations, and pose matrices that are not rotations.
+"""
+import random
+
+from tests.golden.cases import BPBACK, BPFORW, FORW, PBACK, _case
+
+OPS = FORW + PBACK + BPFORW + BPBACK
+
+
+def random_cases(count, seed, max_n=40, min_p=1):
+    rng = random.Random(seed)
+    out = []
+    for k in range(count):
+        op = OPS[k % len(OPS)]
+        n = 2 * rng.randint(1, max_n // 2)
+        os_ = rng.choice([0.5, 0.75, 1.0, 1.25, 1.5, 2.0, 2.5, 3.0])
+        cut = rng.choice([None, None, 0.0, round(rng.uniform(0.5, n), 3), 1000.0])
+        B = rng.randint(1, 3)
+        rec_n = None
+        if op in FORW + PBACK and rng.random() < 0.3:
+            rec_n = 2 * rng.randint(1, max(1, int(n * os_)))
+        c = _case(f"rand{seed}_{k}_{op}", op, dtype="f64" if rng.random() < 0.2 else "f32",
+                  interp=rng.choice(["linear", "cubic"]), os=os_, cutoff=cut, B=B,
+                  P=rng.choice([min_p, 1, 2, 5, 13]), n=n, rec_n=rec_n, shifts=rng.random() < 0.7,
+                  B_rot=rng.choice([1, B]), B_shift=rng.choice([1, B]), weights=rng.random() < 0.6,
+                  grad_weight_rec=rng.random() < 0.6, rg_rot=rng.random() < 0.6, rg_sh=rng.random() < 0.6,
+                  special=rng.random() < 0.3, seed=rng.randint(0, 2 ** 31 - 1))
+        c["scaled"] = rng.random() < 0.25  # turn every other pose matrix into a scaled one
+        out.append(c)
+    return out
+
+
+def scale_poses(args, case):
+    """Scale every other pose matrix by 1.05 (a matrix that is not a rotation)."""
+    idx = {"project_3d_to_2d_forw": 1, "project_2d_forw": 1, "project_3d_to_2d_back": 2, "project_2d_back": 2,
+           "backproject_2d_to_3d_forw": 2, "backproject_2d_forw": 2,
+           "backproject_2d_to_3d_back": 4, "backproject_2d_back": 4}[case["op"]]
+    rot = args[idx]
+    rg = rot.requires_grad
+    r = rot.detach().clone()
+    r[:, ::2] *= 1.05
+    args[idx] = r.requires_grad_(rg)
+    return args
