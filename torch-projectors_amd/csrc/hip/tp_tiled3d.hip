@@ -277,7 +277,7 @@ static_assert(kChunk <= int(kPoseMask) + 1, "pose index must fit below the flag 
 
 // Cull poses [pbase, pend) (at most kChunk) against up to two boxes with a
 // workgroup of NT lanes; returns the count.
-template <int NT, bool TWO>
+template <int NT, bool TWO, int CH = kChunk>
 __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pend, int pbase, const float* lo1,
                                           const float* hi1, const float* lo2, const float* hi2,
                                           unsigned short* plist, int* pcount) {
@@ -285,7 +285,7 @@ __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pe
     if (threadIdx.x == 0) *pcount = 0;
     __syncthreads();
 #pragma unroll 1
-    for (int q0 = 0; q0 < kChunk / NT; q0 += kCullInFlight) {
+    for (int q0 = 0; q0 < CH / NT; q0 += kCullInFlight) {
         float R[kCullInFlight][9];
 #pragma unroll
         for (int q = 0; q < kCullInFlight; ++q) {
@@ -353,7 +353,9 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
     constexpr int NT = kForwThreads, NW = NT / 64;
     constexpr int LOADS = (W3 + NT - 1) / NT;
     __shared__ Cx<float> vt[W3];
-    __shared__ unsigned short plist[kChunk];
+    constexpr int CH = 2 * kChunk;  // poses culled per phase
+    static_assert(CH <= int(kPoseMask) + 1, "pose index must fit below the flag bits");
+    __shared__ unsigned short plist[CH];
     __shared__ int pcount;
     constexpr int QCAP = 256;
     __shared__ Slot slots[NW][KP];
@@ -392,8 +394,8 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
             return vt[((d - (td - LO)) * W + (r - (tr - LO))) * W + (c - (tc - LO))];
         };
         bool loaded = false;
-        for (int pbase = it.p0; pbase < it.p1; pbase += kChunk) {
-            const int np = cull_chunk<NT, false>(rotb, it.p1, pbase, lo, hi, lo, hi, plist, &pcount);
+        for (int pbase = it.p0; pbase < it.p1; pbase += CH) {
+            const int np = cull_chunk<NT, false, CH>(rotb, it.p1, pbase, lo, hi, lo, hi, plist, &pcount);
             if (np == 0) continue;
             if (!loaded) {
                 // stage the tile and its halo, STAGE loads in flight per lane.  When the staged
