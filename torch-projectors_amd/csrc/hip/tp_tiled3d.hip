@@ -586,7 +586,7 @@ __device__ __forceinline__ void scatter_sample(const Geom& g, const Slot& sd, in
 // MODE 0: backprojection, v = proj * conj(phase(r, c)), optional weights.
 // MODE 1: reconstruction gradient of the projection, v = g * phase(-r, -c).
 template <bool CUBIC, int MODE, bool WEIGHTS, int KP>
-__global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu(3))) void k_scatter3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ src,
+__global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_scatter3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ src,
                                                            const float* __restrict__ weights,
                                                            const float* __restrict__ rot,
                                                            const float* __restrict__ shifts,
