@@ -28,7 +28,7 @@ constexpr float kRotationTol = 1e-5f;
 
 // Tile-owner enumeration parameters of the fp32 3D kernels (tp_tiled3d.hip).
 constexpr int kTileEdge = 16;                          // forward tiles: 16^3 voxels
-constexpr int kScTC = 16, kScTR = 12, kScTD = 8;        // scatter tiles (c, r, d): fp64 accumulators
+constexpr int kScTC = 16, kScTR = 8, kScTD = 12;        // scatter tiles (c, r, d): fp64 accumulators
 struct TileSpec {
     int nt, org;              // forward: tiles per axis and signed origin of the tile grid
     int fc0, fc1;             // forward core tiles (split by pose range): [fc0, fc1) on every axis
