@@ -211,19 +211,22 @@ __device__ __forceinline__ void load_pose(const float* __restrict__ rotb, const 
 }
 
 // The hardware deals workgroups to the 8 XCDs (each with its own L2) round-
-// robin by workgroup id.  Items are handed out in runs of kXcdRun neighbouring
+// robin by workgroup id.  Items are handed out in runs of RUN neighbouring
 // tiles per XCD (run k of XCD x is item run 8k + x), so an XCD's L2 shares the
 // halos and projection rows of a run while the runs stay interleaved over the
 // volume for balance.  Slots past the last item do nothing.
-constexpr int kXcds = 8, kXcdRun = 64;
+constexpr int kXcds = 8;
+template <int RUN>
 __host__ __device__ inline int64_t xcd_per(int64_t items) {
-    const int64_t span = int64_t(kXcds) * kXcdRun;
-    return (items + span - 1) / span * kXcdRun;
+    const int64_t span = int64_t(kXcds) * RUN;
+    return (items + span - 1) / span * RUN;
 }
-__device__ __forceinline__ int64_t xcd_item(int64_t slot, int64_t /*per*/) {
+template <int RUN>
+__device__ __forceinline__ int64_t xcd_item(int64_t slot) {
     const int64_t x = slot % kXcds, j = slot / kXcds;
-    return ((j / kXcdRun) * kXcds + x) * kXcdRun + j % kXcdRun;
+    return ((j / RUN) * kXcds + x) * RUN + j % RUN;
 }
+constexpr int kRunForw = 64, kRunScatter = 128;  // measured at the headline
 
 // Work items: first the core tiles, one item per (batch, tile, pose range),
 // then every tile of every batch with all poses (core tiles skipped there).
@@ -368,9 +371,9 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
     const float cut2 = float(g.cut2);
     const float rho2 = ts.rho * ts.rho;
     const int N = g.N, H = g.H;
-    const int64_t per = xcd_per(items);
+    const int64_t per = xcd_per<kRunForw>(items);
     for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
-        const int64_t w = xcd_item(slot_i, per);
+        const int64_t w = xcd_item<kRunForw>(slot_i);
         if (w >= items) continue;
         const Item it = item_of(w, g.B, int(g.P), nt, nt, nt, ts.fc0, ts.fc1, ts.fc0, ts.fc1, ts.fc0, ts.fc1,
                                 ts.ksplit, ts.prange);
@@ -607,9 +610,9 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
     const int64_t items = g.B * (int64_t(ts.sd1 - ts.sd0) * (ts.sr1 - ts.sr0) * ts.sc1 * ts.ksplit +
                                  int64_t(ts.ntd) * ts.ntr * ts.ntc);
     const float cut2 = float(g.cut2);
-    const int64_t per = xcd_per(items);
+    const int64_t per = xcd_per<kRunScatter>(items);
     for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
-        const int64_t w = xcd_item(slot_i, per);
+        const int64_t w = xcd_item<kRunScatter>(slot_i);
         if (w >= items) continue;
         const Item it = item_of(w, g.B, int(g.P), ts.ntd, ts.ntr, ts.ntc, ts.sd0, ts.sd1, ts.sr0, ts.sr1, 0, ts.sc1,
                                 ts.ksplit, ts.prange);
@@ -832,7 +835,7 @@ hipError_t forw_launch(const Geom& g, const TileSpec& ts, const void* rec, const
                        void* out, hipStream_t s) {
     const int64_t fcore = int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * ts.ksplit;
     const int64_t work = g.B * (fcore + int64_t(ts.nt) * ts.nt * ts.nt);
-    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP>), dim3(grid_for(kXcds * xcd_per(work))), dim3(kForwThreads), 0, s, g, ts,
+    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP>), dim3(grid_for(kXcds * xcd_per<kRunForw>(work))), dim3(kForwThreads), 0, s, g, ts,
                        (const Cx<float>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
     return hipGetLastError();
 }
@@ -851,7 +854,7 @@ hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, co
         if (ez != hipSuccess) return ez;
     }
     const int64_t work = g.B * (score + int64_t(ts.ntd) * ts.ntr * ts.ntc);
-    hipLaunchKernelGGL((k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP>), dim3(grid_for(kXcds * xcd_per(work))),
+    hipLaunchKernelGGL((k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP>), dim3(grid_for(kXcds * xcd_per<kRunScatter>(work))),
                        dim3(kScatterThreads), 0, s, g,
                        ts, (const Cx<float>*)src, (const float*)weights, (const float*)rot, (const float*)shifts,
                        (Cx<float>*)dst, (float*)wdst);
