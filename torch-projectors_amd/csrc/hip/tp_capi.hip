@@ -111,6 +111,9 @@ tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
     const int half_tiles = int(std::ceil((rho + 2.0) / L));
     ts.nt = 2 * half_tiles;
     ts.org = -half_tiles * L;
+    const int half_tiles_d = int(std::ceil((rho + 2.0) / tp::kTileEdgeD));
+    ts.ntfd = 2 * half_tiles_d;
+    ts.orgd = -half_tiles_d * tp::kTileEdgeD;
     const int half = g.N / 2;
     ts.ntd = (g.N + tp::kScTD - 1) / tp::kScTD;
     ts.ntr = (g.N + tp::kScTR - 1) / tp::kScTR;
@@ -122,6 +125,8 @@ tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
     const int rc = 40;
     ts.fc0 = std::max(0, (-rc - ts.org) / L);
     ts.fc1 = std::min(ts.nt, (rc - ts.org) / L + 1);
+    ts.fd0 = std::max(0, (-rc - ts.orgd) / tp::kTileEdgeD);
+    ts.fd1 = std::min(ts.ntfd, (rc - ts.orgd) / tp::kTileEdgeD + 1);
     ts.sd0 = std::max(0, (-rc + half - 1) / tp::kScTD);
     ts.sd1 = std::min(ts.ntd, (rc + half - 1) / tp::kScTD + 1);
     ts.sr0 = std::max(0, (-rc + half - 1) / tp::kScTR);
@@ -130,7 +135,7 @@ tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
     const int64_t pk = 512;  // poses per range
     ts.ksplit = int(std::max<int64_t>(1, (g.P + pk - 1) / pk));
     ts.prange = int((g.P + ts.ksplit - 1) / ts.ksplit);
-    if (ts.ksplit == 1) ts.fc1 = ts.fc0 = ts.sd1 = ts.sd0 = ts.sr1 = ts.sr0 = ts.sc1 = 0;  // nothing to split
+    if (ts.ksplit == 1) ts.fc1 = ts.fc0 = ts.fd1 = ts.fd0 = ts.sd1 = ts.sd0 = ts.sr1 = ts.sr0 = ts.sc1 = 0;  // nothing to split
     ts.rho = float(rho);
     ts.os = float(g.os);
     ts.inv_os = float(1.0 / g.os);

@@ -27,11 +27,12 @@ struct Geom {
 constexpr float kRotationTol = 1e-5f;
 
 // Tile-owner enumeration parameters of the fp32 3D kernels (tp_tiled3d.hip).
-constexpr int kTileEdge = 16;                          // forward tiles: 16^3 voxels
+constexpr int kTileEdge = 16, kTileEdgeD = 12;         // forward tiles: 16 x 16 (c, r) x 12 (d) voxels
 constexpr int kScTC = 16, kScTR = 8, kScTD = 12;        // scatter tiles (c, r, d): fp64 accumulators
 struct TileSpec {
-    int nt, org;              // forward: tiles per axis and signed origin of the tile grid
-    int fc0, fc1;             // forward core tiles (split by pose range): [fc0, fc1) on every axis
+    int nt, org;              // forward: tiles along c and r, and the signed origin of the grid there
+    int fc0, fc1;             // forward core tiles (split by pose range): [fc0, fc1) along c and r
+    int ntfd, orgd, fd0, fd1;  // forward: the same along d (tiles of kTileEdgeD)
     int ntd, ntr, ntc;        // scatter: tiles along d, r, c of the stored half volume
     int sd0, sd1, sr0, sr1, sc1;  // scatter core tiles: [sd0, sd1) x [sr0, sr1) x [0, sc1)
     int ksplit, prange;       // pose ranges per core tile, poses per range

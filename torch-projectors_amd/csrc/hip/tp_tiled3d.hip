@@ -41,7 +41,7 @@ namespace tp {
 
 namespace {
 
-constexpr int L = kTileEdge;  // forward tile edge (voxels)
+constexpr int L = kTileEdge, LD = kTileEdgeD;  // forward tile edges (voxels): c and r, d
 constexpr int SC = kScTC, SR = kScTR, SD = kScTD, S3 = SC * SR * SD;  // scatter tile
 constexpr int kForwThreads = 256;     // forward workgroup
 constexpr int kScatterThreads = 256;  // scatter workgroup
@@ -351,7 +351,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                                                         const float* __restrict__ rot,
                                                         const float* __restrict__ shifts,
                                                         Cx<float>* __restrict__ out) {
-    constexpr int LO = CUBIC ? 1 : 0, HI = CUBIC ? 2 : 1, W = L + LO + HI, W3 = W * W * W;
+    constexpr int LO = CUBIC ? 1 : 0, HI = CUBIC ? 2 : 1, W = L + LO + HI, WD = LD + LO + HI, W3 = W * W * WD;
     constexpr int RPS = 64 / KP;
     constexpr int NT = kForwThreads, NW = NT / 64;
     constexpr int LOADS = (W3 + NT - 1) / NT;
@@ -366,8 +366,8 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slot = lane / RPS, jrow = lane % RPS;
     const int nt = ts.nt;
-    const int64_t items = g.B * (int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * ts.ksplit +
-                                 int64_t(nt) * nt * nt);
+    const int64_t items = g.B * (int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fd1 - ts.fd0) * ts.ksplit +
+                                 int64_t(nt) * nt * ts.ntfd);
     const float cut2 = float(g.cut2);
     const float rho2 = ts.rho * ts.rho;
     const int N = g.N, H = g.H;
@@ -375,14 +375,14 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
     for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
         const int64_t w = xcd_item<kRunForw>(slot_i);
         if (w >= items) continue;
-        const Item it = item_of(w, g.B, int(g.P), nt, nt, nt, ts.fc0, ts.fc1, ts.fc0, ts.fc1, ts.fc0, ts.fc1,
+        const Item it = item_of(w, g.B, int(g.P), ts.ntfd, nt, nt, ts.fd0, ts.fd1, ts.fc0, ts.fc1, ts.fc0, ts.fc1,
                                 ts.ksplit, ts.prange);
         if (it.skip) continue;
         const int64_t b = it.b;
-        const int tc = ts.org + it.kc * L, tr = ts.org + it.kr * L, td = ts.org + it.kd * L;
-        // samples owned by this tile: floor(x) in [t, t + L) on every axis (+ slack)
+        const int tc = ts.org + it.kc * L, tr = ts.org + it.kr * L, td = ts.orgd + it.kd * LD;
+        // samples owned by this tile: floor(x) in [t, t + edge) on every axis (+ slack)
         const float lo[3] = {float(tc) - ts.eps, float(tr) - ts.eps, float(td) - ts.eps};
-        const float hi[3] = {float(tc + L) + ts.eps, float(tr + L) + ts.eps, float(td + L) + ts.eps};
+        const float hi[3] = {float(tc + L) + ts.eps, float(tr + L) + ts.eps, float(td + LD) + ts.eps};
         float dist2 = 0.f;
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
@@ -405,7 +405,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                 // box lies on one side of c = 0 and needs no clamping, a cell is a plain wrapped
                 // load (conjugated from the mirrored cell on the c < 0 side).
                 const int c_lo = tc - LO, c_hi = tc - LO + W - 1, r_lo = tr - LO, r_hi = tr - LO + W - 1,
-                          d_lo = td - LO, d_hi = td - LO + W - 1, hn = N / 2;
+                          d_lo = td - LO, d_hi = td - LO + WD - 1, hn = N / 2;
                 const bool plain_pos = c_lo >= 0 && c_hi <= H - 1 && r_lo >= -hn + 1 && r_hi <= hn &&
                                        d_lo >= -hn + 1 && d_hi <= hn;
                 const bool plain_neg = c_hi < 0 && -c_lo <= H - 1 && r_lo >= -hn + 1 && r_hi <= hn - 1 &&
@@ -490,7 +490,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                         float x[3];
                         rotate_slice(sd.R, fr, fc, g.os, x);
                         const int fxc = int(floorf(x[0])), fxr = int(floorf(x[1])), fxd = int(floorf(x[2]));
-                        if (fxc < tc || fxc >= tc + L || fxr < tr || fxr >= tr + L || fxd < td || fxd >= td + L)
+                        if (fxc < tc || fxc >= tc + L || fxr < tr || fxr >= tr + L || fxd < td || fxd >= td + LD)
                             continue;
                         Cx<float> v = CUBIC ? cubic3<float, false, false>(lds, x[2], x[1], x[0]).v
                                             : lerp3<float, false, false>(lds, x[2], x[1], x[0]).v;
@@ -833,8 +833,8 @@ __global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<fl
 template <bool CUBIC, int KP>
 hipError_t forw_launch(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts,
                        void* out, hipStream_t s) {
-    const int64_t fcore = int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * ts.ksplit;
-    const int64_t work = g.B * (fcore + int64_t(ts.nt) * ts.nt * ts.nt);
+    const int64_t fcore = int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fd1 - ts.fd0) * ts.ksplit;
+    const int64_t work = g.B * (fcore + int64_t(ts.nt) * ts.nt * ts.ntfd);
     hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP>), dim3(grid_for(kXcds * xcd_per<kRunForw>(work))), dim3(kForwThreads), 0, s, g, ts,
                        (const Cx<float>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
     return hipGetLastError();
