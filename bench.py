@@ -13,7 +13,8 @@ the kernels run on), and the reference CPU path timed on a bounded sample of
 the same inputs on the host cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--no-cpu]
-Configs: headline (default), c1..c5.
+Configs: headline (default, the bench line), c2..c5 (the other BASELINE.json configurations,
+for per-op timings; no CPU baseline or traffic figure for them).
 """
 import argparse
 import json
@@ -189,7 +190,118 @@ def make_headline(dev, k=0):
     return Workload("headline", cfg["workload"], ops, cpu_sample, cfg)
 
 
-WORKLOADS = {"headline": make_headline}
+def make_c2(dev):
+    """c2: 3D linear forward, 256^3-padded blob volume, 4096 poses of 128 x 65."""
+    import torch
+    T = torch.ops.torch_projectors
+    gen = torch.Generator().manual_seed(20261201 + 2)
+    P, n, os_ = 4096, 128, 2.0
+    vol = blob_volume_rfft(128, 256, 32, 40.0, gen, dev)
+    rot = quat_rotations(P, gen)[None].to(dev)
+    sh = ((torch.rand(1, P, 2, generator=gen) * 10) - 5).to(dev)
+
+    def fwd():
+        T.project_3d_to_2d_forw(vol, rot, sh, [n, n], "linear", os_, None)
+
+    samples = P * n * (n // 2 + 1)
+    cfg = {"workload": "c2: project_3d_to_2d_forw, linear", "volume": [1, 256, 256, 129], "poses": P,
+           "proj": [n, n // 2 + 1], "oversampling": os_}
+    return Workload("c2", cfg["workload"], [("project_3d_to_2d_forw", fwd, bytes_forward(P, n, 3, "linear"),
+                                             samples, P)], None, cfg)
+
+
+def make_c3(dev):
+    """c3: 3D linear backprojection with weights, 8192 poses of 128 x 65 into 256^3."""
+    import torch
+    T = torch.ops.torch_projectors
+    gen = torch.Generator().manual_seed(20261201 + 3)
+    P, n, os_ = 8192, 128, 2.0
+    proj = torch.randn(1, P, n, n // 2 + 1, generator=gen, dtype=torch.complex64).to(dev)
+    w = ctf2_weights(1, P, n, gen).float().to(dev)
+    rot = quat_rotations(P, gen)[None].to(dev)
+    sh = ((torch.rand(1, P, 2, generator=gen) * 10) - 5).to(dev)
+
+    def bp():
+        T.backproject_2d_to_3d_forw(proj, w, rot, sh, "linear", os_, None)
+
+    samples = P * n * (n // 2 + 1)
+    cfg = {"workload": "c3: backproject_2d_to_3d_forw (weights), linear", "volume": [1, 256, 256, 129],
+           "poses": P, "proj": [n, n // 2 + 1], "oversampling": os_}
+    return Workload("c3", cfg["workload"],
+                    [("backproject_2d_to_3d_forw", bp, bytes_backproject(P, n, 3, "linear", 256 * 256 * 129, True),
+                      samples, P)], None, cfg)
+
+
+def make_c4(dev):
+    """c4: 3D cubic forward and its backward (volume, rotation and shift gradients)."""
+    import torch
+    T = torch.ops.torch_projectors
+    gen = torch.Generator().manual_seed(20261201 + 4)
+    P, n, os_ = 2048, 256, 2.0
+    vol = blob_volume_rfft(256, 512, 32, 80.0, gen, dev)
+    rot = quat_rotations(P, gen)[None].to(dev).requires_grad_(True)
+    sh = ((torch.rand(1, P, 2, generator=gen) * 16) - 8).to(dev).requires_grad_(True)
+    g = torch.randn(1, P, n, n // 2 + 1, generator=gen, dtype=torch.complex64).to(dev)
+
+    def fwd():
+        T.project_3d_to_2d_forw(vol, rot.detach(), sh.detach(), [n, n], "cubic", os_, None)
+
+    def back():
+        T.project_3d_to_2d_back(g, vol, rot, sh, "cubic", os_, None)
+
+    V = 512 * 512 * 257
+    samples = P * n * (n // 2 + 1)
+    cfg = {"workload": "c4: project_3d_to_2d_forw + project_3d_to_2d_back (rotation/shift grads), cubic",
+           "volume": [1, 512, 512, 257], "poses": P, "proj": [n, n // 2 + 1], "oversampling": os_}
+    return Workload("c4", cfg["workload"],
+                    [("project_3d_to_2d_forw", fwd, bytes_forward(P, n, 3, "cubic"), samples, P),
+                     ("project_3d_to_2d_back", back, bytes_project_back(P, n, 3, "cubic", V), samples, P)],
+                    None, cfg)
+
+
+def make_c5(dev):
+    """c5: batched 2D cubic, 16 images x 4096 poses: forward, backprojection and both backward ops."""
+    import torch
+    T = torch.ops.torch_projectors
+    gen = torch.Generator().manual_seed(20261201 + 5)
+    B, P, n, os_, cut = 16, 4096, 256, 2.0, 64.0
+    rec = noise_image_rfft(B, 256, 512, gen, dev).to(torch.complex64)
+    rot = angle_rotations((B, P), gen).to(dev)
+    sh = (3 * torch.randn(B, P, 2, generator=gen)).to(dev)
+    rot_g, sh_g = rot.clone().requires_grad_(True), sh.clone().requires_grad_(True)
+    st = {"proj": T.project_2d_forw(rec, rot, sh, [n, n], "cubic", os_, cut)}
+    ones = torch.ones(B, P, n, n // 2 + 1, device=dev)
+    gd = torch.randn(B, 512, 257, generator=gen, dtype=torch.complex64).to(dev)
+    gw = torch.randn(B, 512, 257, generator=gen).to(dev)
+
+    def fwd():
+        st["proj"] = T.project_2d_forw(rec, rot, sh, [n, n], "cubic", os_, cut)
+
+    def bp():
+        T.backproject_2d_forw(st["proj"], ones, rot, sh, "cubic", os_, cut)
+
+    def bp_back():
+        st["gproj"] = T.backproject_2d_back(gd, gw, st["proj"], ones, rot_g, sh_g, "cubic", os_, cut)[0]
+
+    def p_back():
+        T.project_2d_back(st["gproj"], rec, rot_g, sh_g, "cubic", os_, cut)
+
+    samples = B * P * n * (n // 2 + 1)
+    V = B * 512 * 257
+    cfg = {"workload": "c5: batched 2D cubic forward, backprojection (unit weights), both backward ops",
+           "reconstruction": [B, 512, 257], "poses": P, "proj": [n, n // 2 + 1], "oversampling": os_, "cutoff": cut}
+    return Workload("c5", cfg["workload"],
+                    [("project_2d_forw", fwd, bytes_forward(B * P, n, 2, "cubic", cut), samples, B * P),
+                     ("backproject_2d_forw", bp, bytes_backproject(B * P, n, 2, "cubic", V, True, cut), samples,
+                      B * P),
+                     ("backproject_2d_back", bp_back, bytes_backproject_back(B * P, n, 2, "cubic", True, cut),
+                      samples, B * P),
+                     ("project_2d_back", p_back, bytes_project_back(B * P, n, 2, "cubic", V, cut), samples,
+                      B * P)], None, cfg)
+
+
+# headline is the bench line; c2-c5 are the other BASELINE configurations, run on request
+WORKLOADS = {"headline": make_headline, "c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5}
 
 
 # ----------------------------------------------------------------------------- CPU baseline
@@ -255,6 +367,7 @@ def main():
         sys.exit(2)
 
     import torch
+    import torch_projectors  # noqa: F401  (registers torch.ops.torch_projectors; fails without the HIP library)
     dev = torch.device("cuda:0")
     if a.copy_probe:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
