@@ -70,28 +70,29 @@ __global__ __launch_bounds__(kBlock) void k_backproject_forw(Geom g, const Cx<T>
     }
 }
 
-// The poses of an fp32 3D backprojection that are not rotations (the tiled
+// The poses of an fp32 backprojection that are not rotations (the tiled
 // scatter has accumulated the others).  One block per pose.
-template <bool CUBIC, bool WEIGHTS>
-__global__ __launch_bounds__(kBlock) void k_backproject3_forw_rest(Geom g, const Cx<float>* __restrict__ proj,
-                                                                   const float* __restrict__ weights,
-                                                                   const float* __restrict__ rot,
-                                                                   const float* __restrict__ shifts,
-                                                                   Cx<float>* __restrict__ data,
-                                                                   float* __restrict__ wrec) {
+template <int DIM, bool CUBIC, bool WEIGHTS>
+__global__ __launch_bounds__(kBlock) void k_backproject_forw_rest(Geom g, const Cx<float>* __restrict__ proj,
+                                                                  const float* __restrict__ weights,
+                                                                  const float* __restrict__ rot,
+                                                                  const float* __restrict__ shifts,
+                                                                  Cx<float>* __restrict__ data,
+                                                                  float* __restrict__ wrec) {
+    constexpr int RS = DIM * DIM;
     const float cut2 = float(g.cut2);
     for (int64_t bp = blockIdx.x; bp < g.B * g.P; bp += gridDim.x) {
         const int64_t b = bp / g.P, p = bp - b * g.P;
-        const float* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * 9;
-        if (pose_is_rotation(R)) continue;
+        const float* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * RS;
+        if (pose_is_rotation_d<DIM>(R)) continue;
         const float* S = shifts ? shifts + ((g.B_shift == 1 ? 0 : b) * g.P + p) * 2 : nullptr;
         for (int pix = threadIdx.x; pix < g.npix; pix += kBlock) {
             const int i = pix / g.hp, j = pix - i * g.hp;
             const float r = freq_of<float>(i, g.n), c = float(j);
             if (filtered(r, c, cut2) || (j == 0 && i >= g.n / 2)) continue;
             const int64_t pidx = bp * g.npix + pix;
-            backproject_pixel<3, float, CUBIC, WEIGHTS>(g, proj[pidx], WEIGHTS ? weights[pidx] : 0.f, R, S, r, c,
-                                                        data + b * g.vol, WEIGHTS ? wrec + b * g.vol : nullptr);
+            backproject_pixel<DIM, float, CUBIC, WEIGHTS>(g, proj[pidx], WEIGHTS ? weights[pidx] : 0.f, R, S, r, c,
+                                                          data + b * g.vol, WEIGHTS ? wrec + b * g.vol : nullptr);
         }
     }
 }
@@ -183,16 +184,16 @@ hipError_t forw(const Geom& g, const void* proj, const void* weights, const void
     return hipGetLastError();
 }
 
-template <bool CUBIC>
+template <int DIM, bool CUBIC>
 hipError_t forw_rest(const Geom& g, const void* proj, const void* weights, const void* rot, const void* shifts,
                      void* data, void* wrec, hipStream_t s) {
     const unsigned grid = grid_for(g.B * g.P);
     if (weights)
-        hipLaunchKernelGGL((k_backproject3_forw_rest<CUBIC, true>), dim3(grid), dim3(kBlock), 0, s, g,
+        hipLaunchKernelGGL((k_backproject_forw_rest<DIM, CUBIC, true>), dim3(grid), dim3(kBlock), 0, s, g,
                            (const Cx<float>*)proj, (const float*)weights, (const float*)rot, (const float*)shifts,
                            (Cx<float>*)data, (float*)wrec);
     else
-        hipLaunchKernelGGL((k_backproject3_forw_rest<CUBIC, false>), dim3(grid), dim3(kBlock), 0, s, g,
+        hipLaunchKernelGGL((k_backproject_forw_rest<DIM, CUBIC, false>), dim3(grid), dim3(kBlock), 0, s, g,
                            (const Cx<float>*)proj, (const float*)nullptr, (const float*)rot, (const float*)shifts,
                            (Cx<float>*)data, (float*)nullptr);
     return hipGetLastError();
@@ -268,9 +269,13 @@ hipError_t launch_zero(void* p, int64_t words, hipStream_t s) {
 hipError_t launch_backproject_forw(int dim, int dt, bool cubic, const Geom& g, const void* proj, const void* weights,
                                    const void* rot, const void* shifts, void* data, void* wrec, hipStream_t s,
                                    bool rest_only) {
-    if (rest_only && dim == 3 && dt == 0)
-        return cubic ? forw_rest<true>(g, proj, weights, rot, shifts, data, wrec, s)
-                     : forw_rest<false>(g, proj, weights, rot, shifts, data, wrec, s);
+    if (rest_only && dt == 0) {
+        if (dim == 2)
+            return cubic ? forw_rest<2, true>(g, proj, weights, rot, shifts, data, wrec, s)
+                         : forw_rest<2, false>(g, proj, weights, rot, shifts, data, wrec, s);
+        return cubic ? forw_rest<3, true>(g, proj, weights, rot, shifts, data, wrec, s)
+                     : forw_rest<3, false>(g, proj, weights, rot, shifts, data, wrec, s);
+    }
     TP_DISPATCH(dim, dt, cubic, forw, g, proj, weights, rot, shifts, data, wrec, s);
 }
 

@@ -153,6 +153,49 @@ tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
     return ts;
 }
 
+// fp32 2D scatters take the tile-owner kernel (tp_tiled2d.hip) for rotation poses.
+bool use_tiles2(int dim, int dtype, double os, int64_t n) {
+    return dim == 2 && dtype == TP_F32 && os > 0.0 && std::isfinite(os) && n <= 32766;
+}
+
+tp::TileSpec2 tile_spec2(const tp::Geom& g, bool cubic) {
+    constexpr int TC = tp::kTile2C, TR = tp::kTile2R;
+    tp::TileSpec2 ts{};
+    const double grid_r = std::sqrt(2.0) * double(g.n / 2 + 1);
+    double cutr = g.cut2 >= 0.0 ? std::sqrt(g.cut2) : grid_r;
+    if (!std::isfinite(cutr) || cutr > grid_r) cutr = grid_r;
+    const double rho = g.os * cutr * 1.001 + 1.0;
+    // tiles whose cells a tap can reach: |r| and c within rho plus the stencil
+    const double reach = std::min(rho + 3.0, double(g.N));
+    const int half = g.N / 2;
+    const int ntr = (g.N + TR - 1) / TR, ntc = (g.H + TC - 1) / TC;
+    ts.kr0 = std::max(0, int(std::floor((-reach + half - 1) / TR)));
+    const int kr1 = std::min(ntr, int(std::floor((reach + half - 1) / TR)) + 1);
+    ts.nr = std::max(0, kr1 - ts.kr0);
+    ts.nc = std::min(ntc, int(std::floor(reach / TC)) + 1);
+    // Every pose reaches every tile of the disc: split the poses into ranges
+    // until there are a few thousand work items, keeping >= 128 poses a range.
+    const int64_t tiles = g.B * int64_t(ts.nr) * ts.nc;
+    const int64_t want = tiles > 0 ? (4096 + tiles - 1) / tiles : 1;
+    const int64_t most = std::max<int64_t>(1, g.P / 128);
+    ts.ksplit = int(std::max<int64_t>(1, std::min(want, most)));
+    ts.prange = int((g.P + ts.ksplit - 1) / ts.ksplit);
+    ts.rho = float(rho);
+    ts.os = float(g.os);
+    ts.inv_os = float(1.0 / g.os);
+    ts.smax = float(g.os * (g.n + 2));
+    ts.eps = 0.01f + 2.0f * tp::kRotationTol * ts.smax;
+    // rows of a pose's samples in one box: at most its diagonal over os, plus the ends
+    const double wc = TC + (cubic ? 3 : 1) + 2.0 * ts.eps, wr = TR + (cubic ? 3 : 1) + 2.0 * ts.eps;
+    const int rows = int(std::ceil(std::sqrt(wc * wc + wr * wr) / g.os)) + 2;
+    ts.kp = rows <= 16 ? 4 : (rows <= 32 ? 2 : 1);
+    const int cl = int(std::floor(cutr)) + 1;
+    ts.cmax = std::min(g.n / 2, cl);
+    ts.rmin = std::max(g.n / 2 + 1 - g.n, -cl);
+    ts.rmax = std::min(g.n / 2, cl);
+    return ts;
+}
+
 int64_t cx_words(int dtype, int64_t elems) { return elems * (dtype == TP_F32 ? 2 : 4); }
 int64_t re_words(int dtype, int64_t elems) { return elems * (dtype == TP_F32 ? 1 : 2); }
 
@@ -216,6 +259,7 @@ int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, in
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool cubic = interp == TP_CUBIC;
     const bool tiles = use_tiles(dim, dtype, os, n) && g.work > 0;
+    const bool tiles2 = use_tiles2(dim, dtype, os, n) && g.work > 0;
     if (g.B > 0) TP_TRY(need(grec, "grad_reconstruction"));
     if (!tiles) TP_TRY(zero(grec, cx_words(dtype, g.B * g.vol), s));
     TP_TRY(zero(grot, re_words(dtype, g.B_rot * g.P * dim * dim), s));
@@ -228,8 +272,12 @@ int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, in
         TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 1, g, tile_spec(g, cubic), gproj, nullptr, rot, shifts, grec,
                                                   nullptr, s),
                         "tiled reconstruction-gradient launch"));
+    if (tiles2)
+        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 1, g, tile_spec2(g, cubic), gproj, nullptr, rot, shifts,
+                                                  grec, nullptr, s),
+                        "tiled reconstruction-gradient launch"));
     return launched(tp::launch_project_back(dim, dtype, cubic, g, gproj, rec, rot, shifts, grec, grot, gshift, s,
-                                            tiles),
+                                            tiles || tiles2),
                     "projection backward launch");
 }
 
@@ -250,6 +298,7 @@ int backproject_forw(int dim, int dtype, const void* proj, int64_t B, int64_t P,
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool cubic = interp == TP_CUBIC;
     const bool tiles = use_tiles(dim, dtype, os, n) && g.work > 0;
+    const bool tiles2 = use_tiles2(dim, dtype, os, n) && g.work > 0;
     if (g.B > 0) TP_TRY(need(data, "data_reconstruction"));
     if (!tiles) {
         TP_TRY(zero(data, cx_words(dtype, g.B * g.vol), s));
@@ -262,8 +311,12 @@ int backproject_forw(int dim, int dtype, const void* proj, int64_t B, int64_t P,
         TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 0, g, tile_spec(g, cubic), proj, weights, rot, shifts, data, wrec,
                                                   s),
                         "tiled backprojection launch"));
+    if (tiles2)
+        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 0, g, tile_spec2(g, cubic), proj, weights, rot, shifts, data,
+                                                  wrec, s),
+                        "tiled backprojection launch"));
     return launched(
-        tp::launch_backproject_forw(dim, dtype, cubic, g, proj, weights, rot, shifts, data, wrec, s, tiles),
+        tp::launch_backproject_forw(dim, dtype, cubic, g, proj, weights, rot, shifts, data, wrec, s, tiles || tiles2),
         "backprojection launch");
 }
 

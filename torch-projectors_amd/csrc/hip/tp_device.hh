@@ -482,6 +482,18 @@ __device__ __forceinline__ bool pose_is_rotation(const float* __restrict__ R) {
     return fabsf(aa - 1.0f) <= kRotationTol && fabsf(bb - 1.0f) <= kRotationTol && fabsf(ab) <= kRotationTol;
 }
 
+// The same for a 2D pose matrix (row-major 2x2, columns (R[0], R[2]) and (R[1], R[3])).
+__device__ __forceinline__ bool pose_is_rotation2(const float* __restrict__ R) {
+    const float aa = R[0] * R[0] + R[2] * R[2];
+    const float bb = R[1] * R[1] + R[3] * R[3];
+    const float ab = R[0] * R[1] + R[2] * R[3];
+    return fabsf(aa - 1.0f) <= kRotationTol && fabsf(bb - 1.0f) <= kRotationTol && fabsf(ab) <= kRotationTol;
+}
+template <int DIM> __device__ __forceinline__ bool pose_is_rotation_d(const float* __restrict__ R) {
+    if constexpr (DIM == 2) return pose_is_rotation2(R);
+    else return pose_is_rotation(R);
+}
+
 // ---------------------------------------------------------------- atomics
 __device__ __forceinline__ void atomic_add(float* p, float v) { unsafeAtomicAdd(p, v); }
 __device__ __forceinline__ void atomic_add(double* p, double v) { unsafeAtomicAdd(p, v); }

@@ -44,6 +44,19 @@ struct TileSpec {
     int kp_forw, kp_scatter;  // poses per wavefront batch (1, 2 or 4)
 };
 
+// Tile-owner scatter of the fp32 2D operators (tp_tiled2d.hip).
+constexpr int kTile2C = 32, kTile2R = 16;  // tile edges (c, r): fp64 accumulators
+struct TileSpec2 {
+    int kr0, nr, nc;        // tiles that samples can reach: rows [kr0, kr0 + nr), columns [0, nc)
+    int ksplit, prange;     // pose ranges per tile, poses per range
+    int kp;                 // poses per wavefront batch (1, 2 or 4)
+    float rho;              // bound on |x| of every active sample of a rotation pose
+    float eps;              // slack (cells) added to every enumeration box
+    float os, inv_os;       // oversampling and its inverse
+    float smax;             // bound on |c*os| over the pixel grid
+    int cmax, rmin, rmax;   // pixel-grid limits of c and r (grid and cutoff)
+};
+
 constexpr int kBlock = 256;
 constexpr int64_t kMaxGrid = int64_t(1) << 22;
 
@@ -56,12 +69,12 @@ hipError_t launch_zero(void* p, int64_t words, hipStream_t s);
 // `rest_only` (fp32 3D): only masked pixels and poses that are not rotations.
 hipError_t launch_project_forw(int dim, int dt, bool cubic, const Geom& g, const void* rec, const void* rot,
                                const void* shifts, void* out, hipStream_t s, bool rest_only = false);
-// `rest_only` (fp32 3D): the reconstruction-gradient scatter only for poses
+// `rest_only` (fp32 2D and 3D): the reconstruction-gradient scatter only for poses
 // that are not rotations; rotation/shift gradients for all poses.
 hipError_t launch_project_back(int dim, int dt, bool cubic, const Geom& g, const void* gproj, const void* rec,
                                const void* rot, const void* shifts, void* grec, void* grot, void* gshift,
                                hipStream_t s, bool rest_only = false);
-// `rest_only` (fp32 3D): only poses that are not rotations.
+// `rest_only` (fp32 2D and 3D): only poses that are not rotations.
 hipError_t launch_backproject_forw(int dim, int dt, bool cubic, const Geom& g, const void* proj, const void* weights,
                                    const void* rot, const void* shifts, void* data, void* wrec, hipStream_t s,
                                    bool rest_only = false);
@@ -72,6 +85,13 @@ hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec&
 // mode 0: backprojection into data (+ weights), with the x = 0 Hermitian completion;
 // mode 1: reconstruction gradient of the projection.
 hipError_t launch_scatter3_tiled(bool cubic, int mode, const Geom& g, const TileSpec& ts, const void* src,
+                                 const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
+                                 hipStream_t s);
+
+// fp32 2D tile-owner scatter (rotation poses only), into zero-filled dst / wdst.
+// mode 0: backprojection with the x = 0 Hermitian completion; mode 1:
+// reconstruction gradient of the projection.
+hipError_t launch_scatter2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* src,
                                  const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
                                  hipStream_t s);
 

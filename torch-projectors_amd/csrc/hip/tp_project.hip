@@ -88,8 +88,8 @@ __global__ __launch_bounds__(kBlock) void k_project3_forw_rest(Geom g, const Cx<
 // with out-of-range taps dropped and no x = 0 mirror
 // (projection_utils.h:336-362, 414-443).  Rotation and shift gradients are
 // per-pose sums, reduced across the block before one atomic per component.
-// REST (fp32 3D): the reconstruction gradient of rotation poses comes from
-// the tiled scatter; only the other poses are scattered here.
+// REST (fp32): the reconstruction gradient of rotation poses comes from the
+// tiled scatter; only the other poses are scattered here.
 template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT, bool REST>
 __global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __restrict__ gproj,
                                                          const Cx<T>* __restrict__ rec, const T* __restrict__ rot,
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
         bool scatter = true;
         if constexpr (REST) {
-            scatter = !pose_is_rotation(rot + (rb * g.P + p) * RS);
+            scatter = !pose_is_rotation_d<DIM>(rot + (rb * g.P + p) * RS);
             if (!scatter && !ROT && !SHIFT) continue;  // block-uniform
         }
         T acc[K];
@@ -221,9 +221,13 @@ hipError_t launch_project_forw(int dim, int dt, bool cubic, const Geom& g, const
 hipError_t launch_project_back(int dim, int dt, bool cubic, const Geom& g, const void* gproj, const void* rec,
                                const void* rot, const void* shifts, void* grec, void* grot, void* gshift,
                                hipStream_t s, bool rest_only) {
-    if (rest_only && dim == 3 && dt == 0)
+    if (rest_only && dt == 0) {
+        if (dim == 2)
+            return cubic ? back<2, float, true, true>(g, gproj, rec, rot, shifts, grec, grot, gshift, s)
+                         : back<2, float, false, true>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
         return cubic ? back<3, float, true, true>(g, gproj, rec, rot, shifts, grec, grot, gshift, s)
                      : back<3, float, false, true>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+    }
     TP_DISPATCH(dim, dt, cubic, back, g, gproj, rec, rot, shifts, grec, grot, gshift, s);
 }
 

@@ -1,0 +1,467 @@
+// Tile-owner scatter for the 2D operators (fp32): backproject_2d_forw and the
+// reconstruction gradient of project_2d_back.
+//
+// The reference spreads each projection pixel's stencil straight into the
+// image (cpu/2d/backprojection_2d_kernels.cpp:99-282 with
+// projection_utils.h:371-406, 451-493; cpu/2d/projection_2d_kernels.cpp:300-322
+// with projection_utils.h:336-362).  A 2D pose covers the whole frequency
+// disc, so every cell of an image receives taps from every pose: one float
+// atomic per tap into HBM serialises on the same few thousand cells.
+//
+// Here a workgroup owns a TC x TR tile of the stored half plane, accumulated
+// in fp64 LDS, for one range of poses.  Per phase of kChunk2 poses it culls
+// the rotations whose sample half-disc reaches the tile (box 1: direct taps,
+// c >= 0) or its negation (box 2: taps with c < 0, which the reference
+// flips to (-c, -r) and conjugates), then enumerates exactly the samples of
+// each such pose whose stencil reaches the box: one lane per (pose, row)
+// computes the row's column interval, a wave prefix sum packs the samples of
+// KP poses densely onto the lanes.  Partial tiles of the pose ranges are
+// added into the zero-filled image with float atomics (once per cell and
+// range).  The x = 0 Hermitian completion of the backprojection is applied
+// afterwards by k_mirror2_x0.
+//
+// Only poses whose matrix is orthonormal (pose_is_rotation2) take this path;
+// the per-pixel kernels scatter the others.
+#include "tp_device.hh"
+#include "tp_launch.hh"
+#include "tp_tiled_common.hh"
+
+namespace tp {
+
+namespace {
+
+constexpr int TC = kTile2C, TR = kTile2R, T2 = TC * TR;  // tile edges (cells): c, r
+constexpr int kThreads = 256;
+constexpr int kRun = 128;         // XCD run length (items)
+constexpr int kChunk2 = 512;      // poses culled per phase
+constexpr int kInFlight = 2;      // rotations loaded together per lane in the cull
+static_assert((TC & (TC - 1)) == 0, "tile width must be a power of two");
+static_assert(kChunk2 <= 65535, "pose index must fit the list entries");
+
+// Sample position of pixel (r, c), as rotate<2>: x = R (sc, sr).
+__device__ __forceinline__ void rotate_pix(const float* __restrict__ R, float r, float c, double os, float* x) {
+    const float sc = float(double(c) * os), sr = float(double(r) * os);
+    x[0] = R[0] * sc + R[1] * sr;
+    x[1] = R[2] * sc + R[3] * sr;
+}
+
+// Samples have sc >= 0, i.e. x . a >= 0 for a = (R[0], R[2]): does the box
+// reach that half plane?
+__device__ __forceinline__ bool half_plane_hits2(const float* R, const float* lo, const float* hi) {
+    const float a0 = R[0], a1 = R[2];
+    const float u = (a0 >= 0.f ? a0 * hi[0] : a0 * lo[0]) + (a1 >= 0.f ? a1 * hi[1] : a1 * lo[1]);
+    return u >= 0.f;
+}
+
+// Rows r (sr = r*os = x . b, b = (R[1], R[3])) whose samples can lie in the box.
+__device__ __forceinline__ void box_rows2(const float* R, const float* lo, const float* hi, const TileSpec2& ts,
+                                          int& r0, int& r1) {
+    float vlo = 0.f, vhi = 0.f;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const float b = R[2 * k + 1];
+        vlo += b >= 0.f ? b * lo[k] : b * hi[k];
+        vhi += b >= 0.f ? b * hi[k] : b * lo[k];
+    }
+    r0 = max(ts.rmin, to_int_clamped(ceilf(vlo * ts.inv_os)));
+    r1 = min(ts.rmax, to_int_clamped(floorf(vhi * ts.inv_os)));
+}
+
+// Columns c of row r whose sample lies in the box (which carries the slack
+// covering rounding), within the pixel grid and (up to one column) the cutoff.
+__device__ __forceinline__ void row_span2(const float* R, int r, const float* lo, const float* hi,
+                                          const TileSpec2& ts, float cut2, int& c0, int& c1) {
+    const float ros = float(r) * ts.os;
+    float l = -3.0e38f, h = 3.0e38f;
+    bool empty = false;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const float a = R[2 * k], base = ros * R[2 * k + 1];
+        const float lk = lo[k] - base, hk = hi[k] - base;  // need a*sc in [lk, hk]
+        if (fabsf(a) > 1e-6f) {
+            const float ia = __builtin_amdgcn_rcpf(a);
+            const float u0 = lk * ia, u1 = hk * ia;
+            l = fmaxf(l, a > 0.f ? u0 : u1);
+            h = fminf(h, a > 0.f ? u1 : u0);
+        } else {
+            const float tol = fabsf(a) * ts.smax;
+            empty |= lk > tol || hk < -tol;
+        }
+    }
+    c0 = max(0, to_int_clamped(ceilf(l * ts.inv_os - 1e-3f)));
+    c1 = min(ts.cmax, to_int_clamped(floorf(h * ts.inv_os + 1e-3f)));
+    const float rem = cut2 - float(r) * float(r);
+    if (empty || rem < 0.f) c1 = -1;
+    else c1 = min(c1, int(sqrtf(rem)) + 1);
+}
+
+// Per-wave copy of the poses of one batch.
+struct Slot2 {
+    float R[4];
+    float s0, s1;
+    int p;
+};
+
+__device__ __forceinline__ void load_pose2(const float* __restrict__ rotb, const float* __restrict__ shb, int p,
+                                           float* R, float* S) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) R[e] = rotb[int64_t(p) * 4 + e];
+    S[0] = shb ? shb[2 * int64_t(p)] : 0.f;
+    S[1] = shb ? shb[2 * int64_t(p) + 1] : 0.f;
+}
+
+// Cull poses [pbase, pend) (at most kChunk2) against box 1 and box 2.  Box-1
+// survivors fill plist from the front, box-2 survivors from the back.
+__device__ __forceinline__ void cull2(const float* __restrict__ rotb, int pend, int pbase, const float* lo1,
+                                      const float* hi1, const float* lo2, const float* hi2, unsigned short* plist,
+                                      int* pcnt, int& n1, int& n2) {
+    static_assert(kChunk2 % kThreads == 0 && (kChunk2 / kThreads) % kInFlight == 0, "cull shape");
+    __syncthreads();  // every lane has read the previous counts and lists
+    if (threadIdx.x == 0) pcnt[0] = pcnt[1] = 0;
+    __syncthreads();
+#pragma unroll 1
+    for (int q0 = 0; q0 < kChunk2 / kThreads; q0 += kInFlight) {
+        float R[kInFlight][4];
+#pragma unroll
+        for (int q = 0; q < kInFlight; ++q) {
+            const int p = min(pbase + int(threadIdx.x) + (q0 + q) * kThreads, pend - 1);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) R[q][e] = rotb[int64_t(p) * 4 + e];
+        }
+#pragma unroll
+        for (int q = 0; q < kInFlight; ++q) {
+            const int p = pbase + int(threadIdx.x) + (q0 + q) * kThreads;
+            if (p >= pend || !pose_is_rotation2(R[q])) continue;
+            if (half_plane_hits2(R[q], lo1, hi1)) plist[atomicAdd(&pcnt[0], 1)] = (unsigned short)(p - pbase);
+            if (half_plane_hits2(R[q], lo2, hi2))
+                plist[2 * kChunk2 - 1 - atomicAdd(&pcnt[1], 1)] = (unsigned short)(p - pbase);
+        }
+    }
+    __syncthreads();
+    n1 = pcnt[0];
+    n2 = pcnt[1];
+}
+
+// LDS layout of the accumulators: cell (lc, lr) sits at
+// lr * TC + ((lc + swizzle2(lr)) mod TC).  Samples stepping along r land two
+// rows apart; the rotation by lr / 2 spreads them over different banks (an
+// fp64 cell spans two of the 64 four-byte banks).
+__device__ __forceinline__ int swizzle2(int lr) { return (lr >> 1) & (TC - 1); }
+
+// Per-pass constants: local cell of tap j on axis a is sgn * floor(x_a) + off[a] + sgn * j
+// (sgn = -1 for the flipped taps), valid in [lmin[a], S_a).
+struct TapMap2 {
+    int sgn;
+    int off[2];
+    int lmin[2];
+};
+
+// Spread one sample over the tile: taps at floor(x) - LOW + j, weights of the
+// reference's (bi)linear / Catmull-Rom stencil (projection_utils.h:172-300),
+// v * (wr * wc) in fp64 (the reference's (v * wr) * wc in fp32 up to rounding).
+template <bool CUBIC, int MODE, bool WEIGHTS>
+__device__ __forceinline__ void scatter_sample2(const Geom& g, const Slot2& sd, int rr, int cc, Cx<float> v,
+                                                float wpix, bool shifted, bool flip, const TapMap2& tm,
+                                                double* acc_re, double* acc_im, double* acc_w) {
+    constexpr int K = CUBIC ? 4 : 2, LOW = CUBIC ? 1 : 0;
+    const float fr = float(rr), fc = float(cc);
+    float x[2];
+    rotate_pix(sd.R, fr, fc, g.os, x);
+    if (shifted) {
+        if (MODE == 0) v = cmul(v, cconj(phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k)));
+        else v = cmul(v, phase_hw(-fr, -fc, sd.s0, sd.s1, g.phase_k));
+    }
+    constexpr int S[2] = {TC, TR};
+    int loc[2][K];
+    double wt[2][K];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+        float f;
+        const int fl = split_as<false>(x[a], f);
+        const int l0 = (flip ? -fl : fl) + tm.off[a];
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            const int l = l0 + tm.sgn * j;
+            loc[a][j] = (unsigned)(l - tm.lmin[a]) < (unsigned)(S[a] - tm.lmin[a]) ? l : -1;
+            if (CUBIC) wt[a][j] = double(cubic_w<float>(f - float(j - LOW)));
+        }
+        if (!CUBIC) {
+            wt[a][1] = double(f);
+            wt[a][0] = 1.0 - wt[a][1];
+        }
+    }
+    const double vre = double(v.re), vim = flip ? -double(v.im) : double(v.im), wp = double(wpix);
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        if (loc[1][i] < 0) continue;
+        const int row = loc[1][i] * TC, rot = swizzle2(loc[1][i]);
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            if (loc[0][j] < 0) continue;
+            const double w = wt[1][i] * wt[0][j];
+            const int li = row + ((loc[0][j] + rot) & (TC - 1));
+            atomicAdd(&acc_re[li], vre * w);
+            atomicAdd(&acc_im[li], vim * w);
+            if (WEIGHTS) atomicAdd(&acc_w[li], wp * (CUBIC ? fabs(w) : w));
+        }
+    }
+}
+
+// MODE 0: backprojection, v = proj * conj(phase(r, c)), optional weights.
+// MODE 1: reconstruction gradient of the projection, v = g * phase(-r, -c).
+// dst (and wdst) must be zero-filled: every item adds its partial tile.
+template <bool CUBIC, int MODE, bool WEIGHTS, int KP>
+__global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 ts, const Cx<float>* __restrict__ src,
+                                                             const float* __restrict__ weights,
+                                                             const float* __restrict__ rot,
+                                                             const float* __restrict__ shifts,
+                                                             Cx<float>* __restrict__ dst, float* __restrict__ wdst) {
+    constexpr int SL = CUBIC ? 2 : 1, SH = CUBIC ? 1 : 0;  // stencil reach below / above floor(x)
+    constexpr int SLOW = CUBIC ? 1 : 0;                    // first tap at floor(x) - SLOW
+    constexpr int RPS = 64 / KP;
+    constexpr int NW = kThreads / 64;
+    __shared__ double acc_re[T2], acc_im[T2];
+    __shared__ double acc_w[WEIGHTS ? T2 : 1];
+    __shared__ unsigned short plist[2 * kChunk2];
+    __shared__ int pcnt[2];
+    __shared__ Slot2 slots[NW][KP];
+    __shared__ int marks[NW][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int slot = lane / RPS, jrow = lane % RPS;
+    const int N = g.N, H = g.H, half = N / 2;
+    const int64_t items = g.B * ts.ksplit * int64_t(ts.nr) * ts.nc;
+    const float cut2 = float(g.cut2);
+    const int64_t per = xcd_per<kRun>(items);
+    for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
+        const int64_t w = xcd_item<kRun>(slot_i);
+        if (w >= items) continue;
+        // items: tile column fastest, then tile row, pose range, batch
+        const int kc = int(w % ts.nc);
+        int64_t q = w / ts.nc;
+        const int kr = ts.kr0 + int(q % ts.nr);
+        q /= ts.nr;
+        const int jr = int(q % ts.ksplit);
+        const int64_t b = q / ts.ksplit;
+        const int p0 = jr * ts.prange, p1 = min(int(g.P), p0 + ts.prange);
+        // stored cells of this tile, signed coordinates: r in [-N/2+1, N/2], c in [0, N/2]
+        const int tc = kc * TC, tr = -half + 1 + kr * TR;
+        const int fc0 = -tc - TC + 1, fr0 = -tr - TR + 1;
+        const float lo1[2] = {float(tc - SL) - ts.eps, float(tr - SL) - ts.eps};
+        const float hi1[2] = {float(tc + TC + SH) + ts.eps, float(tr + TR + SH) + ts.eps};
+        const float lo2[2] = {float(fc0 - SL) - ts.eps, float(fr0 - SL) - ts.eps};
+        const float hi2[2] = {float(fc0 + TC + SH) + ts.eps, float(fr0 + TR + SH) + ts.eps};
+        for (int e = tid; e < T2; e += kThreads) {
+            acc_re[e] = 0.0;
+            acc_im[e] = 0.0;
+            if (WEIGHTS) acc_w[e] = 0.0;
+        }
+        const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
+        const float* rotb = rot + rb * g.P * 4;
+        const float* shb = shifts ? shifts + sb * g.P * 2 : nullptr;
+        const int64_t pose0 = b * g.P;
+        // samples lie within |x| <= rho; box 2 is box 1 mirrored, so one test serves both
+        float dist2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const float d = lo1[k] > 0.f ? lo1[k] : (hi1[k] < 0.f ? -hi1[k] : 0.f);
+            dist2 += d * d;
+        }
+        const int pend = dist2 > ts.rho * ts.rho ? p0 : p1;
+
+        for (int pbase = p0; pbase < pend; pbase += kChunk2) {
+            int n1, n2;
+            cull2(rotb, pend, pbase, lo1, hi1, lo2, hi2, plist, pcnt, n1, n2);
+#pragma unroll 1
+            for (int pass = 0; pass < 2; ++pass) {
+                const int np = pass == 0 ? n1 : n2;
+                auto pose_at = [&](int k) { return pbase + int(plist[pass == 0 ? k : 2 * kChunk2 - 1 - k]); };
+                float lo[2], hi[2];
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    lo[k] = pass == 0 ? lo1[k] : lo2[k];
+                    hi[k] = pass == 0 ? hi1[k] : hi2[k];
+                }
+                // direct taps: l = floor(x) - LOW + j - t; flipped: l = -(floor(x) - LOW + j) - t,
+                // and at c = 0 a flipped tap must have c < 0 (l >= 1 when t_c = 0)
+                TapMap2 tm;
+                tm.sgn = pass == 0 ? 1 : -1;
+                tm.off[0] = pass == 0 ? -SLOW - tc : SLOW - tc;
+                tm.off[1] = pass == 0 ? -SLOW - tr : SLOW - tr;
+                tm.lmin[0] = (pass == 1 && tc == 0) ? 1 : 0;
+                tm.lmin[1] = 0;
+                int base = wave * KP;
+                float Rn[4], Sn[2];
+                if (base < np) load_pose2(rotb, shb, pose_at(min(base + slot, np - 1)), Rn, Sn);
+                for (; base < np; base += NW * KP) {
+                    const bool sv = base + slot < np;
+                    const int pp = pose_at(min(base + slot, np - 1));
+                    float R[4], Sh[2];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) R[e] = Rn[e];
+                    Sh[0] = Sn[0];
+                    Sh[1] = Sn[1];
+                    if (base + NW * KP < np)
+                        load_pose2(rotb, shb, pose_at(min(base + NW * KP + slot, np - 1)), Rn, Sn);
+                    if (jrow == 0 && sv) {
+                        Slot2& sd = slots[wave][slot];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) sd.R[e] = R[e];
+                        sd.s0 = Sh[0];
+                        sd.s1 = Sh[1];
+                        sd.p = pp;
+                    }
+                    __builtin_amdgcn_wave_barrier();
+                    int r0, r1;
+                    box_rows2(R, lo, hi, ts, r0, r1);
+                    const int nr = sv ? max(0, r1 - r0 + 1) : 0;
+                    const int maxnr = wave_max(nr);
+                    for (int rbase = 0; rbase < maxnr; rbase += RPS) {
+                        const int jj = rbase + jrow;
+                        const int r = r0 + jj;
+                        int c0 = 0, cnt = 0;
+                        if (jj < nr) {
+                            int c1;
+                            row_span2(R, r, lo, hi, ts, cut2, c0, c1);
+                            cnt = max(0, c1 - c0 + 1);
+                        }
+                        const int incl = dpp_scan_add(cnt);
+                        const int excl = incl - cnt;
+                        const int total = __builtin_amdgcn_readlane(incl, 63);
+                        int carry = 0;
+                        // sample e0 + lane of this row block: owner lane, pixel, validity, and its loads
+                        auto fetch_sample = [&](int e0, int& rr, int& cc, int& sl, bool& ok, Cx<float>& v,
+                                                float& wv) {
+                            const int e = e0 + lane;
+                            const int lw = window_owner(cnt, excl, e0, carry, marks[wave]);
+                            rr = __shfl(r, lw, 64);
+                            cc = __shfl(c0, lw, 64) + (e - __shfl(excl, lw, 64));
+                            sl = lw / RPS;
+                            ok = e < total;
+                            const Slot2& sd = slots[wave][sl];
+                            ok = ok && !filtered(float(rr), float(cc), cut2) &&
+                                 !(cc == 0 && (rr == g.n / 2 || rr < 0));  // Friedel half of x = 0
+                            const int i = rr >= 0 ? rr : rr + g.n;
+                            const int64_t pidx = (pose0 + sd.p) * int64_t(g.npix) + i * g.hp + cc;
+                            v = ok ? src[pidx] : Cx<float>{0.f, 0.f};
+                            wv = (WEIGHTS && ok) ? weights[pidx] : 0.f;
+                        };
+                        int rr, cc, sl;
+                        bool ok;
+                        Cx<float> v;
+                        float wv;
+                        fetch_sample(0, rr, cc, sl, ok, v, wv);
+                        for (int e0 = 0; e0 < total; e0 += 64) {
+                            // the next window's loads are in flight while this one is spread
+                            int rr2 = 0, cc2 = 0, sl2 = 0;
+                            bool ok2 = false;
+                            Cx<float> v2 = {0.f, 0.f};
+                            float wv2 = 0.f;
+                            if (e0 + 64 < total) fetch_sample(e0 + 64, rr2, cc2, sl2, ok2, v2, wv2);
+                            if (ok)
+                                scatter_sample2<CUBIC, MODE, WEIGHTS>(g, slots[wave][sl], rr, cc, v, wv,
+                                                                      shifts != nullptr, pass == 1, tm, acc_re,
+                                                                      acc_im, acc_w);
+                            rr = rr2;
+                            cc = cc2;
+                            sl = sl2;
+                            ok = ok2;
+                            v = v2;
+                            wv = wv2;
+                        }
+                    }
+                    __builtin_amdgcn_wave_barrier();
+                }
+            }
+        }
+
+        // add the partial tile into the image (cells past the stored range are dropped taps)
+        __syncthreads();
+        if (pend > p0) {
+            for (int e = tid; e < T2; e += kThreads) {
+                const int lc = e % TC, lr = e / TC;
+                const int c = tc + lc, r = tr + lr;
+                if (c >= H || r > half) continue;
+                const int re = r < 0 ? r + N : r;
+                const int64_t idx = b * g.vol + int64_t(re) * H + c;
+                const int a = (e - lc) + ((lc + swizzle2(lr)) & (TC - 1));
+                const double vr = acc_re[a], vi = acc_im[a];
+                if (vr != 0.0) atomic_add(&dst[idx].re, float(vr));
+                if (vi != 0.0) atomic_add(&dst[idx].im, float(vi));
+                if (WEIGHTS && acc_w[a] != 0.0) atomic_add(&wdst[idx], float(acc_w[a]));
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Hermitian completion of the x = 0 column after an unmirrored accumulation:
+// every x = 0 contribution v of the reference is also added, conjugated, at
+// the partner cell -r (projection_utils.h:398-405, 481-492), so the final
+// value of a cell is A(r) + conj(A(-r)) (weights: A_w(r) + A_w(-r)).  One lane
+// per unordered pair; the self-partnered cells r = 0 and r = N/2 are kept.
+template <bool WEIGHTS>
+__global__ __launch_bounds__(kBlock) void k_mirror2_x0(Geom g, Cx<float>* __restrict__ dst,
+                                                       float* __restrict__ wdst) {
+    const int N = g.N, H = g.H;
+    for (int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x; e < g.B * N; e += int64_t(gridDim.x) * kBlock) {
+        const int64_t b = e / N;
+        const int re = int(e - b * N);
+        const int rm = re == 0 ? 0 : N - re;
+        if (rm <= re) continue;  // self-partnered, or handled by the partner's lane
+        const int64_t i0 = b * g.vol + int64_t(re) * H, i1 = b * g.vol + int64_t(rm) * H;
+        const Cx<float> a = dst[i0], m = dst[i1];
+        dst[i0] = Cx<float>{a.re + m.re, a.im - m.im};
+        dst[i1] = Cx<float>{m.re + a.re, m.im - a.im};
+        if (WEIGHTS) {
+            const float wa = wdst[i0], wm = wdst[i1];
+            wdst[i0] = wa + wm;
+            wdst[i1] = wm + wa;
+        }
+    }
+}
+
+template <bool CUBIC, int MODE, bool WEIGHTS, int KP>
+hipError_t scatter2_launch(const Geom& g, const TileSpec2& ts, const void* src, const void* weights,
+                           const void* rot, const void* shifts, void* dst, void* wdst, hipStream_t s) {
+    const int64_t work = g.B * ts.ksplit * int64_t(ts.nr) * ts.nc;
+    if (work > 0) {
+        hipLaunchKernelGGL((k_scatter2_tiled<CUBIC, MODE, WEIGHTS, KP>), dim3(grid_for(kXcds * xcd_per<kRun>(work))),
+                           dim3(kThreads), 0, s, g, ts, (const Cx<float>*)src, (const float*)weights,
+                           (const float*)rot, (const float*)shifts, (Cx<float>*)dst, (float*)wdst);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (MODE != 0) return hipSuccess;
+    int64_t blocks = (g.B * g.N + kBlock - 1) / kBlock;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) return hipSuccess;
+    hipLaunchKernelGGL(k_mirror2_x0<WEIGHTS>, dim3(unsigned(blocks)), dim3(kBlock), 0, s, g, (Cx<float>*)dst,
+                       (float*)wdst);
+    return hipGetLastError();
+}
+
+template <bool CUBIC, int MODE, bool WEIGHTS>
+hipError_t scatter2_kp(const Geom& g, const TileSpec2& ts, const void* src, const void* weights, const void* rot,
+                       const void* shifts, void* dst, void* wdst, hipStream_t s) {
+    if (ts.kp >= 4) return scatter2_launch<CUBIC, MODE, WEIGHTS, 4>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    if (ts.kp == 2) return scatter2_launch<CUBIC, MODE, WEIGHTS, 2>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    return scatter2_launch<CUBIC, MODE, WEIGHTS, 1>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+}
+
+}  // namespace
+
+hipError_t launch_scatter2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* src,
+                                 const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
+                                 hipStream_t s) {
+    if (mode == 0) {
+        if (weights)
+            return cubic ? scatter2_kp<true, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s)
+                         : scatter2_kp<false, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+        return cubic ? scatter2_kp<true, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
+                     : scatter2_kp<false, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
+    }
+    return cubic ? scatter2_kp<true, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
+                 : scatter2_kp<false, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
+}
+
+}  // namespace tp

@@ -36,6 +36,7 @@
 // masked pixels of the forward.
 #include "tp_device.hh"
 #include "tp_launch.hh"
+#include "tp_tiled_common.hh"
 
 namespace tp {
 
@@ -45,11 +46,6 @@ constexpr int L = kTileEdge, LD = kTileEdgeD;  // forward tile edges (voxels): c
 constexpr int SC = kScTC, SR = kScTR, SD = kScTD, S3 = SC * SR * SD;  // scatter tile
 constexpr int kForwThreads = 256;     // forward workgroup
 constexpr int kScatterThreads = 256;  // scatter workgroup
-
-__device__ __forceinline__ int to_int_clamped(float v) {
-    v = fminf(fmaxf(v, -1.0e8f), 1.0e8f);
-    return int(v);
-}
 
 // Does the slice plane (through the origin, spanned by columns 0 and 1 of R)
 // pass within the box [lo, hi] (x-order c, r, d)?
@@ -120,46 +116,6 @@ __device__ __forceinline__ void row_span(const float* R, int r, const float* lo,
     else c1 = min(c1, int(sqrtf(rem)) + 1);
 }
 
-// Wave-wide inclusive prefix sum / max with DPP row shifts and broadcasts
-// (register-to-register inside the SIMD, no LDS round trip).  Call with
-// every lane active.
-__device__ __forceinline__ int dpp_scan_add(int v) {
-    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
-    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
-    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
-    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
-    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
-    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
-    return v;
-}
-// Values must be >= 0 (0 is the identity).
-__device__ __forceinline__ int dpp_scan_max(int v) {
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false));
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false));
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false));
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false));
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false));
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false));
-    return v;
-}
-__device__ __forceinline__ int wave_max(int v) { return __builtin_amdgcn_readlane(dpp_scan_max(max(v, 0)), 63); }
-
-// Row lanes hold `cnt` samples starting at flattened index `excl`.  For the
-// window [e0, e0 + 64) every lane gets the row lane owning index e0 + lane:
-// rows mark their first index in a per-wave LDS array, a prefix max carries
-// the marks forward, and `carry` brings the owner across windows.
-__device__ __forceinline__ int window_owner(int cnt, int excl, int e0, int& carry, int* marks) {
-    const int lane = threadIdx.x & 63;
-    marks[lane] = 0;
-    __builtin_amdgcn_wave_barrier();
-    if (cnt > 0 && excl >= e0 && excl < e0 + 64) marks[excl - e0] = lane + 1;
-    __builtin_amdgcn_wave_barrier();
-    const int m = max(dpp_scan_max(marks[lane]), carry);
-    carry = __builtin_amdgcn_readlane(m, 63);
-    __builtin_amdgcn_wave_barrier();
-    return m - 1;
-}
-
 // Sample position of pixel (r, c): rotate<3> without its R[k][2] * 0 terms.
 // Adding that signed zero to the other two terms can only flip the sign of a
 // zero coordinate, which floors to the same cell with the same fraction.
@@ -210,22 +166,6 @@ __device__ __forceinline__ void load_pose(const float* __restrict__ rotb, const 
     S[1] = shb ? shb[2 * int64_t(p) + 1] : 0.f;
 }
 
-// The hardware deals workgroups to the 8 XCDs (each with its own L2) round-
-// robin by workgroup id.  Items are handed out in runs of RUN neighbouring
-// tiles per XCD (run k of XCD x is item run 8k + x), so an XCD's L2 shares the
-// halos and projection rows of a run while the runs stay interleaved over the
-// volume for balance.  Slots past the last item do nothing.
-constexpr int kXcds = 8;
-template <int RUN>
-__host__ __device__ inline int64_t xcd_per(int64_t items) {
-    const int64_t span = int64_t(kXcds) * RUN;
-    return (items + span - 1) / span * RUN;
-}
-template <int RUN>
-__device__ __forceinline__ int64_t xcd_item(int64_t slot) {
-    const int64_t x = slot % kXcds, j = slot / kXcds;
-    return ((j / RUN) * kXcds + x) * RUN + j % RUN;
-}
 constexpr int kRunForw = 64, kRunScatter = 128;  // measured at the headline
 
 // Work items: first the core tiles, one item per (batch, tile, pose range),

@@ -1,0 +1,74 @@
+// Wave-level building blocks shared by the tile-owner kernels (tp_tiled3d.hip,
+// tp_tiled2d.hip): DPP scans, the window-owner lookup of compacted sample
+// lists, and the XCD-aware hand-out of work items.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tp {
+namespace {
+
+__device__ __forceinline__ int to_int_clamped(float v) {
+    v = fminf(fmaxf(v, -1.0e8f), 1.0e8f);
+    return int(v);
+}
+
+// Wave-wide inclusive prefix sum / max with DPP row shifts and broadcasts
+// (register-to-register inside the SIMD, no LDS round trip).  Call with
+// every lane active.
+__device__ __forceinline__ int dpp_scan_add(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return v;
+}
+// Values must be >= 0 (0 is the identity).
+__device__ __forceinline__ int dpp_scan_max(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false));
+    return v;
+}
+__device__ __forceinline__ int wave_max(int v) { return __builtin_amdgcn_readlane(dpp_scan_max(max(v, 0)), 63); }
+
+// Row lanes hold `cnt` samples starting at flattened index `excl`.  For the
+// window [e0, e0 + 64) every lane gets the row lane owning index e0 + lane:
+// rows mark their first index in a per-wave LDS array, a prefix max carries
+// the marks forward, and `carry` brings the owner across windows.
+__device__ __forceinline__ int window_owner(int cnt, int excl, int e0, int& carry, int* marks) {
+    const int lane = threadIdx.x & 63;
+    marks[lane] = 0;
+    __builtin_amdgcn_wave_barrier();
+    if (cnt > 0 && excl >= e0 && excl < e0 + 64) marks[excl - e0] = lane + 1;
+    __builtin_amdgcn_wave_barrier();
+    const int m = max(dpp_scan_max(marks[lane]), carry);
+    carry = __builtin_amdgcn_readlane(m, 63);
+    __builtin_amdgcn_wave_barrier();
+    return m - 1;
+}
+
+// The hardware deals workgroups to the 8 XCDs (each with its own L2) round-
+// robin by workgroup id.  Items are handed out in runs of RUN neighbouring
+// tiles per XCD (run k of XCD x is item run 8k + x), so an XCD's L2 shares the
+// halos and projection rows of a run while the runs stay interleaved over the
+// volume for balance.  Slots past the last item do nothing.
+constexpr int kXcds = 8;
+template <int RUN>
+__host__ __device__ inline int64_t xcd_per(int64_t items) {
+    const int64_t span = int64_t(kXcds) * RUN;
+    return (items + span - 1) / span * RUN;
+}
+template <int RUN>
+__device__ __forceinline__ int64_t xcd_item(int64_t slot) {
+    const int64_t x = slot % kXcds, j = slot / kXcds;
+    return ((j / RUN) * kXcds + x) * RUN + j % RUN;
+}
+}  // namespace
+}  // namespace tp
