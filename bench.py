@@ -13,8 +13,8 @@ the kernels run on), and the reference CPU path timed on a bounded sample of
 the same inputs on the host cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--no-cpu]
-Configs: headline (default, the bench line), c2..c5 (the other BASELINE.json configurations,
-for per-op timings; no CPU baseline or traffic figure for them).
+Configs: headline (default, the bench line), c2..c5 (the other BASELINE.json configurations:
+per-op rates and the CPU baseline on a bounded sample; no traffic figure for them).
 """
 import argparse
 import json
@@ -141,11 +141,26 @@ def bytes_backproject_back(npose, n, dim, interp, weights, cutoff=None):
 
 
 # ----------------------------------------------------------------------------- workloads
+def timed_ops(calls, samples_per_op):
+    """Run CPU calls in order, one run each; returns (seconds, samples, per-op seconds)."""
+    import torch
+    torch.cuda.synchronize()
+    parts = {}
+    total = 0.0
+    for name, fn in calls:
+        t0 = time.perf_counter()
+        fn()
+        parts[name] = time.perf_counter() - t0
+        total += parts[name]
+    return total, samples_per_op * len(calls), parts
+
+
 class Workload:
     """Inputs on the GPU, a step as a list of (op name, callable, bytes, samples)."""
 
-    def __init__(self, name, desc, ops, cpu_sample=None, config=None):
+    def __init__(self, name, desc, ops, cpu_sample=None, config=None, cpu_pmax=None):
         self.name, self.desc, self.ops, self.cpu_sample, self.config = name, desc, ops, cpu_sample, config or {}
+        self.cpu_pmax = cpu_pmax or ops[0][4]  # poses the CPU sample may take (one batch item's)
 
 
 def make_headline(dev, k=0):
@@ -182,7 +197,8 @@ def make_headline(dev, k=0):
         t1 = time.perf_counter()
         cpu_ops.backproject_2d_to_3d_forw(pc, wc, rc, sc, "linear", os_, None)
         t2 = time.perf_counter()
-        return t2 - t0, 2 * p_cpu * n * (n // 2 + 1), {"fwd_s": t1 - t0, "bp_s": t2 - t1}
+        return t2 - t0, 2 * p_cpu * n * (n // 2 + 1), {"project_3d_to_2d_forw": t1 - t0,
+                                                       "backproject_2d_to_3d_forw": t2 - t1}
 
     cfg = {"workload": "headline: project_3d_to_2d_forw + backproject_2d_to_3d_forw (weights), linear",
            "volume": [1, 512, 512, 257], "poses": P, "proj": [n, n // 2 + 1], "oversampling": os_,
@@ -203,11 +219,16 @@ def make_c2(dev):
     def fwd():
         T.project_3d_to_2d_forw(vol, rot, sh, [n, n], "linear", os_, None)
 
+    def cpu_sample(p, threads, cpu_ops):
+        vc, rc, sc = vol.cpu(), rot[:, :p].cpu(), sh[:, :p].cpu()
+        return timed_ops([("project_3d_to_2d_forw", lambda: cpu_ops.project_3d_to_2d_forw(
+            vc, rc, sc, [n, n], "linear", os_, None))], p * n * (n // 2 + 1))
+
     samples = P * n * (n // 2 + 1)
     cfg = {"workload": "c2: project_3d_to_2d_forw, linear", "volume": [1, 256, 256, 129], "poses": P,
            "proj": [n, n // 2 + 1], "oversampling": os_}
     return Workload("c2", cfg["workload"], [("project_3d_to_2d_forw", fwd, bytes_forward(P, n, 3, "linear"),
-                                             samples, P)], None, cfg)
+                                             samples, P)], cpu_sample, cfg)
 
 
 def make_c3(dev):
@@ -224,12 +245,17 @@ def make_c3(dev):
     def bp():
         T.backproject_2d_to_3d_forw(proj, w, rot, sh, "linear", os_, None)
 
+    def cpu_sample(p, threads, cpu_ops):
+        pc, wc, rc, sc = proj[:, :p].cpu(), w[:, :p].cpu(), rot[:, :p].cpu(), sh[:, :p].cpu()
+        return timed_ops([("backproject_2d_to_3d_forw", lambda: cpu_ops.backproject_2d_to_3d_forw(
+            pc, wc, rc, sc, "linear", os_, None))], p * n * (n // 2 + 1))
+
     samples = P * n * (n // 2 + 1)
     cfg = {"workload": "c3: backproject_2d_to_3d_forw (weights), linear", "volume": [1, 256, 256, 129],
            "poses": P, "proj": [n, n // 2 + 1], "oversampling": os_}
     return Workload("c3", cfg["workload"],
                     [("backproject_2d_to_3d_forw", bp, bytes_backproject(P, n, 3, "linear", 256 * 256 * 129, True),
-                      samples, P)], None, cfg)
+                      samples, P)], cpu_sample, cfg)
 
 
 def make_c4(dev):
@@ -249,6 +275,15 @@ def make_c4(dev):
     def back():
         T.project_3d_to_2d_back(g, vol, rot, sh, "cubic", os_, None)
 
+    def cpu_sample(p, threads, cpu_ops):
+        vc, gc = vol.cpu(), g[:, :p].cpu()
+        rc = rot[:, :p].detach().cpu().requires_grad_(True)
+        sc = sh[:, :p].detach().cpu().requires_grad_(True)
+        return timed_ops([("project_3d_to_2d_forw", lambda: cpu_ops.project_3d_to_2d_forw(
+                              vc, rc.detach(), sc.detach(), [n, n], "cubic", os_, None)),
+                          ("project_3d_to_2d_back", lambda: cpu_ops.project_3d_to_2d_back(
+                              gc, vc, rc, sc, "cubic", os_, None))], p * n * (n // 2 + 1))
+
     V = 512 * 512 * 257
     samples = P * n * (n // 2 + 1)
     cfg = {"workload": "c4: project_3d_to_2d_forw + project_3d_to_2d_back (rotation/shift grads), cubic",
@@ -256,7 +291,7 @@ def make_c4(dev):
     return Workload("c4", cfg["workload"],
                     [("project_3d_to_2d_forw", fwd, bytes_forward(P, n, 3, "cubic"), samples, P),
                      ("project_3d_to_2d_back", back, bytes_project_back(P, n, 3, "cubic", V), samples, P)],
-                    None, cfg)
+                    cpu_sample, cfg)
 
 
 def make_c5(dev):
@@ -286,6 +321,22 @@ def make_c5(dev):
     def p_back():
         T.project_2d_back(st["gproj"], rec, rot_g, sh_g, "cubic", os_, cut)
 
+    def cpu_sample(p, threads, cpu_ops):
+        """Item 0's first p poses through the four ops."""
+        if "gproj" not in st:
+            bp_back()
+        rc0, r0, s0 = rec[:1].cpu(), rot[:1, :p].cpu(), sh[:1, :p].cpu()
+        rg0, sg0 = r0.clone().requires_grad_(True), s0.clone().requires_grad_(True)
+        pr0, gp0, on0 = st["proj"][:1, :p].cpu(), st["gproj"][:1, :p].cpu(), ones[:1, :p].cpu()
+        gd0, gw0 = gd[:1].cpu(), gw[:1].cpu()
+        return timed_ops([("project_2d_forw", lambda: cpu_ops.project_2d_forw(rc0, r0, s0, [n, n], "cubic", os_, cut)),
+                          ("backproject_2d_forw", lambda: cpu_ops.backproject_2d_forw(
+                              pr0, on0, r0, s0, "cubic", os_, cut)),
+                          ("backproject_2d_back", lambda: cpu_ops.backproject_2d_back(
+                              gd0, gw0, pr0, on0, rg0, sg0, "cubic", os_, cut)),
+                          ("project_2d_back", lambda: cpu_ops.project_2d_back(gp0, rc0, rg0, sg0, "cubic", os_, cut))],
+                         p * n * (n // 2 + 1))
+
     samples = B * P * n * (n // 2 + 1)
     V = B * 512 * 257
     cfg = {"workload": "c5: batched 2D cubic forward, backprojection (unit weights), both backward ops",
@@ -297,7 +348,7 @@ def make_c5(dev):
                      ("backproject_2d_back", bp_back, bytes_backproject_back(B * P, n, 2, "cubic", True, cut),
                       samples, B * P),
                      ("project_2d_back", p_back, bytes_project_back(B * P, n, 2, "cubic", V, cut), samples,
-                      B * P)], None, cfg)
+                      B * P)], cpu_sample, cfg, cpu_pmax=P)
 
 
 # headline is the bench line; c2-c5 are the other BASELINE configurations, run on request
@@ -314,17 +365,32 @@ def cpu_ops_and_kind():
 
 
 def run_cpu_baseline(wl, target_s=12.0):
+    """Time the workload's ops on the host cores on its first p poses.
+
+    p doubles (or scales by the measured rate) until one run takes about half
+    of target_s or covers every pose of the workload; short runs are repeated
+    up to about target_s and the fastest is reported.
+    """
     import torch
     threads = min(16, len(os.sched_getaffinity(0)))
     torch.set_num_threads(threads)
     ops, kind = cpu_ops_and_kind()
-    # probe with a small sample, then scale to about target_s of CPU work
-    t, s, _ = wl.cpu_sample(16, threads, ops)
-    p = int(min(2048, max(16, 16 * target_s / max(t, 1e-3))))
+    p = min(8, wl.cpu_pmax)
     t, s, parts = wl.cpu_sample(p, threads, ops)
+    while t < 0.5 * target_s and p < wl.cpu_pmax:
+        p = int(min(wl.cpu_pmax, max(2 * p, p * 0.6 * target_s / max(t, 1e-3))))
+        t, s, parts = wl.cpu_sample(p, threads, ops)
+    spent, runs = t, 1
+    while spent + t < target_s and runs < 5:
+        t2, s2, parts2 = wl.cpu_sample(p, threads, ops)
+        spent, runs = spent + t2, runs + 1
+        if t2 < t:
+            t, s, parts = t2, s2, parts2
+    split = ", ".join(f"{k} {v:.2f} s" for k, v in parts.items())
     return {"value": s / t, "unit": "Fourier samples/s", "cores": threads, "kind": kind,
-            "sample": f"first {p} of the workload's poses, both ops, one run each ({t:.1f} s; "
-                      f"fwd {parts['fwd_s']:.2f} s, bp {parts['bp_s']:.2f} s), {threads} threads"}
+            "poses_per_s": p / t, "ops_s": {k: round(v, 4) for k, v in parts.items()},
+            "sample": f"first {p} poses of the workload (item 0), every op of the step, best of {runs} "
+                      f"run(s) ({t:.2f} s: {split}), {threads} threads"}
 
 
 # ----------------------------------------------------------------------------- HBM traffic
