@@ -158,9 +158,12 @@ def timed_ops(calls, samples_per_op):
 class Workload:
     """Inputs on the GPU, a step as a list of (op name, callable, bytes, samples)."""
 
-    def __init__(self, name, desc, ops, cpu_sample=None, config=None, cpu_pmax=None):
+    def __init__(self, name, desc, ops, cpu_sample=None, config=None, cpu_pmax=None, cpu_kind=None, cpu_cores=None):
         self.name, self.desc, self.ops, self.cpu_sample, self.config = name, desc, ops, cpu_sample, config or {}
         self.cpu_pmax = cpu_pmax or ops[0][4]  # poses the CPU sample may take (one batch item's)
+        # the CPU leg runs the reference build (or the oracle when absent) on `threads` cores,
+        # unless the workload times its own port (numpy: one core)
+        self.cpu_kind, self.cpu_cores = cpu_kind, cpu_cores
 
 
 def make_headline(dev, k=0):
@@ -351,8 +354,61 @@ def make_c5(dev):
                       B * P)], cpu_sample, cfg, cpu_pmax=P)
 
 
-# headline is the bench line; c2-c5 are the other BASELINE configurations, run on request
-WORKLOADS = {"headline": make_headline, "c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5}
+def make_prep(dev):
+    """prep: the reference preparation around the headline volume, both ways.
+
+    to_fourier: 256^3 real blob volume -> pad_and_fftshift (512^3) -> rfftn ->
+    [512, 512, 257] row-major; reconstruct: a (data, weight) pair of that shape
+    -> normalize_reconstruction -> irfftn -> ifftshift_and_crop -> 256^3.  The
+    pad, crop and normalisation are this library's kernels; the FFTs are rocFFT
+    (through torch.fft).
+    """
+    import torch
+    from torch_projectors import fourier as F
+    gen = torch.Generator().manual_seed(20261201 + 7)
+    n, os_ = 256, 2.0
+    N = 512
+    real = torch.fft.irfftn(blob_volume_rfft(n, N, 32, 80.0, gen, dev), s=(N, N, N), norm="forward")
+    vol = F.ifftshift_and_crop(real, os_)[0].contiguous()  # [n, n, n]
+    w = torch.rand(N, N, N // 2 + 1, generator=gen).to(dev) + 0.5
+    st = {}
+
+    def fwd():
+        st["spec"] = F.to_fourier(vol, os_)
+
+    def back():
+        st["out"] = F.reconstruct(st["spec"], w, os_, 0.01)
+
+    V = N * N * (N // 2 + 1)
+
+    def cpu_sample(p, threads, cpu_ops):
+        """The oracle's numpy restatement with numpy's FFT (one core)."""
+        import numpy as np
+        from oracle import fourier as OF
+        vc, wc = vol.cpu().numpy(), w.cpu().numpy()
+        t0 = time.perf_counter()
+        spec = np.fft.rfftn(OF.pad_and_fftshift(vc, os_), axes=(0, 1, 2), norm="forward").astype(np.complex64)
+        t1 = time.perf_counter()
+        normed = OF.normalize_reconstruction(spec, wc, 0.01)
+        back_ = np.fft.irfftn(normed, s=(N, N, N), axes=(0, 1, 2), norm="forward").astype(np.float32)
+        OF.ifftshift_and_crop(back_, os_)
+        t2 = time.perf_counter()
+        return t2 - t0, 2 * V, {"to_fourier": t1 - t0, "reconstruct": t2 - t1}
+
+    cfg = {"workload": "prep: to_fourier (pad_and_fftshift + rfftn) and reconstruct (normalize + irfftn + "
+                       "ifftshift_and_crop)", "real_volume": [n, n, n], "padded": [N, N, N],
+           "spectrum": [N, N, N // 2 + 1], "oversampling": os_}
+    # minimal bytes: read the input and write the output once
+    return Workload("prep", cfg["workload"],
+                    [("to_fourier", fwd, n ** 3 * 4 + V * 8, V, 0),
+                     ("reconstruct", back, V * (8 + 4) + n ** 3 * 4, V, 0)],
+                    cpu_sample, cfg, cpu_pmax=1, cpu_kind="port", cpu_cores=1)
+
+
+# headline is the bench line; c2-c5 are the other BASELINE configurations and
+# prep the reference preparation around the headline volume, run on request
+WORKLOADS = {"headline": make_headline, "c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5,
+             "prep": make_prep}
 
 
 # ----------------------------------------------------------------------------- CPU baseline
@@ -387,6 +443,7 @@ def run_cpu_baseline(wl, target_s=12.0):
         if t2 < t:
             t, s, parts = t2, s2, parts2
     split = ", ".join(f"{k} {v:.2f} s" for k, v in parts.items())
+    kind, threads = wl.cpu_kind or kind, wl.cpu_cores or threads
     return {"value": s / t, "unit": "Fourier samples/s", "cores": threads, "kind": kind,
             "poses_per_s": p / t, "ops_s": {k: round(v, 4) for k, v in parts.items()},
             "sample": f"first {p} poses of the workload (item 0), every op of the step, best of {runs} "

@@ -159,6 +159,63 @@ int tp_backproject_2d_to_3d_back(int dtype,
                                  void* grad_projections, void* grad_weights, void* grad_rotations, void* grad_shifts,
                                  void* stream);
 
+/* ---------------------------------------------------------------- reference preparation
+ *
+ * The real-space steps around the projectors that the reference performs
+ * with tensor ops in its helpers pad_and_fftshift / ifftshift_and_crop
+ * (tests/test_utils.py:174-247, 250-293; README.md:106-143), as single-pass
+ * kernels, plus the normalisation of a backprojected (data, weight) pair
+ * (no counterpart in the reference, whose dual volumes exist for it:
+ * paper/main.tex:72).  The FFTs between them are library calls (rocFFT).
+ * Elements are moved as opaque words of elem_bytes = 2, 4, 8 or 16 bytes (any
+ * real or complex dtype).  Axes: `dim` (2 or 3) equal-role spatial axes after
+ * one flattened batch axis, row-major. */
+
+/* pad_and_fftshift's output edge: int(boxsize * oversampling), plus one if odd
+ * (tests/test_utils.py:217-220).  Its zero padding before the data is
+ * (padded - boxsize) / 2, rounded down (:223-225). */
+int64_t tp_padded_boxsize(int64_t boxsize, double oversampling);
+
+/* ifftshift_and_crop's output edge: int(boxsize / oversampling)
+ * (tests/test_utils.py:281-286); the crop starts at (boxsize - cropped) / 2. */
+int64_t tp_cropped_boxsize(int64_t boxsize, double oversampling);
+
+/* dst[batch, N^dim] = fftshift over every spatial axis of src[batch, n^dim]
+ * zero-padded to N with pad_before zeros in front (replaces F.pad + fftshift,
+ * tests/test_utils.py:227-245).  Requires n <= N <= 2^30 and
+ * 0 <= pad_before <= N - n. */
+int tp_fftshift_pad(int elem_bytes, const void* src, int64_t batch, int dim, int64_t boxsize,
+                    int64_t padded_boxsize, int64_t pad_before, void* dst, void* stream);
+
+/* dst = ifftshift over every spatial axis of src[batch, len0, len1(, len2)],
+ * keeping indices [crop_start, crop_start + crop_len) of each axis, clipped
+ * to the axis like a Python slice (replaces ifftshift + slicing,
+ * tests/test_utils.py:271-293).  dst has the clipped lengths.  The adjoint
+ * of tp_fftshift_pad with pad_before = crop_start for even lengths. */
+int tp_ifftshift_crop(int elem_bytes, const void* src, int64_t batch, int dim, int64_t len0, int64_t len1,
+                      int64_t len2, int64_t crop_start, int64_t crop_len, void* dst, void* stream);
+
+/* rfftn with norm="forward" (scaled by 1/boxsize^dim) of `batch` real boxes
+ * [batch, boxsize^dim] into [batch, boxsize^(dim-1), boxsize/2+1] complex,
+ * both row-major, through hipFFT (rocFFT) with plans cached per shape for the
+ * life of the process (replaces torch.fft.rfftn in the reference's recipe,
+ * README.md:115-116).  `real` is left unchanged. */
+int tp_rfftn(int dtype, int dim, int64_t batch, int64_t boxsize, const void* real, void* spectrum, void* stream);
+
+/* The inverse (irfftn with norm="forward": unscaled) of tp_rfftn's layout.
+ * `spectrum` is overwritten (the library's complex-to-real transforms use
+ * their input as scratch). */
+int tp_irfftn(int dtype, int dim, int64_t batch, int64_t boxsize, void* spectrum, void* real, void* stream);
+
+/* out[e] = data[e] / (weights[e] + reg) component-wise where weights[e] + reg > 0,
+ * else 0: a Wiener-style normalisation of a backprojected pair (data complex,
+ * weights real, both of `dtype`, `elems` elements).  No counterpart in the
+ * reference (its dual data/weight volumes exist for this step,
+ * paper/main.tex:72); for callers that reconstruct after backprojection.
+ * out may alias data. */
+int tp_normalize_reconstruction(int dtype, const void* data, const void* weights, int64_t elems, double reg,
+                                void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -64,7 +64,9 @@ def build_lib(jobs=8):
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(compile_one, hip_sources()))
     tmp = LIB + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
+    rocm_lib = os.path.join(os.path.dirname(os.path.dirname(os.path.realpath(HIPCC))), "lib")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
+          f"-L{rocm_lib}", f"-Wl,-rpath,{rocm_lib}", "-lhipfft"])
     os.replace(tmp, LIB)
     return LIB
 

@@ -5,6 +5,7 @@
 // per-op TORCH_CHECKs), derives the launch geometry, zero-fills the outputs
 // that are accumulated, and enqueues the kernels on the caller's stream.
 // Nothing is synchronised and nothing is allocated.
+#include <algorithm>
 #include <cmath>
 #include <string>
 
@@ -453,6 +454,105 @@ int tp_backproject_2d_to_3d_back(int dtype, const void* grad_data_rec, const voi
                             P, proj_boxsize, proj_boxsize_half, weights, rotations, B_rot, shifts, B_shift,
                             interpolation, oversampling, has_cutoff, fourier_radius_cutoff, grad_projections,
                             grad_weights, grad_rotations, grad_shifts, stream);
+}
+
+/* ---------------------------------------------------------------- reference preparation */
+
+int64_t tp_padded_boxsize(int64_t boxsize, double oversampling) {
+    const int64_t raw = static_cast<int64_t>(double(boxsize) * oversampling);
+    return raw + (raw % 2);
+}
+
+int64_t tp_cropped_boxsize(int64_t boxsize, double oversampling) {
+    return static_cast<int64_t>(double(boxsize) / oversampling);
+}
+
+int tp_fftshift_pad(int elem_bytes, const void* src, int64_t batch, int dim, int64_t boxsize,
+                    int64_t padded_boxsize, int64_t pad_before, void* dst, void* stream) {
+    g_err.clear();
+    if (elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8 && elem_bytes != 16)
+        return fail("elem_bytes must be 2, 4, 8 or 16");
+    if (dim != 2 && dim != 3) return fail("dim must be 2 or 3");
+    if (batch < 0 || boxsize < 1) return fail("batch must be >= 0 and boxsize >= 1");
+    if (padded_boxsize < boxsize || padded_boxsize > (int64_t(1) << 30))
+        return fail("padded_boxsize must be in [boxsize, 2^30]");
+    if (pad_before < 0 || pad_before > padded_boxsize - boxsize)
+        return fail("pad_before must be in [0, padded_boxsize - boxsize]");
+    if (batch == 0) return TP_OK;
+    TP_TRY(need(src, "src"));
+    TP_TRY(need(dst, "dst"));
+    return launched(tp::launch_fftshift_pad(elem_bytes, dim, src, batch, boxsize, padded_boxsize, pad_before, dst,
+                                            static_cast<hipStream_t>(stream)),
+                    "fftshift-pad launch");
+}
+
+int tp_ifftshift_crop(int elem_bytes, const void* src, int64_t batch, int dim, int64_t len0, int64_t len1,
+                      int64_t len2, int64_t crop_start, int64_t crop_len, void* dst, void* stream) {
+    g_err.clear();
+    if (elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8 && elem_bytes != 16)
+        return fail("elem_bytes must be 2, 4, 8 or 16");
+    if (dim != 2 && dim != 3) return fail("dim must be 2 or 3");
+    const int64_t L[3] = {len0, len1, dim == 3 ? len2 : 1};
+    if (batch < 0 || crop_start < 0 || crop_len < 0) return fail("batch, crop_start and crop_len must be >= 0");
+    int64_t m[3] = {1, 1, 1};
+    for (int a = 0; a < dim; ++a) {
+        if (L[a] < 1 || L[a] > (int64_t(1) << 30)) return fail("axis lengths must be in [1, 2^30]");
+        m[a] = std::max<int64_t>(0, std::min(crop_start + crop_len, L[a]) - crop_start);
+    }
+    if (batch == 0 || m[0] * m[1] * m[2] == 0) return TP_OK;
+    TP_TRY(need(src, "src"));
+    TP_TRY(need(dst, "dst"));
+    return launched(tp::launch_ifftshift_crop(elem_bytes, dim, src, batch, L, m, crop_start, dst,
+                                              static_cast<hipStream_t>(stream)),
+                    "ifftshift-crop launch");
+}
+
+int tp_rfftn(int dtype, int dim, int64_t batch, int64_t boxsize, const void* real, void* spectrum, void* stream) {
+    g_err.clear();
+    if (dtype != TP_F32 && dtype != TP_F64) return fail("dtype must be TP_F32 or TP_F64");
+    if (dim != 2 && dim != 3) return fail("dim must be 2 or 3");
+    if (batch < 0 || batch > INT32_MAX || boxsize < 1 || boxsize > INT32_MAX)
+        return fail("batch must be in [0, 2^31) and boxsize in [1, 2^31)");
+    if (batch == 0) return TP_OK;
+    TP_TRY(need(real, "real"));
+    TP_TRY(need(spectrum, "spectrum"));
+    const int r = tp::fft_forward(dtype, dim, batch, boxsize, real, spectrum, static_cast<hipStream_t>(stream));
+    if (r != 0) {
+        g_err = "hipFFT forward transform failed (hipfftResult " + std::to_string(r) + ")";
+        return TP_ERR_HIP;
+    }
+    return TP_OK;
+}
+
+int tp_irfftn(int dtype, int dim, int64_t batch, int64_t boxsize, void* spectrum, void* real, void* stream) {
+    g_err.clear();
+    if (dtype != TP_F32 && dtype != TP_F64) return fail("dtype must be TP_F32 or TP_F64");
+    if (dim != 2 && dim != 3) return fail("dim must be 2 or 3");
+    if (batch < 0 || batch > INT32_MAX || boxsize < 1 || boxsize > INT32_MAX)
+        return fail("batch must be in [0, 2^31) and boxsize in [1, 2^31)");
+    if (batch == 0) return TP_OK;
+    TP_TRY(need(spectrum, "spectrum"));
+    TP_TRY(need(real, "real"));
+    const int r = tp::fft_inverse(dtype, dim, batch, boxsize, spectrum, real, static_cast<hipStream_t>(stream));
+    if (r != 0) {
+        g_err = "hipFFT inverse transform failed (hipfftResult " + std::to_string(r) + ")";
+        return TP_ERR_HIP;
+    }
+    return TP_OK;
+}
+
+int tp_normalize_reconstruction(int dtype, const void* data, const void* weights, int64_t elems, double reg,
+                                void* out, void* stream) {
+    g_err.clear();
+    if (dtype != TP_F32 && dtype != TP_F64) return fail("dtype must be TP_F32 or TP_F64");
+    if (elems < 0) return fail("elems must be >= 0");
+    if (!std::isfinite(reg)) return fail("reg must be finite");
+    if (elems == 0) return TP_OK;
+    TP_TRY(need(data, "data"));
+    TP_TRY(need(weights, "weights"));
+    TP_TRY(need(out, "out"));
+    return launched(tp::launch_normalize(dtype, data, weights, elems, reg, out, static_cast<hipStream_t>(stream)),
+                    "normalisation launch");
 }
 
 }  // extern "C"

@@ -95,6 +95,24 @@ hipError_t launch_scatter2_tiled(bool cubic, int mode, const Geom& g, const Tile
                                  const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
                                  hipStream_t s);
 
+// Reference preparation (tp_fourier.hip).  Elements are opaque words of
+// elem_bytes (2, 4, 8 or 16); `dim` spatial axes (2 or 3) after the batch.
+// src [batch, n^dim] -> dst [batch, N^dim] = fftshift(zero-pad at pad_before).
+hipError_t launch_fftshift_pad(int elem_bytes, int dim, const void* src, int64_t batch, int64_t n, int64_t N,
+                               int64_t pad_before, void* dst, hipStream_t s);
+// src [batch, L[0..dim)] -> dst [batch, m[0..dim)] = ifftshift(src)[crop_start : crop_start + m] per axis.
+hipError_t launch_ifftshift_crop(int elem_bytes, int dim, const void* src, int64_t batch, const int64_t* L,
+                                 const int64_t* m, int64_t crop_start, void* dst, hipStream_t s);
+// out = data / (weights + reg) where weights + reg > 0, else 0; `dt` 0 (fp32) or 1 (fp64).
+hipError_t launch_normalize(int dt, const void* data, const void* weights, int64_t elems, double reg, void* out,
+                            hipStream_t s);
+
+// rfftn / irfftn (norm="forward") of `batch` contiguous N^dim boxes through
+// hipFFT (rocFFT), with cached plans; return a hipfftResult (0 = success).
+// The inverse overwrites its input.
+int fft_forward(int dt, int dim, int64_t batch, int64_t N, const void* real, void* spec, hipStream_t s);
+int fft_inverse(int dt, int dim, int64_t batch, int64_t N, void* spec, void* real, hipStream_t s);
+
 hipError_t launch_backproject_back(int dim, int dt, bool cubic, const Geom& g, const void* gdata, const void* gw,
                                    const void* proj, const void* rot, const void* shifts, void* gproj,
                                    void* gweights, void* grot, void* gshift, hipStream_t s);

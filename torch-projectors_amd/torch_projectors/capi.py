@@ -31,8 +31,20 @@ SIGNATURES = {
     "tp_backproject_2d_to_3d_forw": [_I, _P, _L, _L, _L, _L, _P, _P, _L, _P, _L, _I, _D, _I, _D, _P, _P, _P],
     "tp_backproject_2d_to_3d_back": [_I, _P, _P, _L, _L, _P, _L, _L, _L, _L, _P, _P, _L, _P, _L, _I, _D, _I,
                                      _D, _P, _P, _P, _P, _P],
+    # reference preparation
+    "tp_fftshift_pad": [_I, _P, _L, _I, _L, _L, _L, _P, _P],
+    "tp_ifftshift_crop": [_I, _P, _L, _I, _L, _L, _L, _L, _L, _P, _P],
+    "tp_rfftn": [_I, _I, _L, _L, _P, _P, _P],
+    "tp_irfftn": [_I, _I, _L, _L, _P, _P, _P],
+    "tp_normalize_reconstruction": [_I, _P, _P, _L, _D, _P, _P],
 }
-EXPORTS = ["tp_last_error", "tp_abi_version", "tp_backproject_rec_boxsize", *SIGNATURES]
+# helpers returning a size: name -> argument types
+SIZE_HELPERS = {
+    "tp_backproject_rec_boxsize": [_L, _D],
+    "tp_padded_boxsize": [_L, _D],
+    "tp_cropped_boxsize": [_L, _D],
+}
+EXPORTS = ["tp_last_error", "tp_abi_version", *SIZE_HELPERS, *SIGNATURES]
 
 _lib = None
 
@@ -47,8 +59,10 @@ def lib():
         L.tp_last_error.argtypes = []
         L.tp_abi_version.restype = ctypes.c_int
         L.tp_abi_version.argtypes = []
-        L.tp_backproject_rec_boxsize.restype = ctypes.c_int64
-        L.tp_backproject_rec_boxsize.argtypes = [ctypes.c_int64, ctypes.c_double]
+        for name, argtypes in SIZE_HELPERS.items():
+            f = getattr(L, name)
+            f.restype = ctypes.c_int64
+            f.argtypes = argtypes
         for name, argtypes in SIGNATURES.items():
             f = getattr(L, name)
             f.restype = ctypes.c_int
@@ -65,3 +79,11 @@ def call(name, *args):
 
 def rec_boxsize(n, oversampling):
     return int(lib().tp_backproject_rec_boxsize(int(n), float(oversampling)))
+
+
+def padded_boxsize(n, oversampling):
+    return int(lib().tp_padded_boxsize(int(n), float(oversampling)))
+
+
+def cropped_boxsize(n, oversampling):
+    return int(lib().tp_cropped_boxsize(int(n), float(oversampling)))
