@@ -56,10 +56,10 @@ __global__ __launch_bounds__(kBlock) void k_backproject_forw(Geom g, const Cx<T>
     const T cut2 = T(g.cut2);
     for (int64_t w = blockIdx.x; w < g.work; w += gridDim.x) {
         const int64_t bp = w / g.chunks;
-        const int pix = int(w - bp * g.chunks) * kBlock + int(threadIdx.x);
-        if (pix >= g.npix) continue;
+        int i = 0, j = 0;
+        if (!rect_pixel(g, int(w - bp * g.chunks) * kBlock + int(threadIdx.x), i, j)) continue;
+        const int pix = i * g.hp + j;
         const int64_t b = bp / g.P, p = bp - b * g.P;
-        const int i = pix / g.hp, j = pix - i * g.hp;
         const T r = freq_of<T>(i, g.n), c = T(j);
         if (filtered(r, c, cut2) || (j == 0 && i >= g.n / 2)) continue;
         const T* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * RS;
@@ -86,8 +86,10 @@ __global__ __launch_bounds__(kBlock) void k_backproject_forw_rest(Geom g, const 
         const float* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * RS;
         if (pose_is_rotation_d<DIM>(R)) continue;
         const float* S = shifts ? shifts + ((g.B_shift == 1 ? 0 : b) * g.P + p) * 2 : nullptr;
-        for (int pix = threadIdx.x; pix < g.npix; pix += kBlock) {
-            const int i = pix / g.hp, j = pix - i * g.hp;
+        for (int q = threadIdx.x; q < g.rect; q += kBlock) {
+            int i, j;
+            rect_pixel(g, q, i, j);
+            const int pix = i * g.hp + j;
             const float r = freq_of<float>(i, g.n), c = float(j);
             if (filtered(r, c, cut2) || (j == 0 && i >= g.n / 2)) continue;
             const int64_t pidx = bp * g.npix + pix;
@@ -114,14 +116,15 @@ __global__ __launch_bounds__(kBlock) void k_backproject_back(Geom g, const Cx<T>
     const T cut2 = T(g.cut2);
     for (int64_t w = blockIdx.x; w < g.work; w += gridDim.x) {
         const int64_t bp = w / g.chunks;
-        const int pix = int(w - bp * g.chunks) * kBlock + int(threadIdx.x);
+        int i = 0, j = 0;
+        const bool in_rect = rect_pixel(g, int(w - bp * g.chunks) * kBlock + int(threadIdx.x), i, j);
+        const int pix = i * g.hp + j;
         const int64_t b = bp / g.P, p = bp - b * g.P;
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
         T acc[K];
 #pragma unroll
         for (int k = 0; k < K; ++k) acc[k] = T(0);
-        if (pix < g.npix) {
-            const int i = pix / g.hp, j = pix - i * g.hp;
+        if (in_rect) {
             const T r = freq_of<T>(i, g.n), c = T(j);
             const int64_t pidx = bp * g.npix + pix;
             Cx<T> out = {0, 0};
@@ -205,7 +208,9 @@ hipError_t back8(const Geom& g, const void* gdata, const void* gw, const void* p
     hipLaunchKernelGGL((k_backproject_back<DIM, T, CUBIC, WG, ROT, SHIFT>), dim3(grid_for(g.work)), dim3(kBlock), 0,
                        s, g, (const Cx<T>*)gdata, (const T*)gw, (const Cx<T>*)proj, (const T*)rot, (const T*)shifts,
                        (Cx<T>*)gproj, (T*)gweights, (T*)grot, (T*)gshift);
-    return hipGetLastError();
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_zero_outside(sizeof(T) == 4 ? 0 : 1, g, gproj, gweights, s);
 }
 
 template <int DIM, typename T, bool CUBIC, bool WG>
@@ -251,7 +256,63 @@ __global__ __launch_bounds__(kBlock) void k_zero(uint32_t* __restrict__ p, int64
     for (int64_t k = head + quads * 4 + t; k < words; k += stride) p[k] = 0u;
 }
 
+// Zero elements [lo, hi) of a 4- or 8-byte-element array with 16-byte stores
+// over the 16-byte-aligned middle; the threads of one block share the span.
+template <typename E>
+__device__ __forceinline__ void zero_span(E* __restrict__ p, int64_t lo, int64_t hi) {
+    constexpr int V = 16 / sizeof(E);
+    const int skip = int(((16 - (reinterpret_cast<uintptr_t>(p + lo) & 15)) & 15) / sizeof(E));
+    int64_t a = lo + skip;
+    if (a > hi) a = hi;
+    const int64_t z = a + (hi - a) / V * V;
+    for (int64_t k = lo + threadIdx.x; k < a; k += kBlock) p[k] = E{};
+    uint4* q = reinterpret_cast<uint4*>(p + a);
+    for (int64_t k = threadIdx.x; k < (z - a) / V; k += kBlock) q[k] = make_uint4(0u, 0u, 0u, 0u);
+    for (int64_t k = z + threadIdx.x; k < hi; k += kBlock) p[k] = E{};
+}
+
+// Zeros on every pixel outside the active rectangle, one block per pose: the
+// rows outside its row range are one contiguous span (rows rmax+1 .. n+rr0-1
+// of the grid order), written with 16-byte stores; the columns past the
+// rectangle on the rows inside, one wave per row.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_zero_outside(Geom g, Cx<T>* __restrict__ out, T* __restrict__ wout) {
+    const int rmax = g.rr0 + g.rnr - 1;
+    const int i_lo = rmax + 1, i_hi = g.n + g.rr0;  // grid rows i in [i_lo, i_hi) are outside
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int64_t bp = blockIdx.x; bp < g.B * g.P; bp += gridDim.x) {
+        const int64_t base = bp * g.npix;
+        if (i_hi > i_lo) {
+            constexpr int W = sizeof(Cx<T>) / 8;  // 8-byte words per complex element
+            if (out)
+                zero_span(reinterpret_cast<uint2*>(out + base), int64_t(i_lo) * g.hp * W, int64_t(i_hi) * g.hp * W);
+            if (wout) zero_span(wout + base, int64_t(i_lo) * g.hp, int64_t(i_hi) * g.hp);
+        }
+        if (g.rnc < g.hp) {
+            for (int kr = wave; kr < g.rnr; kr += kBlock / 64) {
+                const int r = g.rr0 + kr, i = r >= 0 ? r : r + g.n;
+                const int64_t row = base + int64_t(i) * g.hp;
+                for (int j = g.rnc + lane; j < g.hp; j += 64) {
+                    if (out) out[row + j] = Cx<T>{T(0), T(0)};
+                    if (wout) wout[row + j] = T(0);
+                }
+            }
+        }
+    }
+}
+
 }  // namespace
+
+hipError_t launch_zero_outside(int dt, const Geom& g, void* out, void* wout, hipStream_t s) {
+    if (g.rect == g.npix || (!out && !wout) || g.B * g.P == 0) return hipSuccess;
+    const unsigned grid = unsigned(g.B * g.P < 65536 ? g.B * g.P : 65536);
+    if (dt == 0)
+        hipLaunchKernelGGL(k_zero_outside<float>, dim3(grid), dim3(kBlock), 0, s, g, (Cx<float>*)out, (float*)wout);
+    else
+        hipLaunchKernelGGL(k_zero_outside<double>, dim3(grid), dim3(kBlock), 0, s, g, (Cx<double>*)out,
+                           (double*)wout);
+    return hipGetLastError();
+}
 
 hipError_t launch_zero(void* p, int64_t words, hipStream_t s) {
     if (words <= 0) return hipSuccess;

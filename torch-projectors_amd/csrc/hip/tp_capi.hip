@@ -51,8 +51,6 @@ int set_proj(int64_t n, tp::Geom& g) {
     g.n = int(n);
     g.hp = int(hp);
     g.npix = int(n * hp);
-    g.chunks = int((g.npix + tp::kBlock - 1) / tp::kBlock);
-    g.work = g.B * g.P * g.chunks;
     g.phase_k = -2.0 * M_PI / double(n);
     return TP_OK;
 }
@@ -79,6 +77,19 @@ void set_cut(int dtype, int has_cut, double cut, tp::Geom& g) {
     } else {
         g.cut2 = radius * radius;
     }
+    // Active rectangle: |r|, c <= floor(sqrt(cut2)) + 2 covers every pixel the
+    // mask keeps (r^2 + c^2 <= cut2 in the real type); the whole grid when the
+    // radius is not finite or reaches past the grid.
+    const int lo = g.n / 2 + 1 - g.n, hi = g.n / 2;
+    int cl = hi + 1;
+    if (std::isfinite(g.cut2) && g.cut2 < double(hi + 1) * double(hi + 1))
+        cl = int(std::floor(std::sqrt(g.cut2))) + 2;
+    g.rr0 = std::max(lo, -cl);
+    g.rnr = std::min(hi, cl) - g.rr0 + 1;
+    g.rnc = std::min(g.hp, cl + 1);
+    g.rect = g.rnr * g.rnc;
+    g.chunks = (g.rect + tp::kBlock - 1) / tp::kBlock;
+    g.work = g.B * g.P * g.chunks;
 }
 
 int64_t rec_box(int64_t n, double os) {

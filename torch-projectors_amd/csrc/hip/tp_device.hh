@@ -406,6 +406,17 @@ __device__ __forceinline__ T weight_grad_interp(const T* __restrict__ g, int N, 
 }
 
 // ---------------------------------------------------------------- per-pixel geometry
+// Pixel q of a pose's active rectangle (Geom::rr0, rnr, rnc): grid row i and
+// column j, or false past the rectangle.
+__device__ __forceinline__ bool rect_pixel(const Geom& g, int q, int& i, int& j) {
+    if (q >= g.rect) return false;
+    const int kr = q / g.rnc;
+    j = q - kr * g.rnc;
+    const int r = g.rr0 + kr;
+    i = r >= 0 ? r : r + g.n;
+    return true;
+}
+
 // Row index -> signed frequency (projection_utils.h:61-64).
 template <typename T> __device__ __forceinline__ T freq_of(int i, int n) { return i <= n / 2 ? T(i) : T(i - n); }
 // Radius mask (projection_utils.h:69-76): r^2 + c^2 > cutoff^2 in the real type.

@@ -18,7 +18,11 @@ struct Geom {
     double os;                     // oversampling
     double phase_k;                // -2*pi/n, in double (projection_utils.h:82-94)
     double cut2;                   // squared radius cutoff, rounded in the real type
-    int chunks;                    // 256-pixel blocks per pose
+    // Pixels that can be active (inside the cutoff disc) lie in a rectangle of
+    // the grid: row frequencies [rr0, rr0 + rnr), columns [0, rnc).  The
+    // per-pixel kernels walk only its rect = rnr * rnc pixels.
+    int rr0, rnr, rnc, rect;
+    int chunks;                    // 256-pixel blocks of the rectangle per pose
     int64_t work;                  // B*P*chunks
 };
 
@@ -64,6 +68,9 @@ inline unsigned grid_for(int64_t work) { return unsigned(work < kMaxGrid ? work 
 
 // Zero `words` 32-bit words at p.
 hipError_t launch_zero(void* p, int64_t words, hipStream_t s);
+// Zero every pixel outside the active rectangle of [B, P, n, n/2+1] outputs
+// (out complex, wout real; either may be null).
+hipError_t launch_zero_outside(int dt, const Geom& g, void* out, void* wout, hipStream_t s);
 
 // Kernel launchers; `dim` is 2 or 3, `dt` 0 (fp32) or 1 (fp64).
 // `rest_only` (fp32 3D): only masked pixels and poses that are not rotations.

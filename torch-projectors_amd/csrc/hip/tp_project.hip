@@ -40,10 +40,10 @@ __global__ __launch_bounds__(kBlock) void k_project_forw(Geom g, const Cx<T>* __
     const T cut2 = T(g.cut2);
     for (int64_t w = blockIdx.x; w < g.work; w += gridDim.x) {
         const int64_t bp = w / g.chunks;
-        const int pix = int(w - bp * g.chunks) * kBlock + int(threadIdx.x);
-        if (pix >= g.npix) continue;
+        int i = 0, j = 0;
+        if (!rect_pixel(g, int(w - bp * g.chunks) * kBlock + int(threadIdx.x), i, j)) continue;
+        const int pix = i * g.hp + j;
         const int64_t b = bp / g.P, p = bp - b * g.P;
-        const int i = pix / g.hp, j = pix - i * g.hp;
         const T r = freq_of<T>(i, g.n), c = T(j);
         Cx<T> v = {0, 0};
         if (!filtered(r, c, cut2)) {
@@ -101,7 +101,9 @@ __global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __
     const T cut2 = T(g.cut2);
     for (int64_t w = blockIdx.x; w < g.work; w += gridDim.x) {
         const int64_t bp = w / g.chunks;
-        const int pix = int(w - bp * g.chunks) * kBlock + int(threadIdx.x);
+        int i = 0, j = 0;
+        const bool in_rect = rect_pixel(g, int(w - bp * g.chunks) * kBlock + int(threadIdx.x), i, j);
+        const int pix = i * g.hp + j;
         const int64_t b = bp / g.P, p = bp - b * g.P;
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
         bool scatter = true;
@@ -112,8 +114,7 @@ __global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __
         T acc[K];
 #pragma unroll
         for (int k = 0; k < K; ++k) acc[k] = T(0);
-        if (pix < g.npix) {
-            const int i = pix / g.hp, j = pix - i * g.hp;
+        if (in_rect) {
             const T r = freq_of<T>(i, g.n), c = T(j);
             // masked pixels and the Friedel half of the x = 0 line are skipped
             if (!filtered(r, c, cut2) && !(j == 0 && i >= g.n / 2)) {
@@ -170,7 +171,9 @@ template <int DIM, typename T, bool CUBIC>
 hipError_t forw(const Geom& g, const void* rec, const void* rot, const void* shifts, void* out, hipStream_t s) {
     hipLaunchKernelGGL((k_project_forw<DIM, T, CUBIC>), dim3(grid_for(g.work)), dim3(kBlock), 0, s, g,
                        (const Cx<T>*)rec, (const T*)rot, (const T*)shifts, (Cx<T>*)out);
-    return hipGetLastError();
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_zero_outside(sizeof(T) == 4 ? 0 : 1, g, out, nullptr, s);
 }
 
 template <bool CUBIC>
