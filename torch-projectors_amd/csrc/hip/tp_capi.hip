@@ -151,6 +151,7 @@ tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
     ts.rho = float(rho);
     ts.os = float(g.os);
     ts.inv_os = float(1.0 / g.os);
+    ts.os_exact = double(float(g.os)) == g.os;
     ts.smax = float(g.os * (g.n + 2));
     // Slack of the sample boxes: the row and half-plane bounds use the
     // rotation's orthonormality (off by at most kRotationTol * |sc, sr| each),

@@ -46,6 +46,7 @@ struct TileSpec {
     float smax;               // bound on |c*os| over the pixel grid
     int cmax, rmin, rmax;     // pixel-grid limits of c and r (grid and cutoff)
     int kp_forw, kp_scatter;  // poses per wavefront batch (1, 2 or 4)
+    bool os_exact;            // float(os) == os: c * os can be formed in float exactly as in double
 };
 
 // Tile-owner scatter of the fp32 2D operators (tp_tiled2d.hip).

@@ -119,8 +119,11 @@ __device__ __forceinline__ void row_span(const float* R, int r, const float* lo,
 // Sample position of pixel (r, c): rotate<3> without its R[k][2] * 0 terms.
 // Adding that signed zero to the other two terms can only flip the sign of a
 // zero coordinate, which floors to the same cell with the same fraction.
+// OSX: os is a float value (float(os) == os), so c * os is exact in double and
+// float(double(c) * os) is the correctly rounded float product c * float(os).
+template <bool OSX>
 __device__ __forceinline__ void rotate_slice(const float* __restrict__ R, float r, float c, double os, float* x) {
-    const float sc = float(double(c) * os), sr = float(double(r) * os);
+    const float sc = OSX ? c * float(os) : float(double(c) * os), sr = OSX ? r * float(os) : float(double(r) * os);
     x[0] = R[0] * sc + R[1] * sr;
     x[1] = R[3] * sc + R[4] * sr;
     x[2] = R[6] * sc + R[7] * sr;
@@ -147,11 +150,12 @@ __device__ __forceinline__ void q_fill(unsigned* q, int r, int c0, int cnt, int 
     __builtin_amdgcn_wave_barrier();
 }
 
-// Per-wave copy of the poses of one batch.
+// Per-wave copy of the poses of one batch; `base` is the pose's first pixel
+// in the [B, P, n, n/2+1] projections.
 struct Slot {
     float R[9];
     float s0, s1;
-    int p;
+    int64_t base;
 };
 
 __device__ __forceinline__ void load_rot(const float* __restrict__ Rg, float* R) {
@@ -286,7 +290,7 @@ __device__ __forceinline__ void cull_chunk_boxes(const float* __restrict__ rotb,
 }
 
 // ----------------------------------------------------------------------------- forward
-template <bool CUBIC, int KP>
+template <bool CUBIC, int KP, bool OSX>
 __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ rec,
                                                         const float* __restrict__ rot,
                                                         const float* __restrict__ shifts,
@@ -398,7 +402,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                     for (int e = 0; e < 9; ++e) sd.R[e] = R[e];
                     sd.s0 = Sh[0];
                     sd.s1 = Sh[1];
-                    sd.p = pp;
+                    sd.base = (b * g.P + pp) * int64_t(g.npix);
                 }
                 __builtin_amdgcn_wave_barrier();
                 int r0, r1;
@@ -428,7 +432,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                         const float fr = float(rr), fc = float(cc);
                         if (filtered(fr, fc, cut2)) continue;
                         float x[3];
-                        rotate_slice(sd.R, fr, fc, g.os, x);
+                        rotate_slice<OSX>(sd.R, fr, fc, g.os, x);
                         const int fxc = int(floorf(x[0])), fxr = int(floorf(x[1])), fxd = int(floorf(x[2]));
                         if (fxc < tc || fxc >= tc + L || fxr < tr || fxr >= tr + L || fxd < td || fxd >= td + LD)
                             continue;
@@ -436,7 +440,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                                             : lerp3<float, false, false>(lds, x[2], x[1], x[0]).v;
                         if (shifts) v = cmul(v, phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k));
                         const int i = rr >= 0 ? rr : rr + g.n;
-                        out[(b * g.P + sd.p) * int64_t(g.npix) + i * g.hp + cc] = v;
+                        out[sd.base + i * g.hp + cc] = v;
                       }
                     }
                 }
@@ -472,14 +476,14 @@ struct TapMap {
     int lmin[3];
 };
 
-template <bool CUBIC, int MODE, bool WEIGHTS>
+template <bool CUBIC, int MODE, bool WEIGHTS, bool OSX>
 __device__ __forceinline__ void scatter_sample(const Geom& g, const Slot& sd, int rr, int cc, Cx<float> v, float wpix,
                                                bool shifted, bool flip, const TapMap& tm, double* acc_re,
                                                double* acc_im, double* acc_w) {
     constexpr int K = CUBIC ? 4 : 2, LOW = CUBIC ? 1 : 0;  // taps at floor(x) - LOW + j, j < K
     const float fr = float(rr), fc = float(cc);
     float x[3];
-    rotate_slice(sd.R, fr, fc, g.os, x);
+    rotate_slice<OSX>(sd.R, fr, fc, g.os, x);
     if (shifted) {
         if (MODE == 0) v = cmul(v, cconj(phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k)));
         else v = cmul(v, phase_hw(-fr, -fc, sd.s0, sd.s1, g.phase_k));
@@ -528,7 +532,7 @@ __device__ __forceinline__ void scatter_sample(const Geom& g, const Slot& sd, in
 
 // MODE 0: backprojection, v = proj * conj(phase(r, c)), optional weights.
 // MODE 1: reconstruction gradient of the projection, v = g * phase(-r, -c).
-template <bool CUBIC, int MODE, bool WEIGHTS, int KP>
+template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool OSX>
 __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_scatter3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ src,
                                                            const float* __restrict__ weights,
                                                            const float* __restrict__ rot,
@@ -628,7 +632,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                         for (int e = 0; e < 9; ++e) sd.R[e] = R[e];
                         sd.s0 = Sh[0];
                         sd.s1 = Sh[1];
-                        sd.p = pp;
+                        sd.base = (pose0 + pp) * int64_t(g.npix);
                     }
                     __builtin_amdgcn_wave_barrier();
                     {
@@ -662,7 +666,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                             ok = ok && !filtered(float(rr), float(cc), cut2) &&
                                  !(cc == 0 && (rr == g.n / 2 || rr < 0));  // Friedel half of x = 0
                             const int i = rr >= 0 ? rr : rr + g.n;
-                            const int64_t pidx = (pose0 + sd.p) * int64_t(g.npix) + i * g.hp + cc;
+                            const int64_t pidx = sd.base + i * g.hp + cc;
                             v = ok ? src[pidx] : Cx<float>{0.f, 0.f};
                             wv = (WEIGHTS && ok) ? weights[pidx] : 0.f;
                         };
@@ -679,7 +683,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                             float wv2 = 0.f;
                             if (e0 + 64 < total) fetch_sample(e0 + 64, rr2, cc2, sl2, ok2, v2, wv2);
                             if (ok)
-                                scatter_sample<CUBIC, MODE, WEIGHTS>(g, slots[wave][sl], rr, cc, v, wv,
+                                scatter_sample<CUBIC, MODE, WEIGHTS, OSX>(g, slots[wave][sl], rr, cc, v, wv,
                                                                      shifts != nullptr, pass == 1, tm, acc_re,
                                                                      acc_im, acc_w);
                             rr = rr2;
@@ -770,17 +774,17 @@ __global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<fl
     }
 }
 
-template <bool CUBIC, int KP>
+template <bool CUBIC, int KP, bool OSX>
 hipError_t forw_launch(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts,
                        void* out, hipStream_t s) {
     const int64_t fcore = int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fd1 - ts.fd0) * ts.ksplit;
     const int64_t work = g.B * (fcore + int64_t(ts.nt) * ts.nt * ts.ntfd);
-    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP>), dim3(grid_for(kXcds * xcd_per<kRunForw>(work))), dim3(kForwThreads), 0, s, g, ts,
+    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP, OSX>), dim3(grid_for(kXcds * xcd_per<kRunForw>(work))), dim3(kForwThreads), 0, s, g, ts,
                        (const Cx<float>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
     return hipGetLastError();
 }
 
-template <bool CUBIC, int MODE, bool WEIGHTS, int KP>
+template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool OSX>
 hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
                           const void* shifts, void* dst, void* wdst, hipStream_t s) {
     const int64_t score = int64_t(ts.sd1 - ts.sd0) * (ts.sr1 - ts.sr0) * ts.sc1 * ts.ksplit;
@@ -794,7 +798,7 @@ hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, co
         if (ez != hipSuccess) return ez;
     }
     const int64_t work = g.B * (score + int64_t(ts.ntd) * ts.ntr * ts.ntc);
-    hipLaunchKernelGGL((k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP>), dim3(grid_for(kXcds * xcd_per<kRunScatter>(work))),
+    hipLaunchKernelGGL((k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP, OSX>), dim3(grid_for(kXcds * xcd_per<kRunScatter>(work))),
                        dim3(kScatterThreads), 0, s, g,
                        ts, (const Cx<float>*)src, (const float*)weights, (const float*)rot, (const float*)shifts,
                        (Cx<float>*)dst, (float*)wdst);
@@ -808,28 +812,40 @@ hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, co
     return hipGetLastError();
 }
 
+template <bool CUBIC, int MODE, bool WEIGHTS, bool OSX>
+hipError_t scatter_kp_osx(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
+                          const void* shifts, void* dst, void* wdst, hipStream_t s) {
+    if (ts.kp_scatter >= 4)
+        return scatter_launch<CUBIC, MODE, WEIGHTS, 4, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    if (ts.kp_scatter == 2)
+        return scatter_launch<CUBIC, MODE, WEIGHTS, 2, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    return scatter_launch<CUBIC, MODE, WEIGHTS, 1, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+}
+
 template <bool CUBIC, int MODE, bool WEIGHTS>
 hipError_t scatter_kp(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
                       const void* shifts, void* dst, void* wdst, hipStream_t s) {
-    if (ts.kp_scatter >= 4)
-        return scatter_launch<CUBIC, MODE, WEIGHTS, 4>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-    if (ts.kp_scatter == 2)
-        return scatter_launch<CUBIC, MODE, WEIGHTS, 2>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-    return scatter_launch<CUBIC, MODE, WEIGHTS, 1>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    if (ts.os_exact) return scatter_kp_osx<CUBIC, MODE, WEIGHTS, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    return scatter_kp_osx<CUBIC, MODE, WEIGHTS, false>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+}
+
+template <bool CUBIC, bool OSX>
+hipError_t forw_kp(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts, void* out,
+                   hipStream_t s) {
+    if (ts.kp_forw >= 4) return forw_launch<CUBIC, 4, OSX>(g, ts, rec, rot, shifts, out, s);
+    if (ts.kp_forw == 2) return forw_launch<CUBIC, 2, OSX>(g, ts, rec, rot, shifts, out, s);
+    return forw_launch<CUBIC, 1, OSX>(g, ts, rec, rot, shifts, out, s);
 }
 
 }  // namespace
 
 hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* rec,
                                       const void* rot, const void* shifts, void* out, hipStream_t s) {
-    if (cubic) {
-        if (ts.kp_forw >= 4) return forw_launch<true, 4>(g, ts, rec, rot, shifts, out, s);
-        if (ts.kp_forw == 2) return forw_launch<true, 2>(g, ts, rec, rot, shifts, out, s);
-        return forw_launch<true, 1>(g, ts, rec, rot, shifts, out, s);
-    }
-    if (ts.kp_forw >= 4) return forw_launch<false, 4>(g, ts, rec, rot, shifts, out, s);
-    if (ts.kp_forw == 2) return forw_launch<false, 2>(g, ts, rec, rot, shifts, out, s);
-    return forw_launch<false, 1>(g, ts, rec, rot, shifts, out, s);
+    if (cubic)
+        return ts.os_exact ? forw_kp<true, true>(g, ts, rec, rot, shifts, out, s)
+                           : forw_kp<true, false>(g, ts, rec, rot, shifts, out, s);
+    return ts.os_exact ? forw_kp<false, true>(g, ts, rec, rot, shifts, out, s)
+                       : forw_kp<false, false>(g, ts, rec, rot, shifts, out, s);
 }
 
 hipError_t launch_scatter3_tiled(bool cubic, int mode, const Geom& g, const TileSpec& ts, const void* src,
