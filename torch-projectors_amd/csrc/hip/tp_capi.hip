@@ -281,16 +281,19 @@ int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, in
     TP_TRY(need(gproj, "grad_projections"));
     TP_TRY(need(rec, "reconstruction"));
     TP_TRY(need(rot, "rotations"));
-    if (tiles)
-        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 1, g, tile_spec(g, cubic), gproj, nullptr, rot, shifts, grec,
-                                                  nullptr, s),
+    if (tiles) {
+        const tp::TileSpec ts = tile_spec(g, cubic);
+        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, s),
                         "tiled reconstruction-gradient launch"));
+        TP_TRY(launched(tp::launch_grads3_tiled(cubic, g, ts, gproj, rec, rot, shifts, grot, gshift, s),
+                        "tiled rotation/shift-gradient launch"));
+    }
     if (tiles2)
         TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 1, g, tile_spec2(g, cubic), gproj, nullptr, rot, shifts,
                                                   grec, nullptr, s),
                         "tiled reconstruction-gradient launch"));
     return launched(tp::launch_project_back(dim, dtype, cubic, g, gproj, rec, rot, shifts, grec, grot, gshift, s,
-                                            tiles || tiles2),
+                                            (tiles || tiles2) ? 1 : 0),
                     "projection backward launch");
 }
 

@@ -77,11 +77,12 @@ hipError_t launch_zero_outside(int dt, const Geom& g, void* out, void* wout, hip
 // `rest_only` (fp32 3D): only masked pixels and poses that are not rotations.
 hipError_t launch_project_forw(int dim, int dt, bool cubic, const Geom& g, const void* rec, const void* rot,
                                const void* shifts, void* out, hipStream_t s, bool rest_only = false);
-// `rest_only` (fp32 2D and 3D): the reconstruction-gradient scatter only for poses
-// that are not rotations; rotation/shift gradients for all poses.
+// `rest` != 0 (fp32): poses that are rotations are left to the tiled kernels.
+// 2D: their reconstruction-gradient scatter only (rotation/shift gradients here
+// for all poses); 3D: everything (launch_grads3_tiled gives their gradients).
 hipError_t launch_project_back(int dim, int dt, bool cubic, const Geom& g, const void* gproj, const void* rec,
                                const void* rot, const void* shifts, void* grec, void* grot, void* gshift,
-                               hipStream_t s, bool rest_only = false);
+                               hipStream_t s, int rest = 0);
 // `rest_only` (fp32 2D and 3D): only poses that are not rotations.
 hipError_t launch_backproject_forw(int dim, int dt, bool cubic, const Geom& g, const void* proj, const void* weights,
                                    const void* rot, const void* shifts, void* data, void* wrec, hipStream_t s,
@@ -90,6 +91,10 @@ hipError_t launch_backproject_forw(int dim, int dt, bool cubic, const Geom& g, c
 // `rest_only` complete the other poses and the masked pixels).
 hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* rec,
                                       const void* rot, const void* shifts, void* out, hipStream_t s);
+// Rotation/shift gradients of project_3d_to_2d_back for rotation poses, added
+// into zero-filled grot / gshift (either may be null).
+hipError_t launch_grads3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gproj, const void* rec,
+                               const void* rot, const void* shifts, void* grot, void* gshift, hipStream_t s);
 // mode 0: backprojection into data (+ weights), with the x = 0 Hermitian completion;
 // mode 1: reconstruction gradient of the projection.
 hipError_t launch_scatter3_tiled(bool cubic, int mode, const Geom& g, const TileSpec& ts, const void* src,

@@ -88,9 +88,11 @@ __global__ __launch_bounds__(kBlock) void k_project3_forw_rest(Geom g, const Cx<
 // with out-of-range taps dropped and no x = 0 mirror
 // (projection_utils.h:336-362, 414-443).  Rotation and shift gradients are
 // per-pose sums, reduced across the block before one atomic per component.
-// REST (fp32): the reconstruction gradient of rotation poses comes from the
-// tiled scatter; only the other poses are scattered here.
-template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT, bool REST>
+// REST (fp32) 1: the reconstruction gradient of rotation poses comes from the
+// tiled scatter; only the other poses are scattered here.  REST 2: the tiled
+// kernels also give the rotation/shift gradients of rotation poses, which are
+// skipped here entirely.
+template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT, int REST>
 __global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __restrict__ gproj,
                                                          const Cx<T>* __restrict__ rec, const T* __restrict__ rot,
                                                          const T* __restrict__ shifts, Cx<T>* __restrict__ grec,
@@ -107,9 +109,9 @@ __global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __
         const int64_t b = bp / g.P, p = bp - b * g.P;
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
         bool scatter = true;
-        if constexpr (REST) {
+        if constexpr (REST != 0) {
             scatter = !pose_is_rotation_d<DIM>(rot + (rb * g.P + p) * RS);
-            if (!scatter && !ROT && !SHIFT) continue;  // block-uniform
+            if (!scatter && (REST == 2 || (!ROT && !SHIFT))) continue;  // block-uniform
         }
         T acc[K];
 #pragma unroll
@@ -183,7 +185,7 @@ hipError_t forw_rest(const Geom& g, const void* rec, const void* rot, const void
     return hipGetLastError();
 }
 
-template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT, bool REST>
+template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT, int REST>
 hipError_t back4(const Geom& g, const void* gproj, const void* rec, const void* rot, const void* shifts, void* grec,
                  void* grot, void* gshift, hipStream_t s) {
     hipLaunchKernelGGL((k_project_back<DIM, T, CUBIC, ROT, SHIFT, REST>), dim3(grid_for(g.work)), dim3(kBlock), 0,
@@ -192,7 +194,7 @@ hipError_t back4(const Geom& g, const void* gproj, const void* rec, const void* 
     return hipGetLastError();
 }
 
-template <int DIM, typename T, bool CUBIC, bool REST = false>
+template <int DIM, typename T, bool CUBIC, int REST = 0>
 hipError_t back(const Geom& g, const void* gproj, const void* rec, const void* rot, const void* shifts, void* grec,
                 void* grot, void* gshift, hipStream_t s) {
     if (grot && gshift)
@@ -223,13 +225,13 @@ hipError_t launch_project_forw(int dim, int dt, bool cubic, const Geom& g, const
 
 hipError_t launch_project_back(int dim, int dt, bool cubic, const Geom& g, const void* gproj, const void* rec,
                                const void* rot, const void* shifts, void* grec, void* grot, void* gshift,
-                               hipStream_t s, bool rest_only) {
-    if (rest_only && dt == 0) {
+                               hipStream_t s, int rest) {
+    if (rest != 0 && dt == 0) {
         if (dim == 2)
-            return cubic ? back<2, float, true, true>(g, gproj, rec, rot, shifts, grec, grot, gshift, s)
-                         : back<2, float, false, true>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
-        return cubic ? back<3, float, true, true>(g, gproj, rec, rot, shifts, grec, grot, gshift, s)
-                     : back<3, float, false, true>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+            return cubic ? back<2, float, true, 1>(g, gproj, rec, rot, shifts, grec, grot, gshift, s)
+                         : back<2, float, false, 1>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+        return cubic ? back<3, float, true, 2>(g, gproj, rec, rot, shifts, grec, grot, gshift, s)
+                     : back<3, float, false, 2>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
     }
     TP_DISPATCH(dim, dt, cubic, back, g, gproj, rec, rot, shifts, grec, grot, gshift, s);
 }

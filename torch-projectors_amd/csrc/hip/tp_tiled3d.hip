@@ -290,11 +290,66 @@ __device__ __forceinline__ void cull_chunk_boxes(const float* __restrict__ rotb,
 }
 
 // ----------------------------------------------------------------------------- forward
-template <bool CUBIC, int KP, bool OSX>
+// GMODE 0: forward projection into `out`.
+// GMODE 1: rotation and shift gradients of project_3d_to_2d_back for rotation
+//          poses (KP = 1): each owned sample's value and spatial gradient
+//          from the staged tile, paired with grad_projections `gsrc` as in
+//          cpu/3d/projection_3d_to_2d_kernels.cpp:344-379; a wave sums its
+//          pose's terms and adds them to grot / gshift (either may be null).
+constexpr double kTwoPi = 6.283185307179586476925286766559;
+
+// Tricubic value and spatial gradient for the gradient sums (which carry the
+// 1e-4 bar, not bit-identity): the 64 taps are reduced along c first (value
+// and d/dc weights), then r, then d, instead of forming the four triple
+// products per tap.  Weights and taps as cubic3 (interpolation_kernels.h:345-425).
+template <typename F>
+__device__ __forceinline__ Interp<float> cubic3_grads(F&& fetch, float d, float r, float c) {
+    float dx, rx, cx;
+    const int df = split_as<false>(d, dx), rf = split_as<false>(r, rx), cf = split_as<false>(c, cx);
+    float wc[4], dwc[4], wr[4], dwr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        wc[j] = cubic_w<float>(cx - float(j - 1));
+        dwc[j] = cubic_dw<float>(cx - float(j - 1));
+        wr[j] = cubic_w<float>(rx - float(j - 1));
+        dwr[j] = cubic_dw<float>(rx - float(j - 1));
+    }
+    Interp<float> o;
+    o.v = o.g[0] = o.g[1] = o.g[2] = {0.f, 0.f};
+#pragma unroll 1
+    for (int k = 0; k < 4; ++k) {
+        Cx<float> pv = {0.f, 0.f}, pc = {0.f, 0.f}, pr = {0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            Cx<float> a = {0.f, 0.f}, bc = {0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const Cx<float> t = fetch(df + k - 1, rf + i - 1, cf + j - 1);
+                a = cadd(a, cscale(t, wc[j]));
+                bc = cadd(bc, cscale(t, dwc[j]));
+            }
+            pv = cadd(pv, cscale(a, wr[i]));
+            pc = cadd(pc, cscale(bc, wr[i]));
+            pr = cadd(pr, cscale(a, dwr[i]));
+        }
+        const float wd = cubic_w<float>(dx - float(k - 1)), dwd = cubic_dw<float>(dx - float(k - 1));
+        o.v = cadd(o.v, cscale(pv, wd));
+        o.g[0] = cadd(o.g[0], cscale(pc, wd));
+        o.g[1] = cadd(o.g[1], cscale(pr, wd));
+        o.g[2] = cadd(o.g[2], cscale(pv, dwd));
+    }
+    return o;
+}
+
+template <bool CUBIC, int KP, bool OSX, int GMODE = 0>
 __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ rec,
                                                         const float* __restrict__ rot,
                                                         const float* __restrict__ shifts,
-                                                        Cx<float>* __restrict__ out) {
+                                                        Cx<float>* __restrict__ out,
+                                                        const Cx<float>* __restrict__ gsrc = nullptr,
+                                                        float* __restrict__ grot = nullptr,
+                                                        float* __restrict__ gshift = nullptr) {
+    static_assert(GMODE == 0 || KP == 1, "the gradient mode sums one pose per wave batch");
     constexpr int LO = CUBIC ? 1 : 0, HI = CUBIC ? 2 : 1, W = L + LO + HI, WD = LD + LO + HI, W3 = W * W * WD;
     constexpr int RPS = 64 / KP;
     constexpr int NT = kForwThreads, NW = NT / 64;
@@ -405,6 +460,9 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                     sd.base = (b * g.P + pp) * int64_t(g.npix);
                 }
                 __builtin_amdgcn_wave_barrier();
+                float acc[11];  // GMODE 1: this lane's share of the pose's 9 rotation and 2 shift sums
+#pragma unroll
+                for (int k = 0; k < 11; ++k) acc[k] = 0.f;
                 int r0, r1;
                 box_rows(R, lo, hi, ts, r0, r1);
                 const int nr = sv ? max(0, r1 - r0 + 1) : 0;
@@ -431,17 +489,64 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                         const Slot& sd = slots[wave][sl];
                         const float fr = float(rr), fc = float(cc);
                         if (filtered(fr, fc, cut2)) continue;
+                        // the backward skips the Friedel half of the x = 0 line
+                        if (GMODE == 1 && cc == 0 && (rr == g.n / 2 || rr < 0)) continue;
                         float x[3];
                         rotate_slice<OSX>(sd.R, fr, fc, g.os, x);
                         const int fxc = int(floorf(x[0])), fxr = int(floorf(x[1])), fxd = int(floorf(x[2]));
                         if (fxc < tc || fxc >= tc + L || fxr < tr || fxr >= tr + L || fxd < td || fxd >= td + LD)
                             continue;
-                        Cx<float> v = CUBIC ? cubic3<float, false, false>(lds, x[2], x[1], x[0]).v
-                                            : lerp3<float, false, false>(lds, x[2], x[1], x[0]).v;
-                        if (shifts) v = cmul(v, phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k));
                         const int i = rr >= 0 ? rr : rr + g.n;
-                        out[sd.base + i * g.hp + cc] = v;
+                        if constexpr (GMODE == 0) {
+                            Cx<float> v = CUBIC ? cubic3<float, false, false>(lds, x[2], x[1], x[0]).v
+                                                : lerp3<float, false, false>(lds, x[2], x[1], x[0]).v;
+                            if (shifts) v = cmul(v, phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k));
+                            out[sd.base + i * g.hp + cc] = v;
+                        } else {
+                            const Interp<float> ip = CUBIC ? cubic3_grads(lds, x[2], x[1], x[0])
+                                                           : lerp3<float, true, false>(lds, x[2], x[1], x[0]);
+                            const Cx<float> g0 = gsrc[sd.base + i * g.hp + cc];
+                            const Cx<float> ph = shifts ? phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k)
+                                                        : Cx<float>{1.f, 0.f};
+                            if (grot) {
+                                // g' = g * phase(-r, -c) = g * conj(phase(r, c)); s = (sc, sr, 0)
+                                const Cx<float> gg = shifts ? cmul(g0, cconj(ph)) : g0;
+                                const float sc = OSX ? fc * float(g.os) : float(double(fc) * g.os);
+                                const float sr = OSX ? fr * float(g.os) : float(double(fr) * g.os);
+#pragma unroll
+                                for (int row = 0; row < 3; ++row) {
+                                    acc[row * 3 + 0] += cmul(gg, cconj(cscale(ip.g[row], sc))).re;
+                                    acc[row * 3 + 1] += cmul(gg, cconj(cscale(ip.g[row], sr))).re;
+                                }
+                            }
+                            if (gshift) {
+                                const Cx<float> mod = cmul(ip.v, ph);
+                                const Cx<float> kr = {0.f, float(-kTwoPi * double(fr) / double(g.n))};
+                                const Cx<float> kc = {0.f, float(-kTwoPi * double(fc) / double(g.n))};
+                                acc[9] += cmul(g0, cconj(cmul(kr, mod))).re;
+                                acc[10] += cmul(g0, cconj(cmul(kc, mod))).re;
+                            }
+                        }
                       }
+                    }
+                }
+                if constexpr (GMODE == 1) {
+                    // the pose's sums (every lane of the wave takes part; one adds them)
+                    if (grot) {
+#pragma unroll
+                        for (int row = 0; row < 3; ++row)
+#pragma unroll
+                            for (int k = 0; k < 2; ++k) {
+                                const float t = wave_sum(acc[row * 3 + k]);
+                                if (lane == 0 && sv) atomic_add(&grot[(rb * g.P + pp) * 9 + row * 3 + k], t);
+                            }
+                    }
+                    if (gshift) {
+                        const float t0 = wave_sum(acc[9]), t1 = wave_sum(acc[10]);
+                        if (lane == 0 && sv) {
+                            atomic_add(&gshift[(sb * g.P + pp) * 2], t0);
+                            atomic_add(&gshift[(sb * g.P + pp) * 2 + 1], t1);
+                        }
                     }
                 }
                 __builtin_amdgcn_wave_barrier();
@@ -830,6 +935,18 @@ hipError_t scatter_kp(const Geom& g, const TileSpec& ts, const void* src, const 
 }
 
 template <bool CUBIC, bool OSX>
+hipError_t grads_launch(const Geom& g, const TileSpec& ts, const void* gproj, const void* rec, const void* rot,
+                        const void* shifts, void* grot, void* gshift, hipStream_t s) {
+    const int64_t fcore = int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fd1 - ts.fd0) * ts.ksplit;
+    const int64_t work = g.B * (fcore + int64_t(ts.nt) * ts.nt * ts.ntfd);
+    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, 1, OSX, 1>), dim3(grid_for(kXcds * xcd_per<kRunForw>(work))),
+                       dim3(kForwThreads), 0, s, g, ts, (const Cx<float>*)rec, (const float*)rot,
+                       (const float*)shifts, (Cx<float>*)nullptr, (const Cx<float>*)gproj, (float*)grot,
+                       (float*)gshift);
+    return hipGetLastError();
+}
+
+template <bool CUBIC, bool OSX>
 hipError_t forw_kp(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts, void* out,
                    hipStream_t s) {
     if (ts.kp_forw >= 4) return forw_launch<CUBIC, 4, OSX>(g, ts, rec, rot, shifts, out, s);
@@ -846,6 +963,16 @@ hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec&
                            : forw_kp<true, false>(g, ts, rec, rot, shifts, out, s);
     return ts.os_exact ? forw_kp<false, true>(g, ts, rec, rot, shifts, out, s)
                        : forw_kp<false, false>(g, ts, rec, rot, shifts, out, s);
+}
+
+hipError_t launch_grads3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gproj, const void* rec,
+                               const void* rot, const void* shifts, void* grot, void* gshift, hipStream_t s) {
+    if (!grot && !gshift) return hipSuccess;
+    if (cubic)
+        return ts.os_exact ? grads_launch<true, true>(g, ts, gproj, rec, rot, shifts, grot, gshift, s)
+                           : grads_launch<true, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, s);
+    return ts.os_exact ? grads_launch<false, true>(g, ts, gproj, rec, rot, shifts, grot, gshift, s)
+                       : grads_launch<false, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, s);
 }
 
 hipError_t launch_scatter3_tiled(bool cubic, int mode, const Geom& g, const TileSpec& ts, const void* src,

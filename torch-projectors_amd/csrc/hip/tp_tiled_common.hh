@@ -38,6 +38,20 @@ __device__ __forceinline__ int dpp_scan_max(int v) {
 }
 __device__ __forceinline__ int wave_max(int v) { return __builtin_amdgcn_readlane(dpp_scan_max(max(v, 0)), 63); }
 
+// Sum of v over the wave (every lane active), by the same DPP scan.
+template <int CTRL, int ROWS> __device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROWS, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f<0x111, 0xf>(v);  // row_shr:1
+    v += dpp_f<0x112, 0xf>(v);  // row_shr:2
+    v += dpp_f<0x114, 0xf>(v);  // row_shr:4
+    v += dpp_f<0x118, 0xf>(v);  // row_shr:8
+    v += dpp_f<0x142, 0xa>(v);  // row_bcast:15
+    v += dpp_f<0x143, 0xc>(v);  // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // Row lanes hold `cnt` samples starting at flattened index `excl`.  For the
 // window [e0, e0 + 64) every lane gets the row lane owning index e0 + lane:
 // rows mark their first index in a per-wave LDS array, a prefix max carries
