@@ -1,9 +1,11 @@
-"""The fp32 2D scatters at pose counts that split the tile-owner work into pose ranges.
+"""The fp32 2D operators at pose counts that split the tile-owner work into pose ranges.
 
-backproject_2d_forw and project_2d_back (its reconstruction gradient) route
-rotation poses through the tiled scatter, which splits every tile's poses into
-ranges of >= 128 when there are few tiles; the random and golden cases have
-too few poses for that.  These cases run hundreds of poses through the C ABI
+Rotation poses take the tiled kernels: the scatter for backproject_2d_forw
+and project_2d_back's reconstruction gradient, the gather for
+project_2d_forw, project_2d_back's rotation/shift gradients and
+backproject_2d_back.  Both split every tile's poses into ranges of >= 128
+when there are few tiles; the random and golden cases have too few poses for
+that.  These cases run hundreds of poses through the C ABI
 against the oracle, with every third pose matrix scaled (those take the
 per-pixel kernel), broadcast rotations, cutoffs inside and beyond the disc and
 oversampling factors that leave the tile grid ragged.  Bar: tests/parity.py.
@@ -19,7 +21,7 @@ pytestmark = pytest.mark.gpu
 def _cases():
     out = []
     seed = 90210
-    for op in ("backproject_2d_forw", "project_2d_back"):
+    for op in ("backproject_2d_forw", "project_2d_back", "project_2d_forw", "backproject_2d_back"):
         for interp in ("linear", "cubic"):
             for n, os_, cut, P, B, B_rot in ((48, 2.0, None, 700, 2, 2), (64, 1.5, 20.0, 400, 1, 1),
                                              (40, 3.0, 1000.0, 300, 3, 1), (32, 0.75, 9.5, 513, 1, 1)):

@@ -104,7 +104,10 @@ __global__ __launch_bounds__(kBlock) void k_backproject_forw_rest(Geom g, const 
 // Friedel flip without conjugation, zero outside); rotation and shift
 // gradients pair the conj-phased projection with the spatial derivative /
 // value of grad_data_rec (backprojection_2d_to_3d_kernels.cpp:451-567).
-template <int DIM, typename T, bool CUBIC, bool WG, bool ROT, bool SHIFT>
+// REST (fp32): poses that are rotations were computed by the tiled gather;
+// here they only get zeros on their masked pixels (and on grad_weights when
+// there is no grad_weight_rec).
+template <int DIM, typename T, bool CUBIC, bool WG, bool ROT, bool SHIFT, bool REST>
 __global__ __launch_bounds__(kBlock) void k_backproject_back(Geom g, const Cx<T>* __restrict__ gdata,
                                                              const T* __restrict__ gw, const Cx<T>* __restrict__ proj,
                                                              const T* __restrict__ rot, const T* __restrict__ shifts,
@@ -121,6 +124,8 @@ __global__ __launch_bounds__(kBlock) void k_backproject_back(Geom g, const Cx<T>
         const int pix = i * g.hp + j;
         const int64_t b = bp / g.P, p = bp - b * g.P;
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
+        bool tiled = false;
+        if constexpr (REST) tiled = pose_is_rotation_d<DIM>(rot + (rb * g.P + p) * RS);  // block-uniform
         T acc[K];
 #pragma unroll
         for (int k = 0; k < K; ++k) acc[k] = T(0);
@@ -129,7 +134,11 @@ __global__ __launch_bounds__(kBlock) void k_backproject_back(Geom g, const Cx<T>
             const int64_t pidx = bp * g.npix + pix;
             Cx<T> out = {0, 0};
             T outw = T(0);
-            if (!filtered(r, c, cut2) && !(j == 0 && i >= g.n / 2)) {
+            const bool active = !filtered(r, c, cut2) && !(j == 0 && i >= g.n / 2);
+            if (tiled) {
+                if (!active) gproj[pidx] = out;
+                if (gweights && (!active || !WG)) gweights[pidx] = outw;
+            } else if (active) {
                 const T* R = rot + (rb * g.P + p) * RS;
                 const T* S = shifts ? shifts + (sb * g.P + p) * 2 : nullptr;
                 T x[3], sc, sr;
@@ -158,10 +167,12 @@ __global__ __launch_bounds__(kBlock) void k_backproject_back(Geom g, const Cx<T>
                     }
                 }
             }
-            gproj[pidx] = out;
-            if (gweights) gweights[pidx] = outw;
+            if (!tiled) {
+                gproj[pidx] = out;
+                if (gweights) gweights[pidx] = outw;
+            }
         }
-        if (ROT || SHIFT) {
+        if ((ROT || SHIFT) && !tiled) {
             block_sum<T, K>(acc, red);
             if (threadIdx.x == 0) {
                 if (ROT)
@@ -202,10 +213,10 @@ hipError_t forw_rest(const Geom& g, const void* proj, const void* weights, const
     return hipGetLastError();
 }
 
-template <int DIM, typename T, bool CUBIC, bool WG, bool ROT, bool SHIFT>
+template <int DIM, typename T, bool CUBIC, bool WG, bool ROT, bool SHIFT, bool REST>
 hipError_t back8(const Geom& g, const void* gdata, const void* gw, const void* proj, const void* rot,
                  const void* shifts, void* gproj, void* gweights, void* grot, void* gshift, hipStream_t s) {
-    hipLaunchKernelGGL((k_backproject_back<DIM, T, CUBIC, WG, ROT, SHIFT>), dim3(grid_for(g.work)), dim3(kBlock), 0,
+    hipLaunchKernelGGL((k_backproject_back<DIM, T, CUBIC, WG, ROT, SHIFT, REST>), dim3(grid_for(g.work)), dim3(kBlock), 0,
                        s, g, (const Cx<T>*)gdata, (const T*)gw, (const Cx<T>*)proj, (const T*)rot, (const T*)shifts,
                        (Cx<T>*)gproj, (T*)gweights, (T*)grot, (T*)gshift);
     const hipError_t e = hipGetLastError();
@@ -213,26 +224,28 @@ hipError_t back8(const Geom& g, const void* gdata, const void* gw, const void* p
     return launch_zero_outside(sizeof(T) == 4 ? 0 : 1, g, gproj, gweights, s);
 }
 
-template <int DIM, typename T, bool CUBIC, bool WG>
+template <int DIM, typename T, bool CUBIC, bool WG, bool REST>
 hipError_t back4(const Geom& g, const void* gdata, const void* gw, const void* proj, const void* rot,
                  const void* shifts, void* gproj, void* gweights, void* grot, void* gshift, hipStream_t s) {
     if (grot && gshift)
-        return back8<DIM, T, CUBIC, WG, true, true>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+        return back8<DIM, T, CUBIC, WG, true, true, REST>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
+                                                          gshift, s);
     if (grot)
-        return back8<DIM, T, CUBIC, WG, true, false>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift,
-                                                     s);
+        return back8<DIM, T, CUBIC, WG, true, false, REST>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
+                                                           gshift, s);
     if (gshift)
-        return back8<DIM, T, CUBIC, WG, false, true>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift,
-                                                     s);
-    return back8<DIM, T, CUBIC, WG, false, false>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+        return back8<DIM, T, CUBIC, WG, false, true, REST>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
+                                                           gshift, s);
+    return back8<DIM, T, CUBIC, WG, false, false, REST>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
+                                                        gshift, s);
 }
 
-template <int DIM, typename T, bool CUBIC>
+template <int DIM, typename T, bool CUBIC, bool REST = false>
 hipError_t back(const Geom& g, const void* gdata, const void* gw, const void* proj, const void* rot,
                 const void* shifts, void* gproj, void* gweights, void* grot, void* gshift, hipStream_t s) {
     if (gw && gweights)
-        return back4<DIM, T, CUBIC, true>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
-    return back4<DIM, T, CUBIC, false>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+        return back4<DIM, T, CUBIC, true, REST>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+    return back4<DIM, T, CUBIC, false, REST>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
 }
 
 #define TP_DISPATCH(dim, dt, cubic, FN, ...)                                                  \
@@ -342,7 +355,10 @@ hipError_t launch_backproject_forw(int dim, int dt, bool cubic, const Geom& g, c
 
 hipError_t launch_backproject_back(int dim, int dt, bool cubic, const Geom& g, const void* gdata, const void* gw,
                                    const void* proj, const void* rot, const void* shifts, void* gproj,
-                                   void* gweights, void* grot, void* gshift, hipStream_t s) {
+                                   void* gweights, void* grot, void* gshift, hipStream_t s, bool rest_only) {
+    if (rest_only && dim == 2 && dt == 0)
+        return cubic ? back<2, float, true, true>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s)
+                     : back<2, float, false, true>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
     TP_DISPATCH(dim, dt, cubic, back, g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
 }
 

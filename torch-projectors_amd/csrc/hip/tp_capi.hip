@@ -206,6 +206,18 @@ tp::TileSpec2 tile_spec2(const tp::Geom& g, bool cubic) {
     ts.cmax = std::min(g.n / 2, cl);
     ts.rmin = std::max(g.n / 2 + 1 - g.n, -cl);
     ts.rmax = std::min(g.n / 2, cl);
+    // gather: square tiles over the signed plane |x| <= rho (+2), pose ranges as the scatter
+    constexpr int GT = tp::kGat2;
+    const int half_g = int(std::ceil((rho + 2.0) / GT));
+    ts.gnt = 2 * half_g;
+    ts.gorg = -half_g * GT;
+    const int64_t gtiles = g.B * int64_t(ts.gnt) * ts.gnt;
+    const int64_t gwant = gtiles > 0 ? (4096 + gtiles - 1) / gtiles : 1;
+    ts.gksplit = int(std::max<int64_t>(1, std::min(gwant, most)));
+    ts.gprange = int((g.P + ts.gksplit - 1) / ts.gksplit);
+    const double gw = GT + 2.0 * ts.eps;
+    const int grows = int(std::ceil(std::sqrt(2.0) * gw / g.os)) + 2;
+    ts.kp_gather = grows <= 16 ? 4 : (grows <= 32 ? 2 : 1);
     return ts;
 }
 
@@ -253,6 +265,13 @@ int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int6
         return launched(tp::launch_project_forw(dim, dtype, cubic, g, rec, rot, shifts, out, s, true),
                         "projection launch");
     }
+    if (use_tiles2(dim, dtype, os, n)) {
+        TP_TRY(launched(tp::launch_gather2_tiled(cubic, 0, g, tile_spec2(g, cubic), rec, nullptr, rot, shifts, out,
+                                                 nullptr, nullptr, nullptr, nullptr, s),
+                        "tiled projection launch"));
+        return launched(tp::launch_project_forw(dim, dtype, cubic, g, rec, rot, shifts, out, s, true),
+                        "projection launch");
+    }
     return launched(tp::launch_project_forw(dim, dtype, cubic, g, rec, rot, shifts, out, s), "projection launch");
 }
 
@@ -288,10 +307,14 @@ int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, in
         TP_TRY(launched(tp::launch_grads3_tiled(cubic, g, ts, gproj, rec, rot, shifts, grot, gshift, s),
                         "tiled rotation/shift-gradient launch"));
     }
-    if (tiles2)
-        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 1, g, tile_spec2(g, cubic), gproj, nullptr, rot, shifts,
-                                                  grec, nullptr, s),
+    if (tiles2) {
+        const tp::TileSpec2 ts = tile_spec2(g, cubic);
+        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, s),
                         "tiled reconstruction-gradient launch"));
+        TP_TRY(launched(tp::launch_gather2_tiled(cubic, 1, g, ts, rec, nullptr, rot, shifts, nullptr, nullptr, gproj,
+                                                 grot, gshift, s),
+                        "tiled rotation/shift-gradient launch"));
+    }
     return launched(tp::launch_project_back(dim, dtype, cubic, g, gproj, rec, rot, shifts, grec, grot, gshift, s,
                                             (tiles || tiles2) ? 1 : 0),
                     "projection backward launch");
@@ -357,8 +380,14 @@ int backproject_back(int dim, int dtype, const void* gdata, const void* gw, int6
     TP_TRY(need(proj, "projections"));
     TP_TRY(need(rot, "rotations"));
     TP_TRY(need(gproj, "grad_projections"));
-    return launched(tp::launch_backproject_back(dim, dtype, interp == TP_CUBIC, g, gdata, gw, proj, rot, shifts,
-                                                gproj, gweights, grot, gshift, s),
+    const bool cubic = interp == TP_CUBIC;
+    const bool tiles2 = use_tiles2(dim, dtype, os, n);
+    if (tiles2)
+        TP_TRY(launched(tp::launch_gather2_tiled(cubic, 2, g, tile_spec2(g, cubic), gdata, gw, rot, shifts, gproj,
+                                                 (gw && gweights) ? gweights : nullptr, proj, grot, gshift, s),
+                        "tiled backprojection backward launch"));
+    return launched(tp::launch_backproject_back(dim, dtype, cubic, g, gdata, gw, proj, rot, shifts, gproj, gweights,
+                                                grot, gshift, s, tiles2),
                     "backprojection backward launch");
 }
 

@@ -120,12 +120,14 @@ template <typename T> struct Interp {
 };
 
 // Bilinear (interpolation_kernels.h:78-135): lerp along c, then r.
-template <typename T, bool GRADS>
-__device__ __forceinline__ Interp<T> interp2_linear(const Cx<T>* __restrict__ rec, int N, int H, T r, T c) {
+// `fetch(r, c)` returns the tap value the reference's sampler would return for
+// integer coordinates (global fetch2, or a staged copy of it in LDS).
+template <typename T, bool GRADS, bool CLAMP = true, typename F>
+__device__ __forceinline__ Interp<T> lerp2(F&& fetch, T r, T c) {
     T cx, rx;
-    const int cf = split(c, cx), rf = split(r, rx);
-    const Cx<T> p00 = fetch2(rec, N, H, rf, cf), p01 = fetch2(rec, N, H, rf, cf + 1);
-    const Cx<T> p10 = fetch2(rec, N, H, rf + 1, cf), p11 = fetch2(rec, N, H, rf + 1, cf + 1);
+    const int cf = split_as<CLAMP>(c, cx), rf = split_as<CLAMP>(r, rx);
+    const Cx<T> p00 = fetch(rf, cf), p01 = fetch(rf, cf + 1);
+    const Cx<T> p10 = fetch(rf + 1, cf), p11 = fetch(rf + 1, cf + 1);
     const Cx<T> p0 = cadd(p00, cscale(csub(p01, p00), cx));
     const Cx<T> p1 = cadd(p10, cscale(csub(p11, p10), cx));
     Interp<T> o;
@@ -137,12 +139,17 @@ __device__ __forceinline__ Interp<T> interp2_linear(const Cx<T>* __restrict__ re
     }
     return o;
 }
+template <typename T, bool GRADS>
+__device__ __forceinline__ Interp<T> interp2_linear(const Cx<T>* __restrict__ rec, int N, int H, T r, T c) {
+    return lerp2<T, GRADS>([&](int rr, int cc) { return fetch2(rec, N, H, rr, cc); }, r, c);
+}
 
 // Bicubic (interpolation_kernels.h:258-322): sum over r then c of (s*wr)*wc.
-template <typename T, bool GRADS>
-__device__ __forceinline__ Interp<T> interp2_cubic(const Cx<T>* __restrict__ rec, int N, int H, T r, T c) {
+// `fetch` returns the pre-clamped tap of fetch2_cubic.
+template <typename T, bool GRADS, bool CLAMP = true, typename F>
+__device__ __forceinline__ Interp<T> cubic2(F&& fetch, T r, T c) {
     T cx, rx;
-    const int cf = split(c, cx), rf = split(r, rx);
+    const int cf = split_as<CLAMP>(c, cx), rf = split_as<CLAMP>(r, rx);
     T wc[4], dwc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -158,7 +165,7 @@ __device__ __forceinline__ Interp<T> interp2_cubic(const Cx<T>* __restrict__ rec
         const T dwr = GRADS ? cubic_dw<T>(rx - T(i - 1)) : T(0);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const Cx<T> s = fetch2_cubic(rec, N, H, rf + i - 1, cf + j - 1);
+            const Cx<T> s = fetch(rf + i - 1, cf + j - 1);
             o.v = cadd(o.v, cscale(cscale(s, wr), wc[j]));
             if (GRADS) {
                 o.g[1] = cadd(o.g[1], cscale(cscale(s, dwr), wc[j]));
@@ -167,6 +174,10 @@ __device__ __forceinline__ Interp<T> interp2_cubic(const Cx<T>* __restrict__ rec
         }
     }
     return o;
+}
+template <typename T, bool GRADS>
+__device__ __forceinline__ Interp<T> interp2_cubic(const Cx<T>* __restrict__ rec, int N, int H, T r, T c) {
+    return cubic2<T, GRADS>([&](int rr, int cc) { return fetch2_cubic(rec, N, H, rr, cc); }, r, c);
 }
 
 // Trilinear (interpolation_kernels.h:140-228): lerp along c, then r, then d.

@@ -49,8 +49,9 @@ struct TileSpec {
     bool os_exact;            // float(os) == os: c * os can be formed in float exactly as in double
 };
 
-// Tile-owner scatter of the fp32 2D operators (tp_tiled2d.hip).
-constexpr int kTile2C = 32, kTile2R = 16;  // tile edges (c, r): fp64 accumulators
+// Tile-owner kernels of the fp32 2D operators (tp_tiled2d.hip).
+constexpr int kTile2C = 32, kTile2R = 16;  // scatter tile edges (c, r): fp64 accumulators
+constexpr int kGat2 = 32;                  // gather tile edge (c and r)
 struct TileSpec2 {
     int kr0, nr, nc;        // tiles that samples can reach: rows [kr0, kr0 + nr), columns [0, nc)
     int ksplit, prange;     // pose ranges per tile, poses per range
@@ -60,6 +61,9 @@ struct TileSpec2 {
     float os, inv_os;       // oversampling and its inverse
     float smax;             // bound on |c*os| over the pixel grid
     int cmax, rmin, rmax;   // pixel-grid limits of c and r (grid and cutoff)
+    int gnt, gorg;          // gather: tiles per axis over the signed plane, and its origin
+    int gksplit, gprange;   // gather: pose ranges per tile, poses per range
+    int kp_gather;          // gather (forward): poses per wavefront batch
 };
 
 constexpr int kBlock = 256;
@@ -74,12 +78,12 @@ hipError_t launch_zero(void* p, int64_t words, hipStream_t s);
 hipError_t launch_zero_outside(int dt, const Geom& g, void* out, void* wout, hipStream_t s);
 
 // Kernel launchers; `dim` is 2 or 3, `dt` 0 (fp32) or 1 (fp64).
-// `rest_only` (fp32 3D): only masked pixels and poses that are not rotations.
+// `rest_only` (fp32): only masked pixels and poses that are not rotations.
 hipError_t launch_project_forw(int dim, int dt, bool cubic, const Geom& g, const void* rec, const void* rot,
                                const void* shifts, void* out, hipStream_t s, bool rest_only = false);
-// `rest` != 0 (fp32): poses that are rotations are left to the tiled kernels.
-// 2D: their reconstruction-gradient scatter only (rotation/shift gradients here
-// for all poses); 3D: everything (launch_grads3_tiled gives their gradients).
+// `rest` != 0 (fp32): poses that are rotations are left to the tiled kernels
+// entirely (the tiled scatter gives their reconstruction gradient,
+// launch_grads3_tiled / launch_gather2_tiled their rotation/shift gradients).
 hipError_t launch_project_back(int dim, int dt, bool cubic, const Geom& g, const void* gproj, const void* rec,
                                const void* rot, const void* shifts, void* grec, void* grot, void* gshift,
                                hipStream_t s, int rest = 0);
@@ -107,6 +111,15 @@ hipError_t launch_scatter3_tiled(bool cubic, int mode, const Geom& g, const Tile
 hipError_t launch_scatter2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* src,
                                  const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
                                  hipStream_t s);
+// fp32 2D tile-owner gathers (rotation poses only; the per-pixel kernels with
+// `rest` complete the other poses and the masked pixels).  mode 0: forward
+// (rec -> out); mode 1: rotation/shift gradients of project_2d_back (gsrc =
+// grad_projections) into zero-filled grot / gshift; mode 2:
+// backproject_2d_back (rec = grad_data_rec -> out, gw -> wout, and with gsrc =
+// projections the gradients).
+hipError_t launch_gather2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* rec,
+                                const void* gw, const void* rot, const void* shifts, void* out, void* wout,
+                                const void* gsrc, void* grot, void* gshift, hipStream_t s);
 
 // Reference preparation (tp_fourier.hip).  Elements are opaque words of
 // elem_bytes (2, 4, 8 or 16); `dim` spatial axes (2 or 3) after the batch.
@@ -126,8 +139,10 @@ hipError_t launch_normalize(int dt, const void* data, const void* weights, int64
 int fft_forward(int dt, int dim, int64_t batch, int64_t N, const void* real, void* spec, hipStream_t s);
 int fft_inverse(int dt, int dim, int64_t batch, int64_t N, void* spec, void* real, hipStream_t s);
 
+// `rest_only` (fp32 2D): rotation poses only get zeros on their masked pixels
+// (launch_gather2_tiled mode 2 computed the rest); other poses everything.
 hipError_t launch_backproject_back(int dim, int dt, bool cubic, const Geom& g, const void* gdata, const void* gw,
                                    const void* proj, const void* rot, const void* shifts, void* gproj,
-                                   void* gweights, void* grot, void* gshift, hipStream_t s);
+                                   void* gweights, void* grot, void* gshift, hipStream_t s, bool rest_only = false);
 
 }  // namespace tp

@@ -55,20 +55,21 @@ __global__ __launch_bounds__(kBlock) void k_project_forw(Geom g, const Cx<T>* __
     }
 }
 
-// Completes the fp32 3D forward after the tiled kernel, which has written the
+// Completes the fp32 forward after the tiled kernel, which has written the
 // active pixels of rotation poses: zeros on masked pixels, and every pixel of
 // the other poses.  One block per pose.
-template <bool CUBIC>
-__global__ __launch_bounds__(kBlock) void k_project3_forw_rest(Geom g, const Cx<float>* __restrict__ rec,
-                                                               const float* __restrict__ rot,
-                                                               const float* __restrict__ shifts,
-                                                               Cx<float>* __restrict__ out) {
+template <int DIM, bool CUBIC>
+__global__ __launch_bounds__(kBlock) void k_project_forw_rest(Geom g, const Cx<float>* __restrict__ rec,
+                                                              const float* __restrict__ rot,
+                                                              const float* __restrict__ shifts,
+                                                              Cx<float>* __restrict__ out) {
+    constexpr int RS = DIM * DIM;
     const float cut2 = float(g.cut2);
     for (int64_t bp = blockIdx.x; bp < g.B * g.P; bp += gridDim.x) {
         const int64_t b = bp / g.P, p = bp - b * g.P;
-        const float* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * 9;
+        const float* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * RS;
         const float* S = shifts ? shifts + ((g.B_shift == 1 ? 0 : b) * g.P + p) * 2 : nullptr;
-        const bool tiled = pose_is_rotation(R);
+        const bool tiled = pose_is_rotation_d<DIM>(R);
         Cx<float>* outp = out + bp * g.npix;
         // one row per wave, lanes along the row (no per-pixel division)
         for (int i = threadIdx.x / 64; i < g.n; i += kBlock / 64) {
@@ -77,7 +78,7 @@ __global__ __launch_bounds__(kBlock) void k_project3_forw_rest(Geom g, const Cx<
             for (int j = threadIdx.x % 64; j < g.hp; j += 64) {
                 const float c = float(j);
                 if (filtered(r, c, cut2)) row[j] = Cx<float>{0.f, 0.f};
-                else if (!tiled) row[j] = project_pixel<3, float, CUBIC>(g, rec + b * g.vol, R, S, r, c);
+                else if (!tiled) row[j] = project_pixel<DIM, float, CUBIC>(g, rec + b * g.vol, R, S, r, c);
             }
         }
     }
@@ -178,9 +179,9 @@ hipError_t forw(const Geom& g, const void* rec, const void* rot, const void* shi
     return launch_zero_outside(sizeof(T) == 4 ? 0 : 1, g, out, nullptr, s);
 }
 
-template <bool CUBIC>
+template <int DIM, bool CUBIC>
 hipError_t forw_rest(const Geom& g, const void* rec, const void* rot, const void* shifts, void* out, hipStream_t s) {
-    hipLaunchKernelGGL(k_project3_forw_rest<CUBIC>, dim3(grid_for(g.B * g.P)), dim3(kBlock), 0, s, g,
+    hipLaunchKernelGGL((k_project_forw_rest<DIM, CUBIC>), dim3(grid_for(g.B * g.P)), dim3(kBlock), 0, s, g,
                        (const Cx<float>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
     return hipGetLastError();
 }
@@ -218,8 +219,12 @@ hipError_t back(const Geom& g, const void* gproj, const void* rec, const void* r
 
 hipError_t launch_project_forw(int dim, int dt, bool cubic, const Geom& g, const void* rec, const void* rot,
                                const void* shifts, void* out, hipStream_t s, bool rest_only) {
-    if (rest_only && dim == 3 && dt == 0)
-        return cubic ? forw_rest<true>(g, rec, rot, shifts, out, s) : forw_rest<false>(g, rec, rot, shifts, out, s);
+    if (rest_only && dt == 0) {
+        if (dim == 2)
+            return cubic ? forw_rest<2, true>(g, rec, rot, shifts, out, s)
+                         : forw_rest<2, false>(g, rec, rot, shifts, out, s);
+        return cubic ? forw_rest<3, true>(g, rec, rot, shifts, out, s) : forw_rest<3, false>(g, rec, rot, shifts, out, s);
+    }
     TP_DISPATCH(dim, dt, cubic, forw, g, rec, rot, shifts, out, s);
 }
 
@@ -228,8 +233,8 @@ hipError_t launch_project_back(int dim, int dt, bool cubic, const Geom& g, const
                                hipStream_t s, int rest) {
     if (rest != 0 && dt == 0) {
         if (dim == 2)
-            return cubic ? back<2, float, true, 1>(g, gproj, rec, rot, shifts, grec, grot, gshift, s)
-                         : back<2, float, false, 1>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+            return cubic ? back<2, float, true, 2>(g, gproj, rec, rot, shifts, grec, grot, gshift, s)
+                         : back<2, float, false, 2>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
         return cubic ? back<3, float, true, 2>(g, gproj, rec, rot, shifts, grec, grot, gshift, s)
                      : back<3, float, false, 2>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
     }

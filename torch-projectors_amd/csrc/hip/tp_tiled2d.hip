@@ -448,7 +448,284 @@ hipError_t scatter2_kp(const Geom& g, const TileSpec2& ts, const void* src, cons
     return scatter2_launch<CUBIC, MODE, WEIGHTS, 1>(g, ts, src, weights, rot, shifts, dst, wdst, s);
 }
 
+// ----------------------------------------------------------------------------- gather
+// Tile-owner gathers of the 2D operators, over 32 x 32 (c, r) tiles of the
+// signed frequency plane (origin ts.gorg, ts.gnt tiles per axis).  A sample is
+// computed by the one tile that holds floor(x); the tile plus its stencil halo
+// is staged in LDS with exactly the values the reference's sampler returns
+// (Friedel conjugation and clamping applied), so the interpolation is
+// bit-identical to the per-pixel one.
+//
+//   GMODE 0  forward projection into `out` (project_2d_forw).
+//   GMODE 1  rotation/shift gradients of project_2d_back: `gsrc` holds
+//            grad_projections; terms as cpu/2d/projection_2d_kernels.cpp:300-375.
+//   GMODE 2  backproject_2d_back: grad_projections (`out`) gathered from
+//            grad_data_rec (`rec`), grad_weights (`wout`) bilinearly from
+//            grad_weight_rec (`gw`, a second staged tile with the weight-tap
+//            rules), and with RS the rotation/shift gradients against the
+//            projections `gsrc` (cpu/2d/backprojection_2d_kernels.cpp:420-520).
+// In GMODE 1/2 a wave takes one pose at a time (KP = 1) and sums its terms
+// before one atomic per gradient component.
+constexpr int GC = kGat2, GR = kGat2;
+constexpr double kTwoPi2 = 6.283185307179586476925286766559;
+
+template <bool CUBIC, int KP, int GMODE, bool RS, bool WG>
+__global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts, const Cx<float>* __restrict__ rec,
+                                                            const float* __restrict__ gw,
+                                                            const float* __restrict__ rot,
+                                                            const float* __restrict__ shifts,
+                                                            Cx<float>* __restrict__ out, float* __restrict__ wout,
+                                                            const Cx<float>* __restrict__ gsrc,
+                                                            float* __restrict__ grot, float* __restrict__ gshift) {
+    static_assert(GMODE == 0 || KP == 1, "the gradient modes sum one pose per wave batch");
+    constexpr int LO = CUBIC ? 1 : 0, HI = CUBIC ? 2 : 1, WC = GC + LO + HI, WR = GR + LO + HI, W2 = WC * WR;
+    constexpr int WW = (GMODE == 2 && WG) ? (GC + 1) * (GR + 1) : 1;  // bilinear weight taps
+    constexpr int RPS = 64 / KP, NW = kThreads / 64, CH = 2048;
+    constexpr bool GRADS = GMODE == 1 || (GMODE == 2 && RS);
+    __shared__ Cx<float> vt[W2];
+    __shared__ float wt[WW];
+    __shared__ unsigned short plist[CH];
+    __shared__ int pcnt[2];
+    __shared__ Slot2 slots[NW][KP];
+    __shared__ int marks[NW][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int slot = lane / RPS, jrow = lane % RPS;
+    const int N = g.N, H = g.H;
+    const int64_t items = g.B * ts.gksplit * int64_t(ts.gnt) * ts.gnt;
+    const float cut2 = float(g.cut2);
+    const int64_t per = xcd_per<kRun>(items);
+    for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
+        const int64_t w = xcd_item<kRun>(slot_i);
+        if (w >= items) continue;
+        const int kc = int(w % ts.gnt);
+        int64_t q = w / ts.gnt;
+        const int kr = int(q % ts.gnt);
+        q /= ts.gnt;
+        const int jr = int(q % ts.gksplit);
+        const int64_t b = q / ts.gksplit;
+        const int p0 = jr * ts.gprange, p1 = min(int(g.P), p0 + ts.gprange);
+        const int tc = ts.gorg + kc * GC, tr = ts.gorg + kr * GR;
+        // samples owned by this tile: floor(x) in [t, t + edge) on both axes (+ slack)
+        const float lo[2] = {float(tc) - ts.eps, float(tr) - ts.eps};
+        const float hi[2] = {float(tc + GC) + ts.eps, float(tr + GR) + ts.eps};
+        float dist2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const float d = lo[k] > 0.f ? lo[k] : (hi[k] < 0.f ? -hi[k] : 0.f);
+            dist2 += d * d;
+        }
+        if (dist2 > ts.rho * ts.rho || p1 <= p0) continue;
+        const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
+        const float* rotb = rot + rb * g.P * 4;
+        const float* shb = shifts ? shifts + sb * g.P * 2 : nullptr;
+        const int64_t pose0 = b * g.P;
+        auto lds = [&](int r, int c) { return vt[(r - (tr - LO)) * WC + (c - (tc - LO))]; };
+        bool loaded = false;
+        for (int pbase = p0; pbase < p1; pbase += CH) {
+            // cull: rotations whose sample half-disc reaches the tile
+            __syncthreads();
+            if (tid == 0) pcnt[0] = 0;
+            __syncthreads();
+            for (int k = tid; k < CH && pbase + k < p1; k += kThreads) {
+                float R[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) R[e] = rotb[int64_t(pbase + k) * 4 + e];
+                if (pose_is_rotation2(R) && half_plane_hits2(R, lo, hi)) plist[atomicAdd(&pcnt[0], 1)] = k;
+            }
+            __syncthreads();
+            const int np = pcnt[0];
+            if (np == 0) continue;
+            if (!loaded) {
+                const Cx<float>* recb = rec + b * g.vol;
+                for (int e = tid; e < W2; e += kThreads) {
+                    const int r = tr - LO + e / WC, c = tc - LO + e % WC;
+                    vt[e] = CUBIC ? fetch2_cubic(recb, N, H, r, c) : fetch2(recb, N, H, r, c);
+                }
+                if constexpr (GMODE == 2 && WG) {
+                    const float* gwb = gw + b * g.vol;
+                    for (int e = tid; e < WW; e += kThreads)
+                        wt[e] = weight_tap<2>(gwb, N, H, 0, tr + e / (GC + 1), tc + e % (GC + 1));
+                }
+                __syncthreads();
+                loaded = true;
+            }
+            auto pose_at = [&](int k) { return pbase + int(plist[k]); };
+            int base = wave * KP;
+            float Rn[4], Sn[2];
+            if (base < np) load_pose2(rotb, shb, pose_at(min(base + slot, np - 1)), Rn, Sn);
+            for (; base < np; base += NW * KP) {
+                const bool sv = base + slot < np;
+                const int pp = pose_at(min(base + slot, np - 1));
+                float R[4], Sh[2];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) R[e] = Rn[e];
+                Sh[0] = Sn[0];
+                Sh[1] = Sn[1];
+                if (base + NW * KP < np) load_pose2(rotb, shb, pose_at(min(base + NW * KP + slot, np - 1)), Rn, Sn);
+                if (jrow == 0 && sv) {
+                    Slot2& sd = slots[wave][slot];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) sd.R[e] = R[e];
+                    sd.s0 = Sh[0];
+                    sd.s1 = Sh[1];
+                    sd.p = pp;
+                }
+                __builtin_amdgcn_wave_barrier();
+                float acc[6];  // GMODE 1/2: 4 rotation and 2 shift terms of this lane's samples
+#pragma unroll
+                for (int k = 0; k < 6; ++k) acc[k] = 0.f;
+                int r0, r1;
+                box_rows2(R, lo, hi, ts, r0, r1);
+                const int nr = sv ? max(0, r1 - r0 + 1) : 0;
+                const int maxnr = wave_max(nr);
+                for (int rbase = 0; rbase < maxnr; rbase += RPS) {
+                    const int jj = rbase + jrow;
+                    const int r = r0 + jj;
+                    int c0 = 0, cnt = 0;
+                    if (jj < nr) {
+                        int c1;
+                        row_span2(R, r, lo, hi, ts, cut2, c0, c1);
+                        cnt = max(0, c1 - c0 + 1);
+                    }
+                    const int incl = dpp_scan_add(cnt);
+                    const int excl = incl - cnt;
+                    const int total = __builtin_amdgcn_readlane(incl, 63);
+                    int carry = 0;
+                    for (int e0 = 0; e0 < total; e0 += 64) {
+                        const int e = e0 + lane;
+                        const int lw = window_owner(cnt, excl, e0, carry, marks[wave]);
+                        const int rr = __shfl(r, lw, 64);
+                        const int cc = __shfl(c0, lw, 64) + (e - __shfl(excl, lw, 64));
+                        if (e >= total) continue;
+                        const Slot2& sd = slots[wave][lw / RPS];
+                        const float fr = float(rr), fc = float(cc);
+                        if (filtered(fr, fc, cut2)) continue;
+                        // the backward ops skip the Friedel half of the x = 0 line
+                        if (GMODE != 0 && cc == 0 && (rr == g.n / 2 || rr < 0)) continue;
+                        float x[2];
+                        rotate_pix(sd.R, fr, fc, g.os, x);
+                        const int fxc = int(floorf(x[0])), fxr = int(floorf(x[1]));
+                        if (fxc < tc || fxc >= tc + GC || fxr < tr || fxr >= tr + GR) continue;
+                        const int i = rr >= 0 ? rr : rr + g.n;
+                        const int64_t pidx = (pose0 + sd.p) * int64_t(g.npix) + i * g.hp + cc;
+                        const Interp<float> ip = CUBIC ? cubic2<float, GRADS, false>(lds, x[1], x[0])
+                                                       : lerp2<float, GRADS, false>(lds, x[1], x[0]);
+                        const Cx<float> ph = shifts ? phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k) : Cx<float>{1.f, 0.f};
+                        if constexpr (GMODE == 0) {
+                            out[pidx] = shifts ? cmul(ip.v, ph) : ip.v;
+                        } else {
+                            if constexpr (GMODE == 2) {
+                                out[pidx] = shifts ? cmul(ip.v, ph) : ip.v;
+                                if constexpr (WG) {
+                                    // bilinear as weight_grad_interp<2>
+                                    float cx, rx;
+                                    const int cf = split_as<false>(x[0], cx), rf = split_as<false>(x[1], rx);
+                                    const float* wr0 = &wt[(rf - tr) * (GC + 1) + (cf - tc)];
+                                    const float p00 = wr0[0], p01 = wr0[1], p10 = wr0[GC + 1], p11 = wr0[GC + 2];
+                                    const float q0 = p00 + (p01 - p00) * cx;
+                                    const float q1 = p10 + (p11 - p10) * cx;
+                                    wout[pidx] = q0 + (q1 - q0) * rx;
+                                }
+                            }
+                            if constexpr (GRADS) {
+                                // project_2d_back pairs g' = g * conj(phase) with dF/dx and g with the
+                                // modulated value; backproject_2d_back pairs proj * conj(phase) with both
+                                const Cx<float> g0 = gsrc[pidx];
+                                const Cx<float> gg = shifts ? cmul(g0, cconj(ph)) : g0;
+                                const Cx<float> sv_ = GMODE == 1 ? g0 : gg;
+                                const Cx<float> mv = GMODE == 1 ? cmul(ip.v, ph) : ip.v;
+                                if (grot) {
+                                    const float sc = float(double(fc) * g.os), sr = float(double(fr) * g.os);
+#pragma unroll
+                                    for (int row = 0; row < 2; ++row) {
+                                        acc[row * 2 + 0] += cmul(gg, cconj(cscale(ip.g[row], sc))).re;
+                                        acc[row * 2 + 1] += cmul(gg, cconj(cscale(ip.g[row], sr))).re;
+                                    }
+                                }
+                                if (gshift) {
+                                    const Cx<float> kr = {0.f, float(-kTwoPi2 * double(fr) / double(g.n))};
+                                    const Cx<float> kc = {0.f, float(-kTwoPi2 * double(fc) / double(g.n))};
+                                    acc[4] += cmul(sv_, cconj(cmul(kr, mv))).re;
+                                    acc[5] += cmul(sv_, cconj(cmul(kc, mv))).re;
+                                }
+                            }
+                        }
+                    }
+                }
+                if constexpr (GRADS) {
+                    if (grot) {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const float t = wave_sum(acc[k]);
+                            if (lane == 0 && sv) atomic_add(&grot[(rb * g.P + pp) * 4 + k], t);
+                        }
+                    }
+                    if (gshift) {
+                        const float t0 = wave_sum(acc[4]), t1 = wave_sum(acc[5]);
+                        if (lane == 0 && sv) {
+                            atomic_add(&gshift[(sb * g.P + pp) * 2], t0);
+                            atomic_add(&gshift[(sb * g.P + pp) * 2 + 1], t1);
+                        }
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <bool CUBIC, int KP, int GMODE, bool RS, bool WG>
+hipError_t gather2_launch(const Geom& g, const TileSpec2& ts, const void* rec, const void* gw, const void* rot,
+                          const void* shifts, void* out, void* wout, const void* gsrc, void* grot, void* gshift,
+                          hipStream_t s) {
+    const int64_t work = g.B * ts.gksplit * int64_t(ts.gnt) * ts.gnt;
+    if (work == 0) return hipSuccess;
+    hipLaunchKernelGGL((k_gather2_tiled<CUBIC, KP, GMODE, RS, WG>), dim3(grid_for(kXcds * xcd_per<kRun>(work))),
+                       dim3(kThreads), 0, s, g, ts, (const Cx<float>*)rec, (const float*)gw, (const float*)rot,
+                       (const float*)shifts, (Cx<float>*)out, (float*)wout, (const Cx<float>*)gsrc, (float*)grot,
+                       (float*)gshift);
+    return hipGetLastError();
+}
+
+template <bool CUBIC>
+hipError_t gather2_modes(int mode, const Geom& g, const TileSpec2& ts, const void* rec, const void* gw,
+                         const void* rot, const void* shifts, void* out, void* wout, const void* gsrc, void* grot,
+                         void* gshift, hipStream_t s) {
+    if (mode == 0) {
+        if (ts.kp_gather >= 4)
+            return gather2_launch<CUBIC, 4, 0, false, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
+                                                             gshift, s);
+        if (ts.kp_gather == 2)
+            return gather2_launch<CUBIC, 2, 0, false, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
+                                                             gshift, s);
+        return gather2_launch<CUBIC, 1, 0, false, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift,
+                                                         s);
+    }
+    if (mode == 1)
+        return gather2_launch<CUBIC, 1, 1, true, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift,
+                                                        s);
+    const bool rs = grot || gshift;
+    if (wout)
+        return rs ? gather2_launch<CUBIC, 1, 2, true, true>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
+                                                            gshift, s)
+                  : gather2_launch<CUBIC, 1, 2, false, true>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
+                                                             gshift, s);
+    return rs ? gather2_launch<CUBIC, 1, 2, true, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift,
+                                                         s)
+              : gather2_launch<CUBIC, 1, 2, false, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
+                                                          gshift, s);
+}
+
 }  // namespace
+
+hipError_t launch_gather2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* rec,
+                                const void* gw, const void* rot, const void* shifts, void* out, void* wout,
+                                const void* gsrc, void* grot, void* gshift, hipStream_t s) {
+    if (mode == 1 && !grot && !gshift) return hipSuccess;
+    return cubic ? gather2_modes<true>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, s)
+                 : gather2_modes<false>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, s);
+}
 
 hipError_t launch_scatter2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* src,
                                  const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
