@@ -104,9 +104,8 @@ __global__ __launch_bounds__(kBlock) void k_backproject_forw_rest(Geom g, const 
 // Friedel flip without conjugation, zero outside); rotation and shift
 // gradients pair the conj-phased projection with the spatial derivative /
 // value of grad_data_rec (backprojection_2d_to_3d_kernels.cpp:451-567).
-// REST (fp32): poses that are rotations were computed by the tiled gather;
-// here they only get zeros on their masked pixels (and on grad_weights when
-// there is no grad_weight_rec).
+// REST (fp32): poses that are rotations were computed by the tiled gather
+// into zero-filled outputs and are skipped here.
 template <int DIM, typename T, bool CUBIC, bool WG, bool ROT, bool SHIFT, bool REST>
 __global__ __launch_bounds__(kBlock) void k_backproject_back(Geom g, const Cx<T>* __restrict__ gdata,
                                                              const T* __restrict__ gw, const Cx<T>* __restrict__ proj,
@@ -124,8 +123,9 @@ __global__ __launch_bounds__(kBlock) void k_backproject_back(Geom g, const Cx<T>
         const int pix = i * g.hp + j;
         const int64_t b = bp / g.P, p = bp - b * g.P;
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
-        bool tiled = false;
-        if constexpr (REST) tiled = pose_is_rotation_d<DIM>(rot + (rb * g.P + p) * RS);  // block-uniform
+        if constexpr (REST) {
+            if (pose_is_rotation_d<DIM>(rot + (rb * g.P + p) * RS)) continue;  // block-uniform
+        }
         T acc[K];
 #pragma unroll
         for (int k = 0; k < K; ++k) acc[k] = T(0);
@@ -134,11 +134,7 @@ __global__ __launch_bounds__(kBlock) void k_backproject_back(Geom g, const Cx<T>
             const int64_t pidx = bp * g.npix + pix;
             Cx<T> out = {0, 0};
             T outw = T(0);
-            const bool active = !filtered(r, c, cut2) && !(j == 0 && i >= g.n / 2);
-            if (tiled) {
-                if (!active) gproj[pidx] = out;
-                if (gweights && (!active || !WG)) gweights[pidx] = outw;
-            } else if (active) {
+            if (!filtered(r, c, cut2) && !(j == 0 && i >= g.n / 2)) {
                 const T* R = rot + (rb * g.P + p) * RS;
                 const T* S = shifts ? shifts + (sb * g.P + p) * 2 : nullptr;
                 T x[3], sc, sr;
@@ -167,12 +163,10 @@ __global__ __launch_bounds__(kBlock) void k_backproject_back(Geom g, const Cx<T>
                     }
                 }
             }
-            if (!tiled) {
-                gproj[pidx] = out;
-                if (gweights) gweights[pidx] = outw;
-            }
+            gproj[pidx] = out;
+            if (gweights) gweights[pidx] = outw;
         }
-        if ((ROT || SHIFT) && !tiled) {
+        if (ROT || SHIFT) {
             block_sum<T, K>(acc, red);
             if (threadIdx.x == 0) {
                 if (ROT)
@@ -216,11 +210,12 @@ hipError_t forw_rest(const Geom& g, const void* proj, const void* weights, const
 template <int DIM, typename T, bool CUBIC, bool WG, bool ROT, bool SHIFT, bool REST>
 hipError_t back8(const Geom& g, const void* gdata, const void* gw, const void* proj, const void* rot,
                  const void* shifts, void* gproj, void* gweights, void* grot, void* gshift, hipStream_t s) {
-    hipLaunchKernelGGL((k_backproject_back<DIM, T, CUBIC, WG, ROT, SHIFT, REST>), dim3(grid_for(g.work)), dim3(kBlock), 0,
+    const unsigned grid = REST ? unsigned(g.work < 8192 ? g.work : 8192) : grid_for(g.work);
+    hipLaunchKernelGGL((k_backproject_back<DIM, T, CUBIC, WG, ROT, SHIFT, REST>), dim3(grid), dim3(kBlock), 0,
                        s, g, (const Cx<T>*)gdata, (const T*)gw, (const Cx<T>*)proj, (const T*)rot, (const T*)shifts,
                        (Cx<T>*)gproj, (T*)gweights, (T*)grot, (T*)gshift);
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || REST) return e;  // with REST the outputs were zero-filled first
     return launch_zero_outside(sizeof(T) == 4 ? 0 : 1, g, gproj, gweights, s);
 }
 

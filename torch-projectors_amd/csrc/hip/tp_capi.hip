@@ -266,6 +266,9 @@ int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int6
                         "projection launch");
     }
     if (use_tiles2(dim, dtype, os, n)) {
+        // zero-fill first: the tiled gather writes the active pixels of rotation poses, the
+        // rest kernel the other poses
+        TP_TRY(zero(out, cx_words(dtype, g.B * g.P * int64_t(g.npix)), s));
         TP_TRY(launched(tp::launch_gather2_tiled(cubic, 0, g, tile_spec2(g, cubic), rec, nullptr, rot, shifts, out,
                                                  nullptr, nullptr, nullptr, nullptr, s),
                         "tiled projection launch"));
@@ -382,6 +385,10 @@ int backproject_back(int dim, int dtype, const void* gdata, const void* gw, int6
     TP_TRY(need(gproj, "grad_projections"));
     const bool cubic = interp == TP_CUBIC;
     const bool tiles2 = use_tiles2(dim, dtype, os, n);
+    if (tiles2) {
+        TP_TRY(zero(gproj, cx_words(dtype, g.B * g.P * int64_t(g.npix)), s));
+        TP_TRY(zero(gweights, re_words(dtype, g.B * g.P * int64_t(g.npix)), s));
+    }
     if (tiles2)
         TP_TRY(launched(tp::launch_gather2_tiled(cubic, 2, g, tile_spec2(g, cubic), gdata, gw, rot, shifts, gproj,
                                                  (gw && gweights) ? gweights : nullptr, proj, grot, gshift, s),

@@ -57,8 +57,9 @@ __global__ __launch_bounds__(kBlock) void k_project_forw(Geom g, const Cx<T>* __
 
 // Completes the fp32 forward after the tiled kernel, which has written the
 // active pixels of rotation poses: zeros on masked pixels, and every pixel of
-// the other poses.  One block per pose.
-template <int DIM, bool CUBIC>
+// the other poses.  One block per pose.  ZEROED: the output was zero-filled
+// first, so rotation poses are done.
+template <int DIM, bool CUBIC, bool ZEROED>
 __global__ __launch_bounds__(kBlock) void k_project_forw_rest(Geom g, const Cx<float>* __restrict__ rec,
                                                               const float* __restrict__ rot,
                                                               const float* __restrict__ shifts,
@@ -70,6 +71,7 @@ __global__ __launch_bounds__(kBlock) void k_project_forw_rest(Geom g, const Cx<f
         const float* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * RS;
         const float* S = shifts ? shifts + ((g.B_shift == 1 ? 0 : b) * g.P + p) * 2 : nullptr;
         const bool tiled = pose_is_rotation_d<DIM>(R);
+        if (ZEROED && tiled) continue;  // block-uniform
         Cx<float>* outp = out + bp * g.npix;
         // one row per wave, lanes along the row (no per-pixel division)
         for (int i = threadIdx.x / 64; i < g.n; i += kBlock / 64) {
@@ -181,15 +183,18 @@ hipError_t forw(const Geom& g, const void* rec, const void* rot, const void* shi
 
 template <int DIM, bool CUBIC>
 hipError_t forw_rest(const Geom& g, const void* rec, const void* rot, const void* shifts, void* out, hipStream_t s) {
-    hipLaunchKernelGGL((k_project_forw_rest<DIM, CUBIC>), dim3(grid_for(g.B * g.P)), dim3(kBlock), 0, s, g,
-                       (const Cx<float>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
+    // 2D: the C ABI zero-fills the output first (a streaming fill beats per-row masked zeros)
+    hipLaunchKernelGGL((k_project_forw_rest<DIM, CUBIC, DIM == 2>), dim3(grid_for(g.B * g.P)), dim3(kBlock), 0, s,
+                       g, (const Cx<float>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
     return hipGetLastError();
 }
 
 template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT, int REST>
 hipError_t back4(const Geom& g, const void* gproj, const void* rec, const void* rot, const void* shifts, void* grec,
                  void* grot, void* gshift, hipStream_t s) {
-    hipLaunchKernelGGL((k_project_back<DIM, T, CUBIC, ROT, SHIFT, REST>), dim3(grid_for(g.work)), dim3(kBlock), 0,
+    // with REST most (pose, chunk) items are skipped at once: fewer, longer-lived blocks
+    const unsigned grid = REST ? unsigned(g.work < 8192 ? g.work : 8192) : grid_for(g.work);
+    hipLaunchKernelGGL((k_project_back<DIM, T, CUBIC, ROT, SHIFT, REST>), dim3(grid), dim3(kBlock), 0,
                        s, g, (const Cx<T>*)gproj, (const Cx<T>*)rec, (const T*)rot, (const T*)shifts, (Cx<T>*)grec,
                        (T*)grot, (T*)gshift);
     return hipGetLastError();
