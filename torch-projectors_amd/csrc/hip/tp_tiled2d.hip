@@ -469,6 +469,40 @@ hipError_t scatter2_kp(const Geom& g, const TileSpec2& ts, const void* src, cons
 constexpr int GC = kGat2, GR = kGat2;
 constexpr double kTwoPi2 = 6.283185307179586476925286766559;
 
+// Bicubic value and gradient with the 16 taps reduced along c first (value
+// and d/dc weights), then r.  EXACT_V keeps the value in the reference's order
+// ((s * wr) * wc summed over r then c, interpolation_kernels.h:258-322) for
+// outputs that are gathers; the gradient carries the 1e-4 bar either way.
+template <bool EXACT_V, typename F>
+__device__ __forceinline__ Interp<float> cubic2_grads(F&& fetch, float r, float c) {
+    float cx, rx;
+    const int cf = split_as<false>(c, cx), rf = split_as<false>(r, rx);
+    float wc[4], dwc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        wc[j] = cubic_w<float>(cx - float(j - 1));
+        dwc[j] = cubic_dw<float>(cx - float(j - 1));
+    }
+    Interp<float> o;
+    o.v = o.g[0] = o.g[1] = o.g[2] = {0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float wr = cubic_w<float>(rx - float(i - 1)), dwr = cubic_dw<float>(rx - float(i - 1));
+        Cx<float> a = {0.f, 0.f}, bc = {0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const Cx<float> t = fetch(rf + i - 1, cf + j - 1);
+            if (EXACT_V) o.v = cadd(o.v, cscale(cscale(t, wr), wc[j]));
+            a = cadd(a, cscale(t, wc[j]));
+            bc = cadd(bc, cscale(t, dwc[j]));
+        }
+        if (!EXACT_V) o.v = cadd(o.v, cscale(a, wr));
+        o.g[0] = cadd(o.g[0], cscale(bc, wr));
+        o.g[1] = cadd(o.g[1], cscale(a, dwr));
+    }
+    return o;
+}
+
 template <bool CUBIC, int KP, int GMODE, bool RS, bool WG>
 __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts, const Cx<float>* __restrict__ rec,
                                                             const float* __restrict__ gw,
@@ -608,8 +642,10 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
                         if (fxc < tc || fxc >= tc + GC || fxr < tr || fxr >= tr + GR) continue;
                         const int i = rr >= 0 ? rr : rr + g.n;
                         const int64_t pidx = (pose0 + sd.p) * int64_t(g.npix) + i * g.hp + cc;
-                        const Interp<float> ip = CUBIC ? cubic2<float, GRADS, false>(lds, x[1], x[0])
-                                                       : lerp2<float, GRADS, false>(lds, x[1], x[0]);
+                        Interp<float> ip;
+                        if constexpr (CUBIC && GRADS) ip = cubic2_grads<GMODE == 2>(lds, x[1], x[0]);
+                        else if constexpr (CUBIC) ip = cubic2<float, false, false>(lds, x[1], x[0]);
+                        else ip = lerp2<float, GRADS, false>(lds, x[1], x[0]);
                         const Cx<float> ph = shifts ? phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k) : Cx<float>{1.f, 0.f};
                         if constexpr (GMODE == 0) {
                             out[pidx] = shifts ? cmul(ip.v, ph) : ip.v;
