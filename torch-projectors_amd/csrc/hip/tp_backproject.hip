@@ -116,16 +116,21 @@ __global__ __launch_bounds__(kBlock) void k_backproject_back(Geom g, const Cx<T>
     constexpr int K = RS + 2;
     __shared__ T red[kBlock / 64][K];
     const T cut2 = T(g.cut2);
-    for (int64_t w = blockIdx.x; w < g.work; w += gridDim.x) {
+    // REST: one pose per outer step, skipped at once when it is a rotation
+    const int64_t outer_n = REST ? g.B * g.P : g.work;
+    for (int64_t outer = blockIdx.x; outer < outer_n; outer += gridDim.x) {
+      if constexpr (REST) {
+        const int64_t b0 = outer / g.P;
+        if (pose_is_rotation_d<DIM>(rot + ((g.B_rot == 1 ? 0 : b0) * g.P + (outer - b0 * g.P)) * RS)) continue;
+      }
+      for (int ch = 0; ch < (REST ? g.chunks : 1); ++ch) {
+        const int64_t w = REST ? outer * g.chunks + ch : outer;
         const int64_t bp = w / g.chunks;
         int i = 0, j = 0;
         const bool in_rect = rect_pixel(g, int(w - bp * g.chunks) * kBlock + int(threadIdx.x), i, j);
         const int pix = i * g.hp + j;
         const int64_t b = bp / g.P, p = bp - b * g.P;
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
-        if constexpr (REST) {
-            if (pose_is_rotation_d<DIM>(rot + (rb * g.P + p) * RS)) continue;  // block-uniform
-        }
         T acc[K];
 #pragma unroll
         for (int k = 0; k < K; ++k) acc[k] = T(0);
@@ -175,6 +180,7 @@ __global__ __launch_bounds__(kBlock) void k_backproject_back(Geom g, const Cx<T>
                     for (int k = 0; k < 2; ++k) atomic_add(&gshift[(sb * g.P + p) * 2 + k], acc[RS + k]);
             }
         }
+      }
     }
 }
 
@@ -210,7 +216,7 @@ hipError_t forw_rest(const Geom& g, const void* proj, const void* weights, const
 template <int DIM, typename T, bool CUBIC, bool WG, bool ROT, bool SHIFT, bool REST>
 hipError_t back8(const Geom& g, const void* gdata, const void* gw, const void* proj, const void* rot,
                  const void* shifts, void* gproj, void* gweights, void* grot, void* gshift, hipStream_t s) {
-    const unsigned grid = REST ? unsigned(g.work < 8192 ? g.work : 8192) : grid_for(g.work);
+    const unsigned grid = REST ? grid_for(g.B * g.P) : grid_for(g.work);
     hipLaunchKernelGGL((k_backproject_back<DIM, T, CUBIC, WG, ROT, SHIFT, REST>), dim3(grid), dim3(kBlock), 0,
                        s, g, (const Cx<T>*)gdata, (const T*)gw, (const Cx<T>*)proj, (const T*)rot, (const T*)shifts,
                        (Cx<T>*)gproj, (T*)gweights, (T*)grot, (T*)gshift);
@@ -253,15 +259,24 @@ hipError_t back(const Geom& g, const void* gdata, const void* gw, const void* pr
         return cubic ? FN<3, double, true>(__VA_ARGS__) : FN<3, double, false>(__VA_ARGS__);                   \
     } while (0)
 
-// Zero fill with 16-byte stores over the aligned body.
+// Zero fill with 16-byte streaming (non-temporal) stores over the aligned
+// body, four per lane per step.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(kBlock) void k_zero(uint32_t* __restrict__ p, int64_t head, int64_t quads,
                                                  int64_t words) {
-    const int64_t stride = int64_t(gridDim.x) * kBlock;
     const int64_t t = int64_t(blockIdx.x) * kBlock + threadIdx.x;
     if (t < head) p[t] = 0u;
-    uint4* q = reinterpret_cast<uint4*>(p + head);
-    for (int64_t k = t; k < quads; k += stride) q[k] = make_uint4(0u, 0u, 0u, 0u);
-    for (int64_t k = head + quads * 4 + t; k < words; k += stride) p[k] = 0u;
+    u32x4* q = reinterpret_cast<u32x4*>(p + head);
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    const int64_t step = int64_t(gridDim.x) * kBlock * 4;
+    int64_t k = int64_t(blockIdx.x) * kBlock * 4 + threadIdx.x;
+    for (; k + 3 * kBlock < quads; k += step) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) __builtin_nontemporal_store(z, q + k + u * kBlock);
+    }
+    for (int u = 0; u < 4; ++u)
+        if (k + u * kBlock < quads) __builtin_nontemporal_store(z, q + k + u * kBlock);
+    for (int64_t e = head + quads * 4 + t; e < words; e += int64_t(gridDim.x) * kBlock) p[e] = 0u;
 }
 
 // Zero elements [lo, hi) of a 4- or 8-byte-element array with 16-byte stores

@@ -104,18 +104,23 @@ __global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __
     constexpr int K = RS + 2;
     __shared__ T red[kBlock / 64][K];
     const T cut2 = T(g.cut2);
-    for (int64_t w = blockIdx.x; w < g.work; w += gridDim.x) {
+    // REST: one pose per outer step, checked once
+    const int64_t outer_n = REST != 0 ? g.B * g.P : g.work;
+    for (int64_t outer = blockIdx.x; outer < outer_n; outer += gridDim.x) {
+      bool scatter = true;
+      if constexpr (REST != 0) {
+        const int64_t b0 = outer / g.P;
+        scatter = !pose_is_rotation_d<DIM>(rot + ((g.B_rot == 1 ? 0 : b0) * g.P + (outer - b0 * g.P)) * RS);
+        if (!scatter && (REST == 2 || (!ROT && !SHIFT))) continue;  // block-uniform
+      }
+      for (int ch = 0; ch < (REST != 0 ? g.chunks : 1); ++ch) {
+        const int64_t w = REST != 0 ? outer * g.chunks + ch : outer;
         const int64_t bp = w / g.chunks;
         int i = 0, j = 0;
         const bool in_rect = rect_pixel(g, int(w - bp * g.chunks) * kBlock + int(threadIdx.x), i, j);
         const int pix = i * g.hp + j;
         const int64_t b = bp / g.P, p = bp - b * g.P;
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
-        bool scatter = true;
-        if constexpr (REST != 0) {
-            scatter = !pose_is_rotation_d<DIM>(rot + (rb * g.P + p) * RS);
-            if (!scatter && (REST == 2 || (!ROT && !SHIFT))) continue;  // block-uniform
-        }
         T acc[K];
 #pragma unroll
         for (int k = 0; k < K; ++k) acc[k] = T(0);
@@ -169,6 +174,7 @@ __global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __
                     for (int k = 0; k < 2; ++k) atomic_add(&gshift[(sb * g.P + p) * 2 + k], acc[RS + k]);
             }
         }
+      }
     }
 }
 
@@ -193,7 +199,7 @@ template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT, int REST>
 hipError_t back4(const Geom& g, const void* gproj, const void* rec, const void* rot, const void* shifts, void* grec,
                  void* grot, void* gshift, hipStream_t s) {
     // with REST most (pose, chunk) items are skipped at once: fewer, longer-lived blocks
-    const unsigned grid = REST ? unsigned(g.work < 8192 ? g.work : 8192) : grid_for(g.work);
+    const unsigned grid = REST ? grid_for(g.B * g.P) : grid_for(g.work);
     hipLaunchKernelGGL((k_project_back<DIM, T, CUBIC, ROT, SHIFT, REST>), dim3(grid), dim3(kBlock), 0,
                        s, g, (const Cx<T>*)gproj, (const Cx<T>*)rec, (const T*)rot, (const T*)shifts, (Cx<T>*)grec,
                        (T*)grot, (T*)gshift);
