@@ -16,8 +16,8 @@ pytestmark = pytest.mark.gpu
 def _cases():
     out = []
     seed = 555000
-    for op in ("project_3d_to_2d_forw", "backproject_2d_to_3d_forw", "project_3d_to_2d_back", "project_2d_forw",
-               "backproject_2d_forw"):
+    for op in ("project_3d_to_2d_forw", "backproject_2d_to_3d_forw", "project_3d_to_2d_back",
+               "backproject_2d_to_3d_back", "project_2d_forw", "backproject_2d_forw"):
         for interp in ("linear", "cubic"):
             for os_, cut in ((1.1, None), (1.3, 7.5), (1.7, None), (2.2, 11.0)):
                 seed += 1

@@ -366,9 +366,13 @@ hipError_t launch_backproject_forw(int dim, int dt, bool cubic, const Geom& g, c
 hipError_t launch_backproject_back(int dim, int dt, bool cubic, const Geom& g, const void* gdata, const void* gw,
                                    const void* proj, const void* rot, const void* shifts, void* gproj,
                                    void* gweights, void* grot, void* gshift, hipStream_t s, bool rest_only) {
-    if (rest_only && dim == 2 && dt == 0)
-        return cubic ? back<2, float, true, true>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s)
-                     : back<2, float, false, true>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+    if (rest_only && dt == 0) {
+        if (dim == 2)
+            return cubic ? back<2, float, true, true>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s)
+                         : back<2, float, false, true>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+        return cubic ? back<3, float, true, true>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s)
+                     : back<3, float, false, true>(g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+    }
     TP_DISPATCH(dim, dt, cubic, back, g, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
 }
 

@@ -385,16 +385,22 @@ int backproject_back(int dim, int dtype, const void* gdata, const void* gw, int6
     TP_TRY(need(gproj, "grad_projections"));
     const bool cubic = interp == TP_CUBIC;
     const bool tiles2 = use_tiles2(dim, dtype, os, n);
-    if (tiles2) {
+    const bool tiles = use_tiles(dim, dtype, os, n);
+    if (tiles2 || tiles) {
+        // the tiled gathers write the active pixels of rotation poses, the per-pixel kernel the rest
         TP_TRY(zero(gproj, cx_words(dtype, g.B * g.P * int64_t(g.npix)), s));
         TP_TRY(zero(gweights, re_words(dtype, g.B * g.P * int64_t(g.npix)), s));
     }
+    if (tiles)
+        TP_TRY(launched(tp::launch_bpback3_tiled(cubic, g, tile_spec(g, cubic), gdata, gw, proj, rot, shifts, gproj,
+                                                 gweights, grot, gshift, s),
+                        "tiled backprojection backward launch"));
     if (tiles2)
         TP_TRY(launched(tp::launch_gather2_tiled(cubic, 2, g, tile_spec2(g, cubic), gdata, gw, rot, shifts, gproj,
                                                  (gw && gweights) ? gweights : nullptr, proj, grot, gshift, s),
                         "tiled backprojection backward launch"));
     return launched(tp::launch_backproject_back(dim, dtype, cubic, g, gdata, gw, proj, rot, shifts, gproj, gweights,
-                                                grot, gshift, s, tiles2),
+                                                grot, gshift, s, tiles2 || tiles),
                     "backprojection backward launch");
 }
 

@@ -99,6 +99,12 @@ hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec&
 // into zero-filled grot / gshift (either may be null).
 hipError_t launch_grads3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gproj, const void* rec,
                                const void* rot, const void* shifts, void* grot, void* gshift, hipStream_t s);
+// backproject_2d_to_3d_back for rotation poses into zero-filled outputs:
+// grad_projections from grad_data_rec, grad_weights from grad_weight_rec (when
+// both gw and gweights are given), rotation/shift gradients (either may be null).
+hipError_t launch_bpback3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gdata, const void* gw,
+                                const void* proj, const void* rot, const void* shifts, void* gproj, void* gweights,
+                                void* grot, void* gshift, hipStream_t s);
 // mode 0: backprojection into data (+ weights), with the x = 0 Hermitian completion;
 // mode 1: reconstruction gradient of the projection.
 hipError_t launch_scatter3_tiled(bool cubic, int mode, const Geom& g, const TileSpec& ts, const void* src,
@@ -139,8 +145,8 @@ hipError_t launch_normalize(int dt, const void* data, const void* weights, int64
 int fft_forward(int dt, int dim, int64_t batch, int64_t N, const void* real, void* spec, hipStream_t s);
 int fft_inverse(int dt, int dim, int64_t batch, int64_t N, void* spec, void* real, hipStream_t s);
 
-// `rest_only` (fp32 2D): rotation poses only get zeros on their masked pixels
-// (launch_gather2_tiled mode 2 computed the rest); other poses everything.
+// `rest_only` (fp32): rotation poses were computed by the tiled gathers into
+// zero-filled outputs and are skipped; other poses everything.
 hipError_t launch_backproject_back(int dim, int dt, bool cubic, const Geom& g, const void* gdata, const void* gw,
                                    const void* proj, const void* rot, const void* shifts, void* gproj,
                                    void* gweights, void* grot, void* gshift, hipStream_t s, bool rest_only = false);

@@ -296,13 +296,21 @@ __device__ __forceinline__ void cull_chunk_boxes(const float* __restrict__ rotb,
 //          from the staged tile, paired with grad_projections `gsrc` as in
 //          cpu/3d/projection_3d_to_2d_kernels.cpp:344-379; a wave sums its
 //          pose's terms and adds them to grot / gshift (either may be null).
+// GMODE 2: backproject_2d_to_3d_back for rotation poses (KP = 1): `rec` is
+//          grad_data_rec; grad_projections (`out`) gathered with the value in
+//          the reference's order, grad_weights (`wout`, WG) trilinearly from a
+//          second staged tile of grad_weight_rec `gw` with the weight-tap rules,
+//          and with RS the rotation/shift gradients against the projections
+//          `gsrc` (cpu/3d/backprojection_2d_to_3d_kernels.cpp:451-567).
 constexpr double kTwoPi = 6.283185307179586476925286766559;
 
 // Tricubic value and spatial gradient for the gradient sums (which carry the
 // 1e-4 bar, not bit-identity): the 64 taps are reduced along c first (value
 // and d/dc weights), then r, then d, instead of forming the four triple
-// products per tap.  Weights and taps as cubic3 (interpolation_kernels.h:345-425).
-template <typename F>
+// products per tap.  EXACT_V also forms the value in the reference's order
+// (((s * wd) * wr) * wc summed over d, r, c) for outputs that are gathers.
+// Weights and taps as cubic3 (interpolation_kernels.h:345-425).
+template <bool EXACT_V, typename F>
 __device__ __forceinline__ Interp<float> cubic3_grads(F&& fetch, float d, float r, float c) {
     float dx, rx, cx;
     const int df = split_as<false>(d, dx), rf = split_as<false>(r, rx), cf = split_as<false>(c, cx);
@@ -316,8 +324,10 @@ __device__ __forceinline__ Interp<float> cubic3_grads(F&& fetch, float d, float 
     }
     Interp<float> o;
     o.v = o.g[0] = o.g[1] = o.g[2] = {0.f, 0.f};
+    Cx<float> ve = {0.f, 0.f};  // EXACT_V: the value in the reference's order
 #pragma unroll 1
     for (int k = 0; k < 4; ++k) {
+        const float wd = cubic_w<float>(dx - float(k - 1)), dwd = cubic_dw<float>(dx - float(k - 1));
         Cx<float> pv = {0.f, 0.f}, pc = {0.f, 0.f}, pr = {0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -325,6 +335,7 @@ __device__ __forceinline__ Interp<float> cubic3_grads(F&& fetch, float d, float 
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const Cx<float> t = fetch(df + k - 1, rf + i - 1, cf + j - 1);
+                if (EXACT_V) ve = cadd(ve, cscale(cscale(cscale(t, wd), wr[i]), wc[j]));
                 a = cadd(a, cscale(t, wc[j]));
                 bc = cadd(bc, cscale(t, dwc[j]));
             }
@@ -332,24 +343,29 @@ __device__ __forceinline__ Interp<float> cubic3_grads(F&& fetch, float d, float 
             pc = cadd(pc, cscale(bc, wr[i]));
             pr = cadd(pr, cscale(a, dwr[i]));
         }
-        const float wd = cubic_w<float>(dx - float(k - 1)), dwd = cubic_dw<float>(dx - float(k - 1));
         o.v = cadd(o.v, cscale(pv, wd));
         o.g[0] = cadd(o.g[0], cscale(pc, wd));
         o.g[1] = cadd(o.g[1], cscale(pr, wd));
         o.g[2] = cadd(o.g[2], cscale(pv, dwd));
     }
+    if (EXACT_V) o.v = ve;
     return o;
 }
 
-template <bool CUBIC, int KP, bool OSX, int GMODE = 0>
+template <bool CUBIC, int KP, bool OSX, int GMODE = 0, bool RS = true, bool WG = false>
 __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ rec,
                                                         const float* __restrict__ rot,
                                                         const float* __restrict__ shifts,
                                                         Cx<float>* __restrict__ out,
                                                         const Cx<float>* __restrict__ gsrc = nullptr,
                                                         float* __restrict__ grot = nullptr,
-                                                        float* __restrict__ gshift = nullptr) {
-    static_assert(GMODE == 0 || KP == 1, "the gradient mode sums one pose per wave batch");
+                                                        float* __restrict__ gshift = nullptr,
+                                                        const float* __restrict__ gw = nullptr,
+                                                        float* __restrict__ wout = nullptr) {
+    static_assert(GMODE == 0 || KP == 1, "the gradient modes sum one pose per wave batch");
+    constexpr bool GRADS = GMODE == 1 || (GMODE == 2 && RS);
+    constexpr int WW = (GMODE == 2 && WG) ? (L + 1) * (L + 1) * (LD + 1) : 1;  // trilinear weight taps
+    __shared__ float wt[WW];
     constexpr int LO = CUBIC ? 1 : 0, HI = CUBIC ? 2 : 1, W = L + LO + HI, WD = LD + LO + HI, W3 = W * W * WD;
     constexpr int RPS = 64 / KP;
     constexpr int NT = kForwThreads, NW = NT / 64;
@@ -432,6 +448,13 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                     for (int q = 0; q < STAGE; ++q)
                         if (tid + (q0 + q) * NT < W3) vt[tid + (q0 + q) * NT] = v[q];
                 }
+                if constexpr (GMODE == 2 && WG) {
+                    const float* gwb = gw + b * g.vol;
+                    for (int e = tid; e < WW; e += NT) {
+                        const int lc = e % (L + 1), lr = (e / (L + 1)) % (L + 1), ld = e / ((L + 1) * (L + 1));
+                        wt[e] = weight_tap<3>(gwb, N, H, td + ld, tr + lr, tc + lc);
+                    }
+                }
                 __syncthreads();
                 loaded = true;
             }
@@ -489,8 +512,8 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                         const Slot& sd = slots[wave][sl];
                         const float fr = float(rr), fc = float(cc);
                         if (filtered(fr, fc, cut2)) continue;
-                        // the backward skips the Friedel half of the x = 0 line
-                        if (GMODE == 1 && cc == 0 && (rr == g.n / 2 || rr < 0)) continue;
+                        // the backward ops skip the Friedel half of the x = 0 line
+                        if (GMODE != 0 && cc == 0 && (rr == g.n / 2 || rr < 0)) continue;
                         float x[3];
                         rotate_slice<OSX>(sd.R, fr, fc, g.os, x);
                         const int fxc = int(floorf(x[0])), fxr = int(floorf(x[1])), fxd = int(floorf(x[2]));
@@ -502,8 +525,57 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                                                 : lerp3<float, false, false>(lds, x[2], x[1], x[0]).v;
                             if (shifts) v = cmul(v, phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k));
                             out[sd.base + i * g.hp + cc] = v;
+                        } else if constexpr (GMODE == 2) {
+                            Interp<float> ip;
+                            if constexpr (CUBIC && GRADS) ip = cubic3_grads<true>(lds, x[2], x[1], x[0]);
+                            else if constexpr (CUBIC) ip = cubic3<float, false, false>(lds, x[2], x[1], x[0]);
+                            else ip = lerp3<float, GRADS, false>(lds, x[2], x[1], x[0]);
+                            const int64_t pidx = sd.base + i * g.hp + cc;
+                            const Cx<float> ph = shifts ? phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k)
+                                                        : Cx<float>{1.f, 0.f};
+                            out[pidx] = shifts ? cmul(ip.v, ph) : ip.v;
+                            if constexpr (WG) {
+                                // trilinear as weight_grad_interp<3>
+                                float cx, rx, dx;
+                                const int cf = split_as<false>(x[0], cx), rf = split_as<false>(x[1], rx),
+                                          df = split_as<false>(x[2], dx);
+                                auto wa = [&](int d, int r, int c) {
+                                    return wt[((d - td) * (L + 1) + (r - tr)) * (L + 1) + (c - tc)];
+                                };
+                                const float p000 = wa(df, rf, cf), p001 = wa(df, rf, cf + 1);
+                                const float p010 = wa(df, rf + 1, cf), p011 = wa(df, rf + 1, cf + 1);
+                                const float p100 = wa(df + 1, rf, cf), p101 = wa(df + 1, rf, cf + 1);
+                                const float p110 = wa(df + 1, rf + 1, cf), p111 = wa(df + 1, rf + 1, cf + 1);
+                                const float p00 = p000 + (p001 - p000) * cx;
+                                const float p01 = p010 + (p011 - p010) * cx;
+                                const float p10 = p100 + (p101 - p100) * cx;
+                                const float p11 = p110 + (p111 - p110) * cx;
+                                const float p0 = p00 + (p01 - p00) * rx;
+                                const float p1 = p10 + (p11 - p10) * rx;
+                                wout[pidx] = p0 + (p1 - p0) * dx;
+                            }
+                            if constexpr (GRADS) {
+                                // proj * conj(phase) against dF/dx * s and against -i 2 pi k / n * F
+                                Cx<float> pv = gsrc[pidx];
+                                if (shifts) pv = cmul(pv, cconj(ph));
+                                if (grot) {
+                                    const float sc = OSX ? fc * float(g.os) : float(double(fc) * g.os);
+                                    const float sr = OSX ? fr * float(g.os) : float(double(fr) * g.os);
+#pragma unroll
+                                    for (int row = 0; row < 3; ++row) {
+                                        acc[row * 3 + 0] += cmul(pv, cconj(cscale(ip.g[row], sc))).re;
+                                        acc[row * 3 + 1] += cmul(pv, cconj(cscale(ip.g[row], sr))).re;
+                                    }
+                                }
+                                if (gshift) {
+                                    const Cx<float> kr = {0.f, float(-kTwoPi * double(fr) / double(g.n))};
+                                    const Cx<float> kc = {0.f, float(-kTwoPi * double(fc) / double(g.n))};
+                                    acc[9] += cmul(pv, cconj(cmul(kr, ip.v))).re;
+                                    acc[10] += cmul(pv, cconj(cmul(kc, ip.v))).re;
+                                }
+                            }
                         } else {
-                            const Interp<float> ip = CUBIC ? cubic3_grads(lds, x[2], x[1], x[0])
+                            const Interp<float> ip = CUBIC ? cubic3_grads<false>(lds, x[2], x[1], x[0])
                                                            : lerp3<float, true, false>(lds, x[2], x[1], x[0]);
                             const Cx<float> g0 = gsrc[sd.base + i * g.hp + cc];
                             const Cx<float> ph = shifts ? phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k)
@@ -530,7 +602,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                       }
                     }
                 }
-                if constexpr (GMODE == 1) {
+                if constexpr (GRADS) {
                     // the pose's sums (every lane of the wave takes part; one adds them)
                     if (grot) {
 #pragma unroll
@@ -946,6 +1018,35 @@ hipError_t grads_launch(const Geom& g, const TileSpec& ts, const void* gproj, co
     return hipGetLastError();
 }
 
+template <bool CUBIC, bool OSX, bool RS, bool WG>
+hipError_t bpback_launch(const Geom& g, const TileSpec& ts, const void* gdata, const void* gw, const void* proj,
+                         const void* rot, const void* shifts, void* gproj, void* gweights, void* grot, void* gshift,
+                         hipStream_t s) {
+    const int64_t fcore = int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fd1 - ts.fd0) * ts.ksplit;
+    const int64_t work = g.B * (fcore + int64_t(ts.nt) * ts.nt * ts.ntfd);
+    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, 1, OSX, 2, RS, WG>), dim3(grid_for(kXcds * xcd_per<kRunForw>(work))),
+                       dim3(kForwThreads), 0, s, g, ts, (const Cx<float>*)gdata, (const float*)rot,
+                       (const float*)shifts, (Cx<float>*)gproj, (const Cx<float>*)proj, (float*)grot, (float*)gshift,
+                       (const float*)gw, (float*)gweights);
+    return hipGetLastError();
+}
+
+template <bool CUBIC, bool OSX>
+hipError_t bpback_flags(const Geom& g, const TileSpec& ts, const void* gdata, const void* gw, const void* proj,
+                        const void* rot, const void* shifts, void* gproj, void* gweights, void* grot, void* gshift,
+                        hipStream_t s) {
+    const bool rs = grot || gshift, wg = gw && gweights;
+    if (rs)
+        return wg ? bpback_launch<CUBIC, OSX, true, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
+                                                          gshift, s)
+                  : bpback_launch<CUBIC, OSX, true, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, nullptr, grot,
+                                                           gshift, s);
+    return wg ? bpback_launch<CUBIC, OSX, false, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
+                                                       gshift, s)
+              : bpback_launch<CUBIC, OSX, false, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, nullptr, grot,
+                                                        gshift, s);
+}
+
 template <bool CUBIC, bool OSX>
 hipError_t forw_kp(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts, void* out,
                    hipStream_t s) {
@@ -973,6 +1074,16 @@ hipError_t launch_grads3_tiled(bool cubic, const Geom& g, const TileSpec& ts, co
                            : grads_launch<true, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, s);
     return ts.os_exact ? grads_launch<false, true>(g, ts, gproj, rec, rot, shifts, grot, gshift, s)
                        : grads_launch<false, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, s);
+}
+
+hipError_t launch_bpback3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gdata, const void* gw,
+                                const void* proj, const void* rot, const void* shifts, void* gproj, void* gweights,
+                                void* grot, void* gshift, hipStream_t s) {
+    if (cubic)
+        return ts.os_exact ? bpback_flags<true, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s)
+                           : bpback_flags<true, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+    return ts.os_exact ? bpback_flags<false, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s)
+                       : bpback_flags<false, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
 }
 
 hipError_t launch_scatter3_tiled(bool cubic, int mode, const Geom& g, const TileSpec& ts, const void* src,
