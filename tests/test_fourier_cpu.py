@@ -176,3 +176,22 @@ def test_wrapper_errors_follow_the_reference():
         fourier.pad_and_fftshift(torch.zeros(8, 8), 2.0)
     with pytest.raises(RuntimeError, match="on the GPU"):
         fourier.ifftshift_and_crop(torch.zeros(8, 8), 2.0)
+
+
+@pytest.mark.parametrize("fn,args,msg", [
+    ("tp_rfftn", (5, 3, 1, 8), "dtype"),
+    ("tp_rfftn", (0, 4, 1, 8), "dim"),
+    ("tp_rfftn", (0, 3, -1, 8), "batch"),
+    ("tp_rfftn", (0, 3, 1, 0), "boxsize"),
+    ("tp_irfftn", (1, 2, 1, 1 << 31), "boxsize"),
+])
+def test_capi_fft_rejects(fn, args, msg):
+    rc = getattr(capi.lib(), fn)(*args, _P(8), _P(8), _P(None))
+    assert rc == capi.TP_ERR_INVALID
+    assert msg in capi.lib().tp_last_error().decode()
+
+
+def test_capi_fft_nothing_to_do():
+    # no boxes: nothing enqueued, no pointers needed (no GPU touched)
+    assert capi.lib().tp_rfftn(0, 3, 0, 8, _P(None), _P(None), _P(None)) == capi.TP_OK
+    assert capi.lib().tp_irfftn(0, 2, 0, 8, _P(None), _P(None), _P(None)) == capi.TP_OK
