@@ -277,10 +277,11 @@ __device__ __forceinline__ void cull_chunk_boxes(const float* __restrict__ rotb,
 #pragma unroll
         for (int q = 0; q < kCullInFlight; ++q) {
             const int p = pbase + int(threadIdx.x) + (q0 + q) * NT;
-            if (p >= pend || !pose_is_rotation(R[q])) continue;
-            if (plane_hits(R[q], lo1, hi1) && half_plane_hits(R[q], hi1, lo1))
-                plist[atomicAdd(&pcnt[0], 1)] = (unsigned short)(p - pbase);
-            if (plane_hits(R[q], lo2, hi2) && half_plane_hits(R[q], hi2, lo2))
+            // box 2 is box 1 negated (bit for bit), which a plane through the origin
+            // crosses exactly when it crosses box 1: one plane test serves both
+            if (p >= pend || !pose_is_rotation(R[q]) || !plane_hits(R[q], lo1, hi1)) continue;
+            if (half_plane_hits(R[q], hi1, lo1)) plist[atomicAdd(&pcnt[0], 1)] = (unsigned short)(p - pbase);
+            if (half_plane_hits(R[q], hi2, lo2))
                 plist[kChunk - 1 - atomicAdd(&pcnt[1], 1)] = (unsigned short)(p - pbase);
         }
     }
@@ -750,6 +751,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
         const float lo2[3] = {float(fc0 - SL) - ts.eps, float(fr0 - SL) - ts.eps, float(fd0 - SL) - ts.eps};
         const float hi2[3] = {float(fc0 + SC + SH) + ts.eps, float(fr0 + SR + SH) + ts.eps,
                               float(fd0 + SD + SH) + ts.eps};
+        static_assert(SL - SH == 1, "box 2 is box 1 negated when the stencil reaches one cell further below");
         for (int e = tid; e < S3; e += NT) {
             acc_re[e] = 0.0;
             acc_im[e] = 0.0;
