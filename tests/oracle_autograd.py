@@ -2,12 +2,13 @@
 
 The four differentiable operators of the reference's Python API
 (torch_projectors/ops.py:29-264 of the reference) with the oracle's forward
-and backward functions under torch.autograd, so the gradient-property checks
-of tests/autograd_props.py run on the CPU restatement as they do on the HIP
-operators.  Rotation/shift gradients are requested exactly when autograd
+and backward functions under torch.autograd, so the property checks of
+tests/reference_props.py run on the CPU restatement as they do on the HIP
+operators; pad_and_fftshift and ifftshift_and_crop are oracle/fourier.py's.  Rotation/shift gradients are requested exactly when autograd
 needs them, as the reference's backward does (ops.py:430-514).  Tensors are
 CPU tensors; poses are [B_rot, P, d, d] and shifts [B_shift, P, 2].
 """
+from oracle import fourier as OF
 from oracle import oracle as O
 
 import torch
@@ -93,3 +94,11 @@ def backproject_2d_to_3d_forw(projections, rotations, weights=None, shifts=None,
                               oversampling=1.0, fourier_radius_cutoff=None):
     return _Backproject.apply(O.backproject_2d_to_3d_forw, O.backproject_2d_to_3d_back, projections, weights,
                               rotations, shifts, interpolation, oversampling, fourier_radius_cutoff)
+
+
+def pad_and_fftshift(tensor, oversampling_factor):
+    return torch.from_numpy(OF.pad_and_fftshift(tensor.detach().cpu().numpy(), oversampling_factor))
+
+
+def ifftshift_and_crop(real_tensor, oversampling_factor):
+    return torch.from_numpy(OF.ifftshift_and_crop(real_tensor.detach().cpu().numpy(), oversampling_factor).copy())

@@ -1,10 +1,11 @@
-"""Gradient and batching properties of the public operators.
+"""Gradient, batching and oversampling properties of the public operators.
 
 The checks follow the reference's own test strategy for these operators
 (tests/2d/forw/test_gradients.py, tests/2d/back/test_gradients_back.py,
 tests/3d/forw/test_gradients_3d_to_2d.py,
-tests/3d/back/test_gradients_back_2d_to_3d.py and the test_batching*.py
-files beside them), with the same sizes, poses and tolerances:
+tests/3d/back/test_gradients_back_2d_to_3d.py and the test_batching*.py and
+test_oversampling*.py files beside them), with the same sizes, poses and
+tolerances:
 
 * torch.autograd.gradcheck in complex128/float64 (atol 1e-4, rtol 1e-2).  The
   x = 0 column entries whose Friedel mates are written or read by the forward
@@ -19,12 +20,18 @@ files beside them), with the same sizes, poses and tolerances:
 * one gradient step from a zero image through a real-space loss correlates
   with the image that made the target;
 * batched and broadcast calls equal per-item calls; backprojecting in two
-  halves and adding equals backprojecting all at once.
+  halves and adding equals backprojecting all at once;
+* projecting a spectrum padded `os` times with oversampling `os` equals
+  projecting the unpadded one (a quarter turn keeps every sample on the
+  grid, so the two agree to rounding once the 1/os^dim of the padded
+  transform is undone), and backprojections at oversampling 1 and `os`
+  agree in real space after ifftshift_and_crop.
 
 Every check takes `api` — a module with the public functions project_2d_forw,
-project_3d_to_2d_forw, backproject_2d_forw and backproject_2d_to_3d_forw —
-and a device, so the same bodies run on the HIP operators (cuda:0) and on the
-CPU oracle (tests/oracle_autograd.py).  Inputs come from seeded CPU
+project_3d_to_2d_forw, backproject_2d_forw and backproject_2d_to_3d_forw, and
+for the oversampling checks pad_and_fftshift and ifftshift_and_crop — and a
+device, so the same bodies run on the HIP operators (cuda:0) and on the CPU
+oracle (tests/oracle_autograd.py).  Inputs come from seeded CPU
 generators and are then moved to the device, so both see the same numbers.
 """
 import math
@@ -445,3 +452,94 @@ def batching_backprojection(api, dev, dim, interp):
     e, _ = bp(proj, rotations=rot1.expand(B, P, dim, dim).contiguous(), shifts=sh.expand(B, P, 2).contiguous(),
               interpolation=interp)
     assert torch.allclose(a, e, atol=1e-5)
+
+
+# ----------------------------------------------------------------------------- oversampling
+def quarter_turn(dim, dev):
+    if dim == 2:
+        R = [[0.0, -1.0], [1.0, 0.0]]
+    else:
+        R = [[0.0, 0.0, 1.0], [0.0, 1.0, 0.0], [-1.0, 0.0, 0.0]]
+    return torch.tensor(R, device=dev)[None, None]
+
+
+def oversampling_projection(api, dev, dim, interp, os_, B):
+    """Reference: tests/2d/forw/test_oversampling.py:17-100,
+    tests/3d/forw/test_oversampling_3d_to_2d.py:17-94: noise images padded
+    with pad_and_fftshift(os) and rfftn(norm="forward"), projected at a
+    quarter turn with oversampling os, against the unpadded spectrum at
+    oversampling 1.  The reference asks for real-space NCC > 0.99 (2D) and
+    allclose(atol 0.1) (3D, where every value is far below 0.1); both are
+    checked here, with the stronger rel-L2 < 1e-4 of the two after scaling by
+    os^dim, away from the output's Nyquist row and column: a sample at
+    -n/2 along a volume row or depth axis is clamped to -n/2 + 1, as in the
+    reference (csrc/cpu/common/interpolation_kernels.h:331-340), which is a
+    different frequency in the two boxes."""
+    n = 32
+    g = torch.Generator().manual_seed(5)
+    real = torch.randn((B,) + (n,) * dim, generator=g).to(dev)
+    axes = tuple(range(-dim, 0))
+    fp = torch.fft.rfftn(api.pad_and_fftshift(real, os_), dim=axes, norm="forward")
+    fo = torch.fft.rfftn(api.pad_and_fftshift(real, 1.0), dim=axes, norm="forward")
+    if dim == 3:
+        fp[0, 0, 0, 0] = 0
+        fo[0, 0, 0, 0] = 0
+    rot, sh = quarter_turn(dim, dev), torch.zeros(1, 1, 2, device=dev)
+    f = forw(api, dim)
+    pp = f(fp, rot, shifts=sh, output_shape=(n, n), interpolation=interp, oversampling=os_)
+    po = f(fo, rot, shifts=sh, output_shape=(n, n), interpolation=interp, oversampling=1.0)
+    for b in range(B):
+        score = ncc(torch.fft.irfft2(po[b]), torch.fft.irfft2(pp[b]))
+        assert score > 0.99, (b, score.item())
+    assert torch.allclose(po, pp, rtol=1e-5, atol=1e-1)
+    rows = torch.cat([torch.arange(0, n // 2), torch.arange(n // 2 + 1, n)]).to(dev)
+    inner_o, inner_p = po[:, :, rows, :n // 2], pp[:, :, rows, :n // 2] * os_ ** dim
+    rel = ((inner_p - inner_o).abs().norm() / inner_o.abs().norm()).item()
+    assert rel < 1e-4, rel
+
+
+def oversampling_backprojection(api, dev, dim, interp, os_, B):
+    """Reference: tests/2d/back/test_oversampling_back.py:17-97,
+    tests/3d/back/test_oversampling_back_2d_to_3d.py:17-111: noise
+    projections backprojected (quarter turn in 2D, identity in 3D, one random
+    shift) at oversampling 1 and os, each taken to real space with irfftn and
+    ifftshift_and_crop(os): NCC > 0.99 (2D), > 0.9 (3D)."""
+    n = 32
+    g = torch.Generator().manual_seed(6)
+    proj = crandn((B, 1, n, n // 2 + 1), torch.complex64, 6, dev)
+    rot = quarter_turn(2, dev) if dim == 2 else torch.eye(3, device=dev)[None, None]
+    sh = ((torch.rand(1, 1, 2, generator=g) - 0.5) * (10 if dim == 2 else 5)).to(dev)
+    bp = backproj(api, dim)
+    d1, _ = bp(proj, rot, shifts=sh, interpolation=interp, oversampling=1.0)
+    dn, _ = bp(proj, rot, shifts=sh, interpolation=interp, oversampling=os_)
+    axes = tuple(range(-dim, 0))
+    scores = []
+    for b in range(B):
+        r1 = api.ifftshift_and_crop(torch.fft.irfftn(d1[b], dim=axes), 1.0)
+        rn = api.ifftshift_and_crop(torch.fft.irfftn(dn[b], dim=axes), os_)
+        assert r1.shape == rn.shape
+        scores.append(ncc(r1, rn).item())
+    assert sum(scores) / B > (0.99 if dim == 2 else 0.9), scores
+
+
+def oversampling_weights(api, dev, dim, os_=2.0):
+    """Reference: tests/2d/back/test_oversampling_back.py:100-157,
+    tests/3d/back/test_oversampling_back_2d_to_3d.py:114-176: three identity
+    poses with weights, oversampling 1 against 2; data and weight
+    reconstructions in real space, NCC > 0.99 each."""
+    n = 16
+    shape = (1, 3, n, n // 2 + 1)
+    proj = crandn(shape, torch.complex64, 42, dev)
+    w = rrand(shape, torch.float32, 43, dev)
+    rot = torch.eye(dim, device=dev)[None, None].expand(1, 3, dim, dim)
+    bp = backproj(api, dim)
+    d1, w1 = bp(proj, rot, weights=w, oversampling=1.0)
+    dn, wn = bp(proj, rot, weights=w, oversampling=os_)
+    axes = tuple(range(-dim, 0))
+
+    def real(x, o):
+        x = x if x.is_complex() else torch.complex(x, torch.zeros_like(x))
+        return api.ifftshift_and_crop(torch.fft.irfftn(x, dim=axes), o)
+
+    assert ncc(real(d1[0], 1.0), real(dn[0], os_)) > 0.99
+    assert ncc(real(w1[0], 1.0), real(wn[0], os_)) > 0.99

@@ -1,6 +1,7 @@
 """The public operators on cuda:0 under torch.autograd: the reference's own
-gradient and batching checks (tests/autograd_props.py) through the dispatcher
-ops and the autograd Functions of torch_projectors.ops.
+gradient, batching and oversampling checks (tests/reference_props.py)
+through the dispatcher ops, the autograd Functions of torch_projectors.ops
+and the preparation helpers of torch_projectors.fourier.
 
 complex128 gradchecks run the fp64 kernels; the fp32 checks (shift and
 rotation gradients, weights, convergence, batching) run the tile-owner
@@ -8,7 +9,7 @@ kernels for rotation poses.
 """
 import pytest
 
-from tests import autograd_props as A
+from tests import reference_props as A
 
 pytestmark = pytest.mark.gpu
 
@@ -91,3 +92,33 @@ def test_batching(api, gpu, dim, interp):
     _say("batching", dim, interp)
     A.batching_projection(api, gpu, dim, interp)
     A.batching_backprojection(api, gpu, dim, interp)
+
+
+@pytest.mark.parametrize("B", [1, 3])
+@pytest.mark.parametrize("os_", [2.0, 3.0])
+@pytest.mark.parametrize("interp", INTERP)
+@pytest.mark.parametrize("dim", DIMS)
+def test_oversampling_equivalence(api, gpu, dim, interp, os_, B):
+    from torch_projectors import fourier
+    _say("oversampling", dim, interp, os_, B)
+    both = _With(api, fourier)
+    A.oversampling_projection(both, gpu, dim, interp, os_, B)
+    A.oversampling_backprojection(both, gpu, dim, interp, os_, B)
+
+
+@pytest.mark.parametrize("dim", DIMS)
+def test_oversampling_weights(api, gpu, dim):
+    from torch_projectors import fourier
+    _say("oversampling weights", dim)
+    A.oversampling_weights(_With(api, fourier), gpu, dim)
+
+
+class _With:
+    """The operators of `ops` with the preparation helpers of `prep`."""
+
+    def __init__(self, ops, prep):
+        self._ops, self.pad_and_fftshift, self.ifftshift_and_crop = ops, prep.pad_and_fftshift, \
+            prep.ifftshift_and_crop
+
+    def __getattr__(self, name):
+        return getattr(self._ops, name)

@@ -1,5 +1,6 @@
-"""The reference's gradient and batching checks (tests/autograd_props.py) on
-the CPU oracle under torch.autograd (tests/oracle_autograd.py).
+"""The reference's gradient, batching and oversampling checks
+(tests/reference_props.py) on the CPU oracle under torch.autograd
+(tests/oracle_autograd.py).
 
 They pin the oracle's backward functions against what the mathematics fixes —
 complex128 gradcheck, shift gradients against a phase ramp written in torch
@@ -11,7 +12,7 @@ operators in tests/test_gpu_autograd.py.
 import pytest
 import torch
 
-from tests import autograd_props as A
+from tests import reference_props as A
 from tests import oracle_autograd as OA
 
 CPU = "cpu"
@@ -123,3 +124,13 @@ def test_checks_notice_planted_mistakes(monkeypatch, name, kind, fix, check):
     monkeypatch.setattr(OA, "plant", _on(kind, fix))
     with pytest.raises(FAILS):
         check()
+
+
+@pytest.mark.parametrize("interp", INTERP)
+@pytest.mark.parametrize("dim", DIMS)
+def test_oversampling(dim, interp):
+    for os_ in (2.0, 3.0):
+        for B in (1, 3):
+            A.oversampling_projection(OA, CPU, dim, interp, os_, B)
+            A.oversampling_backprojection(OA, CPU, dim, interp, os_, B)
+    A.oversampling_weights(OA, CPU, dim)
