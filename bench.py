@@ -405,10 +405,45 @@ def make_prep(dev):
                     cpu_sample, cfg, cpu_pmax=1, cpu_kind="port", cpu_cores=1)
 
 
-# headline is the bench line; c2-c5 are the other BASELINE configurations and
-# prep the reference preparation around the headline volume, run on request
+def make_half(dev):
+    """half: the headline forward from the same volume stored as complex32 (the
+    opt-in low-precision storage), beside the complex64 forward, linear and cubic."""
+    import torch
+    import torch_projectors as tp
+    gen = torch.Generator().manual_seed(20261201 + 6)
+    P, n, os_ = 2048, 256, 2.0
+    vol = blob_volume_rfft(256, 512, 32, 80.0, gen, dev)
+    rot = quat_rotations(P, gen)[None].to(dev)
+    sh = ((torch.rand(1, P, 2, generator=gen) * 16) - 8).to(dev)
+    vol16 = vol.to(torch.complex32)
+
+    def fwd(v, interp):
+        return lambda: tp.project_3d_to_2d_forw(v, rot, sh, output_shape=(n, n), interpolation=interp,
+                                                oversampling=os_)
+
+    samples = P * n * (n // 2 + 1)
+    ops = []
+    for interp in ("linear", "cubic"):
+        for tag, v in (("complex32", vol16), ("complex64", vol)):
+            ops.append((f"project_3d_to_2d_forw[{interp},{tag}]", fwd(v, interp),
+                        bytes_forward(P, n, 3, interp), samples, P))
+
+    def cpu_sample(p_cpu, threads, cpu_ops):
+        """The CPU reference on the widened volume (the storage's definition), linear."""
+        vc, rc, sc = vol16.to(torch.complex64).cpu(), rot[:, :p_cpu].cpu(), sh[:, :p_cpu].cpu()
+        return timed_ops([("project_3d_to_2d_forw[linear,complex32]", lambda: cpu_ops.project_3d_to_2d_forw(
+            vc, rc, sc, [n, n], "linear", os_, None))], p_cpu * n * (n // 2 + 1))
+
+    cfg = {"workload": "half: headline forward from a complex32 volume beside complex64, linear and cubic",
+           "volume": [1, 512, 512, 257], "poses": P, "proj": [n, n // 2 + 1], "oversampling": os_}
+    return Workload("half", cfg["workload"], ops, cpu_sample, cfg)
+
+
+# headline is the bench line; c2-c5 are the other BASELINE configurations,
+# prep the reference preparation around the headline volume and half the
+# headline forward from low-precision storage, run on request
 WORKLOADS = {"headline": make_headline, "c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5,
-             "prep": make_prep}
+             "prep": make_prep, "half": make_half}
 
 
 # ----------------------------------------------------------------------------- CPU baseline

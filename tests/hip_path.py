@@ -22,7 +22,13 @@ def _dt(t):
         return capi.TP_F32
     if t.dtype == torch.complex128:
         return capi.TP_F64
-    raise RuntimeError("complex64 or complex128 expected")
+    if t.dtype == torch.complex32:  # forward projections of a complex-half volume
+        return capi.TP_F16S
+    raise RuntimeError("complex64, complex128 or (forward) complex32 expected")
+
+
+def _proj_dtype(rec):
+    return torch.complex64 if rec.dtype == torch.complex32 else rec.dtype
 
 
 def _interp(s):
@@ -69,7 +75,7 @@ def project_2d_forw(reconstruction, rotations, shifts, output_shape, interpolati
     rec, rot, sh = _g(reconstruction), _g(rotations), _g(shifts)
     B, N, H = rec.shape
     n = int(output_shape[0])
-    out = torch.empty(B, rot.shape[1], n, n // 2 + 1, dtype=rec.dtype, device=DEV)
+    out = torch.empty(B, rot.shape[1], n, n // 2 + 1, dtype=_proj_dtype(rec), device=DEV)
     capi.call("tp_project_2d_forw", _dt(rec), _p(rec), B, N, H, _p(rot), rot.shape[0], rot.shape[1], _p(sh),
               sh.shape[0] if sh is not None else 1, n, *_tail(interpolation, oversampling, fourier_radius_cutoff),
               _p(out), _stream())
@@ -81,7 +87,7 @@ def project_3d_to_2d_forw(reconstruction, rotations, shifts, output_shape, inter
     rec, rot, sh = _g(reconstruction), _g(rotations), _g(shifts)
     B, D, N, H = rec.shape
     n = int(output_shape[0])
-    out = torch.empty(B, rot.shape[1], n, n // 2 + 1, dtype=rec.dtype, device=DEV)
+    out = torch.empty(B, rot.shape[1], n, n // 2 + 1, dtype=_proj_dtype(rec), device=DEV)
     capi.call("tp_project_3d_to_2d_forw", _dt(rec), _p(rec), B, D, N, H, _p(rot), rot.shape[0], rot.shape[1],
               _p(sh), sh.shape[0] if sh is not None else 1, n,
               *_tail(interpolation, oversampling, fourier_radius_cutoff), _p(out), _stream())

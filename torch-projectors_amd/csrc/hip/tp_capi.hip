@@ -243,15 +243,23 @@ int need(const void* p, const char* name) {
 
 int launched(hipError_t e, const char* what) { return e == hipSuccess ? TP_OK : hip_fail(e, what); }
 
+// TP_F16S: the volume is stored as complex half; it is widened exactly to
+// fp32 on load and everything else (poses, arithmetic, projections) is the
+// TP_F32 path.
 int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int64_t N, int64_t H, const void* rot,
                  int64_t B_rot, int64_t P, const void* shifts, int64_t B_shift, int64_t n, int interp, double os,
                  int has_cut, double cut, void* out, void* stream) {
+    const bool rec_half = dtype == TP_F16S;
+    const int dt = rec_half ? TP_F32 : dtype;  // arithmetic and output type
+    const int kdt = rec_half ? 2 : dt;         // per-pixel kernels' volume type
     tp::Geom g{};
-    TP_TRY(check_common(dtype, interp, B, P, B_rot, shifts, B_shift, g));
+    if (dtype != TP_F32 && dtype != TP_F64 && !rec_half)
+        return fail("dtype must be TP_F32, TP_F64 or (forward projections) TP_F16S");
+    TP_TRY(check_common(dt, interp, B, P, B_rot, shifts, B_shift, g));
     if (dim == 3 && D != N) return fail("reconstruction depth must equal its height");
     TP_TRY(set_rec(dim, N, H, g));
     TP_TRY(set_proj(n, g));
-    set_cut(dtype, has_cut, cut, g);
+    set_cut(dt, has_cut, cut, g);
     g.os = os;
     if (g.work == 0) return TP_OK;
     TP_TRY(need(rec, "reconstruction"));
@@ -259,23 +267,24 @@ int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int6
     TP_TRY(need(out, "projections"));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool cubic = interp == TP_CUBIC;
-    if (use_tiles(dim, dtype, os, n)) {
-        TP_TRY(launched(tp::launch_project3_forw_tiled(cubic, g, tile_spec(g, cubic), rec, rot, shifts, out, s),
+    if (use_tiles(dim, dt, os, n)) {
+        TP_TRY(launched(tp::launch_project3_forw_tiled(cubic, g, tile_spec(g, cubic), rec, rot, shifts, out, s,
+                                                       rec_half),
                         "tiled projection launch"));
-        return launched(tp::launch_project_forw(dim, dtype, cubic, g, rec, rot, shifts, out, s, true),
+        return launched(tp::launch_project_forw(dim, kdt, cubic, g, rec, rot, shifts, out, s, true),
                         "projection launch");
     }
-    if (use_tiles2(dim, dtype, os, n)) {
+    if (use_tiles2(dim, dt, os, n)) {
         // zero-fill first: the tiled gather writes the active pixels of rotation poses, the
         // rest kernel the other poses
-        TP_TRY(zero(out, cx_words(dtype, g.B * g.P * int64_t(g.npix)), s));
+        TP_TRY(zero(out, cx_words(dt, g.B * g.P * int64_t(g.npix)), s));
         TP_TRY(launched(tp::launch_gather2_tiled(cubic, 0, g, tile_spec2(g, cubic), rec, nullptr, rot, shifts, out,
-                                                 nullptr, nullptr, nullptr, nullptr, s),
+                                                 nullptr, nullptr, nullptr, nullptr, s, rec_half),
                         "tiled projection launch"));
-        return launched(tp::launch_project_forw(dim, dtype, cubic, g, rec, rot, shifts, out, s, true),
+        return launched(tp::launch_project_forw(dim, kdt, cubic, g, rec, rot, shifts, out, s, true),
                         "projection launch");
     }
-    return launched(tp::launch_project_forw(dim, dtype, cubic, g, rec, rot, shifts, out, s), "projection launch");
+    return launched(tp::launch_project_forw(dim, kdt, cubic, g, rec, rot, shifts, out, s), "projection launch");
 }
 
 int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, int64_t n, int64_t hp, const void* rec,

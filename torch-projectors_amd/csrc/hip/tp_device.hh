@@ -10,8 +10,11 @@
 // rfft column (the Hermitian half axis), x[1] the row, x[2] the slice.
 #pragma once
 
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "tp_launch.hh"
 
@@ -30,6 +33,22 @@ template <typename T> __device__ __forceinline__ Cx<T> cmul(Cx<T> a, Cx<T> b) {
     return {a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re};
 }
 template <typename T> __device__ __forceinline__ Cx<T> cconj(Cx<T> a) { return {a.re, -a.im}; }
+
+// Volume storage: a reconstruction element is a Cx<S>; it is computed on as a
+// Cx<wide_t<S>>.  Complex-half volumes (the opt-in low-precision storage of
+// the forward projections) widen each stored value exactly to fp32 on load,
+// so every later step is the fp32 path applied to the widened volume.
+template <typename S> struct Wide { using type = S; };
+template <> struct Wide<__half> { using type = float; };
+template <typename S> using wide_t = typename Wide<S>::type;
+// Element i of a complex-half volume, widened.  (fp32 / fp64 volumes are read
+// with a plain indexed load at each call site: routing them through a helper
+// like this one splits the compiler's 8-byte loads and serialises them.)
+__device__ __forceinline__ Cx<float> load_widened(const Cx<__half>* p, int64_t i) {
+    const Cx<__half> h = p[i];
+    return {__half2float(h.re), __half2float(h.im)};
+}
+template <typename S> constexpr bool kHalfVolume = std::is_same<S, __half>::value;
 
 // floor(x) as an int plus the fraction x - floor(x).  The reference keeps
 // floor(x) in int64 (interpolation_kernels.h, projection_utils.h); beyond
@@ -73,19 +92,21 @@ template <typename T> __device__ __forceinline__ T cubic_dw(T s) {
 // Friedel-aware FFTW-layout fetch with edge replication (fftw_sampling.h:42-76,
 // 96-137): c < 0 mirrors all coordinates and conjugates; c is clamped to N/2,
 // r and d to [-N/2+1, N/2], negatives wrap by +N.
-template <typename T>
-__device__ __forceinline__ Cx<T> fetch2(const Cx<T>* __restrict__ rec, int N, int H, int r, int c) {
+template <typename S>
+__device__ __forceinline__ Cx<wide_t<S>> fetch2(const Cx<S>* __restrict__ rec, int N, int H, int r, int c) {
     const bool cj = c < 0;
     if (cj) { c = -c; r = -r; }
     c = min(c, H - 1);
     r = min(N / 2, max(r, -N / 2 + 1));
     if (r < 0) r += N;
-    Cx<T> v = rec[r * H + c];
+    Cx<wide_t<S>> v;
+    if constexpr (kHalfVolume<S>) v = load_widened(rec, r * H + c);
+    else v = rec[r * H + c];
     if (cj) v.im = -v.im;
     return v;
 }
-template <typename T>
-__device__ __forceinline__ Cx<T> fetch3(const Cx<T>* __restrict__ rec, int N, int H, int d, int r, int c) {
+template <typename S>
+__device__ __forceinline__ Cx<wide_t<S>> fetch3(const Cx<S>* __restrict__ rec, int N, int H, int d, int r, int c) {
     const bool cj = c < 0;
     if (cj) { c = -c; r = -r; d = -d; }
     c = min(c, H - 1);
@@ -93,19 +114,22 @@ __device__ __forceinline__ Cx<T> fetch3(const Cx<T>* __restrict__ rec, int N, in
     d = min(N / 2, max(d, -N / 2 + 1));
     if (r < 0) r += N;
     if (d < 0) d += N;
-    Cx<T> v = rec[((int64_t)d * N + r) * H + c];
+    Cx<wide_t<S>> v;
+    if constexpr (kHalfVolume<S>) v = load_widened(rec, ((int64_t)d * N + r) * H + c);
+    else v = rec[((int64_t)d * N + r) * H + c];
     if (cj) v.im = -v.im;
     return v;
 }
 // Cubic stencils pre-clamp before the Friedel fetch (interpolation_kernels.h:245-255, 331-342).
-template <typename T>
-__device__ __forceinline__ Cx<T> fetch2_cubic(const Cx<T>* __restrict__ rec, int N, int H, int r, int c) {
+template <typename S>
+__device__ __forceinline__ Cx<wide_t<S>> fetch2_cubic(const Cx<S>* __restrict__ rec, int N, int H, int r, int c) {
     if (abs(c) >= H) c = (c < 0) ? -(H - 1) : (H - 1);
     r = max(-N / 2 + 1, min(r, N / 2));
     return fetch2(rec, N, H, r, c);
 }
-template <typename T>
-__device__ __forceinline__ Cx<T> fetch3_cubic(const Cx<T>* __restrict__ rec, int N, int H, int d, int r, int c) {
+template <typename S>
+__device__ __forceinline__ Cx<wide_t<S>> fetch3_cubic(const Cx<S>* __restrict__ rec, int N, int H, int d, int r,
+                                                      int c) {
     if (abs(c) >= H) c = (c < 0) ? -(H - 1) : (H - 1);
     r = max(-N / 2 + 1, min(r, N / 2));
     d = max(-N / 2 + 1, min(d, N / 2));
@@ -139,8 +163,8 @@ __device__ __forceinline__ Interp<T> lerp2(F&& fetch, T r, T c) {
     }
     return o;
 }
-template <typename T, bool GRADS>
-__device__ __forceinline__ Interp<T> interp2_linear(const Cx<T>* __restrict__ rec, int N, int H, T r, T c) {
+template <typename T, bool GRADS, typename S>
+__device__ __forceinline__ Interp<T> interp2_linear(const Cx<S>* __restrict__ rec, int N, int H, T r, T c) {
     return lerp2<T, GRADS>([&](int rr, int cc) { return fetch2(rec, N, H, rr, cc); }, r, c);
 }
 
@@ -175,8 +199,8 @@ __device__ __forceinline__ Interp<T> cubic2(F&& fetch, T r, T c) {
     }
     return o;
 }
-template <typename T, bool GRADS>
-__device__ __forceinline__ Interp<T> interp2_cubic(const Cx<T>* __restrict__ rec, int N, int H, T r, T c) {
+template <typename T, bool GRADS, typename S>
+__device__ __forceinline__ Interp<T> interp2_cubic(const Cx<S>* __restrict__ rec, int N, int H, T r, T c) {
     return cubic2<T, GRADS>([&](int rr, int cc) { return fetch2_cubic(rec, N, H, rr, cc); }, r, c);
 }
 
@@ -209,8 +233,8 @@ __device__ __forceinline__ Interp<T> lerp3(F&& fetch, T d, T r, T c) {
     }
     return o;
 }
-template <typename T, bool GRADS>
-__device__ __forceinline__ Interp<T> interp3_linear(const Cx<T>* __restrict__ rec, int N, int H, T d, T r, T c) {
+template <typename T, bool GRADS, typename S>
+__device__ __forceinline__ Interp<T> interp3_linear(const Cx<S>* __restrict__ rec, int N, int H, T d, T r, T c) {
     return lerp3<T, GRADS>([&](int dd, int rr, int cc) { return fetch3(rec, N, H, dd, rr, cc); }, d, r, c);
 }
 
@@ -253,13 +277,13 @@ __device__ __forceinline__ Interp<T> cubic3(F&& fetch, T d, T r, T c) {
     }
     return o;
 }
-template <typename T, bool GRADS>
-__device__ __forceinline__ Interp<T> interp3_cubic(const Cx<T>* __restrict__ rec, int N, int H, T d, T r, T c) {
+template <typename T, bool GRADS, typename S>
+__device__ __forceinline__ Interp<T> interp3_cubic(const Cx<S>* __restrict__ rec, int N, int H, T d, T r, T c) {
     return cubic3<T, GRADS>([&](int dd, int rr, int cc) { return fetch3_cubic(rec, N, H, dd, rr, cc); }, d, r, c);
 }
 
-template <int DIM, typename T, bool CUBIC, bool GRADS>
-__device__ __forceinline__ Interp<T> interpolate(const Cx<T>* __restrict__ rec, int N, int H, const T* x) {
+template <int DIM, typename T, bool CUBIC, bool GRADS, typename S>
+__device__ __forceinline__ Interp<T> interpolate(const Cx<S>* __restrict__ rec, int N, int H, const T* x) {
     if constexpr (DIM == 2) {
         if constexpr (CUBIC) return interp2_cubic<T, GRADS>(rec, N, H, x[1], x[0]);
         else return interp2_linear<T, GRADS>(rec, N, H, x[1], x[0]);

@@ -77,7 +77,8 @@ hipError_t launch_zero(void* p, int64_t words, hipStream_t s);
 // (out complex, wout real; either may be null).
 hipError_t launch_zero_outside(int dt, const Geom& g, void* out, void* wout, hipStream_t s);
 
-// Kernel launchers; `dim` is 2 or 3, `dt` 0 (fp32) or 1 (fp64).
+// Kernel launchers; `dim` is 2 or 3, `dt` 0 (fp32) or 1 (fp64); launch_project_forw
+// also takes `dt` 2: a complex-half volume with fp32 arithmetic and output.
 // `rest_only` (fp32): only masked pixels and poses that are not rotations.
 hipError_t launch_project_forw(int dim, int dt, bool cubic, const Geom& g, const void* rec, const void* rot,
                                const void* shifts, void* out, hipStream_t s, bool rest_only = false);
@@ -92,9 +93,11 @@ hipError_t launch_backproject_forw(int dim, int dt, bool cubic, const Geom& g, c
                                    const void* rot, const void* shifts, void* data, void* wrec, hipStream_t s,
                                    bool rest_only = false);
 // fp32 3D tile-owner paths (rotation poses only; the per-pixel kernels with
-// `rest_only` complete the other poses and the masked pixels).
+// `rest_only` complete the other poses and the masked pixels).  `rec_half`:
+// the volume is stored as complex half and widened to fp32 on load.
 hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* rec,
-                                      const void* rot, const void* shifts, void* out, hipStream_t s);
+                                      const void* rot, const void* shifts, void* out, hipStream_t s,
+                                      bool rec_half = false);
 // Rotation/shift gradients of project_3d_to_2d_back for rotation poses, added
 // into zero-filled grot / gshift (either may be null).
 hipError_t launch_grads3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gproj, const void* rec,
@@ -123,9 +126,10 @@ hipError_t launch_scatter2_tiled(bool cubic, int mode, const Geom& g, const Tile
 // grad_projections) into zero-filled grot / gshift; mode 2:
 // backproject_2d_back (rec = grad_data_rec -> out, gw -> wout, and with gsrc =
 // projections the gradients).
+// `rec_half` (mode 0): the volume is stored as complex half and widened to fp32 on load.
 hipError_t launch_gather2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* rec,
                                 const void* gw, const void* rot, const void* shifts, void* out, void* wout,
-                                const void* gsrc, void* grot, void* gshift, hipStream_t s);
+                                const void* gsrc, void* grot, void* gshift, hipStream_t s, bool rec_half = false);
 
 // Reference preparation (tp_fourier.hip).  Elements are opaque words of
 // elem_bytes (2, 4, 8 or 16); `dim` spatial axes (2 or 3) after the batch.

@@ -21,9 +21,10 @@ namespace {
 
 constexpr double kTwoPi = 6.283185307179586476925286766559;
 
-// Value of one active pixel (frequency r, c) of one pose.
-template <int DIM, typename T, bool CUBIC>
-__device__ __forceinline__ Cx<T> project_pixel(const Geom& g, const Cx<T>* __restrict__ recb, const T* __restrict__ R,
+// Value of one active pixel (frequency r, c) of one pose; the volume is
+// stored as Cx<VS> (VS = T, or half for a T = float computation).
+template <int DIM, typename T, bool CUBIC, typename VS>
+__device__ __forceinline__ Cx<T> project_pixel(const Geom& g, const Cx<VS>* __restrict__ recb, const T* __restrict__ R,
                                                const T* __restrict__ S, T r, T c) {
     T x[3], sc, sr;
     rotate<DIM>(R, r, c, g.os, x, sc, sr);
@@ -32,8 +33,8 @@ __device__ __forceinline__ Cx<T> project_pixel(const Geom& g, const Cx<T>* __res
     return v;
 }
 
-template <int DIM, typename T, bool CUBIC>
-__global__ __launch_bounds__(kBlock) void k_project_forw(Geom g, const Cx<T>* __restrict__ rec,
+template <int DIM, typename T, bool CUBIC, typename VS = T>
+__global__ __launch_bounds__(kBlock) void k_project_forw(Geom g, const Cx<VS>* __restrict__ rec,
                                                          const T* __restrict__ rot, const T* __restrict__ shifts,
                                                          Cx<T>* __restrict__ out) {
     constexpr int RS = DIM * DIM;
@@ -59,8 +60,8 @@ __global__ __launch_bounds__(kBlock) void k_project_forw(Geom g, const Cx<T>* __
 // active pixels of rotation poses: zeros on masked pixels, and every pixel of
 // the other poses.  One block per pose.  ZEROED: the output was zero-filled
 // first, so rotation poses are done.
-template <int DIM, bool CUBIC, bool ZEROED>
-__global__ __launch_bounds__(kBlock) void k_project_forw_rest(Geom g, const Cx<float>* __restrict__ rec,
+template <int DIM, bool CUBIC, bool ZEROED, typename VS = float>
+__global__ __launch_bounds__(kBlock) void k_project_forw_rest(Geom g, const Cx<VS>* __restrict__ rec,
                                                               const float* __restrict__ rot,
                                                               const float* __restrict__ shifts,
                                                               Cx<float>* __restrict__ out) {
@@ -178,20 +179,20 @@ __global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __
     }
 }
 
-template <int DIM, typename T, bool CUBIC>
+template <int DIM, typename T, bool CUBIC, typename VS = T>
 hipError_t forw(const Geom& g, const void* rec, const void* rot, const void* shifts, void* out, hipStream_t s) {
-    hipLaunchKernelGGL((k_project_forw<DIM, T, CUBIC>), dim3(grid_for(g.work)), dim3(kBlock), 0, s, g,
-                       (const Cx<T>*)rec, (const T*)rot, (const T*)shifts, (Cx<T>*)out);
+    hipLaunchKernelGGL((k_project_forw<DIM, T, CUBIC, VS>), dim3(grid_for(g.work)), dim3(kBlock), 0, s, g,
+                       (const Cx<VS>*)rec, (const T*)rot, (const T*)shifts, (Cx<T>*)out);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_zero_outside(sizeof(T) == 4 ? 0 : 1, g, out, nullptr, s);
 }
 
-template <int DIM, bool CUBIC>
+template <int DIM, bool CUBIC, typename VS = float>
 hipError_t forw_rest(const Geom& g, const void* rec, const void* rot, const void* shifts, void* out, hipStream_t s) {
     // 2D: the C ABI zero-fills the output first (a streaming fill beats per-row masked zeros)
-    hipLaunchKernelGGL((k_project_forw_rest<DIM, CUBIC, DIM == 2>), dim3(grid_for(g.B * g.P)), dim3(kBlock), 0, s,
-                       g, (const Cx<float>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
+    hipLaunchKernelGGL((k_project_forw_rest<DIM, CUBIC, DIM == 2, VS>), dim3(grid_for(g.B * g.P)), dim3(kBlock), 0,
+                       s, g, (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
     return hipGetLastError();
 }
 
@@ -230,6 +231,20 @@ hipError_t back(const Geom& g, const void* gproj, const void* rec, const void* r
 
 hipError_t launch_project_forw(int dim, int dt, bool cubic, const Geom& g, const void* rec, const void* rot,
                                const void* shifts, void* out, hipStream_t s, bool rest_only) {
+    if (dt == 2) {  // complex-half volume, fp32 arithmetic and output
+        if (rest_only) {
+            if (dim == 2)
+                return cubic ? forw_rest<2, true, __half>(g, rec, rot, shifts, out, s)
+                             : forw_rest<2, false, __half>(g, rec, rot, shifts, out, s);
+            return cubic ? forw_rest<3, true, __half>(g, rec, rot, shifts, out, s)
+                         : forw_rest<3, false, __half>(g, rec, rot, shifts, out, s);
+        }
+        if (dim == 2)
+            return cubic ? forw<2, float, true, __half>(g, rec, rot, shifts, out, s)
+                         : forw<2, float, false, __half>(g, rec, rot, shifts, out, s);
+        return cubic ? forw<3, float, true, __half>(g, rec, rot, shifts, out, s)
+                     : forw<3, float, false, __half>(g, rec, rot, shifts, out, s);
+    }
     if (rest_only && dt == 0) {
         if (dim == 2)
             return cubic ? forw_rest<2, true>(g, rec, rot, shifts, out, s)

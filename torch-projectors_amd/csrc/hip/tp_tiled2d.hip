@@ -22,6 +22,8 @@
 //
 // Only poses whose matrix is orthonormal (pose_is_rotation2) take this path;
 // the per-pixel kernels scatter the others.
+#include <type_traits>
+
 #include "tp_device.hh"
 #include "tp_launch.hh"
 #include "tp_tiled_common.hh"
@@ -503,8 +505,8 @@ __device__ __forceinline__ Interp<float> cubic2_grads(F&& fetch, float r, float 
     return o;
 }
 
-template <bool CUBIC, int KP, int GMODE, bool RS, bool WG>
-__global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts, const Cx<float>* __restrict__ rec,
+template <bool CUBIC, int KP, int GMODE, bool RS, bool WG, typename VS = float>
+__global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts, const Cx<VS>* __restrict__ rec,
                                                             const float* __restrict__ gw,
                                                             const float* __restrict__ rot,
                                                             const float* __restrict__ shifts,
@@ -512,6 +514,7 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
                                                             const Cx<float>* __restrict__ gsrc,
                                                             float* __restrict__ grot, float* __restrict__ gshift) {
     static_assert(GMODE == 0 || KP == 1, "the gradient modes sum one pose per wave batch");
+    static_assert(GMODE == 0 || std::is_same<VS, float>::value, "complex-half volumes are read by the forward only");
     constexpr int LO = CUBIC ? 1 : 0, HI = CUBIC ? 2 : 1, WC = GC + LO + HI, WR = GR + LO + HI, W2 = WC * WR;
     constexpr int WW = (GMODE == 2 && WG) ? (GC + 1) * (GR + 1) : 1;  // bilinear weight taps
     constexpr int RPS = 64 / KP, NW = kThreads / 64, CH = 2048;
@@ -570,7 +573,7 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
             const int np = pcnt[0];
             if (np == 0) continue;
             if (!loaded) {
-                const Cx<float>* recb = rec + b * g.vol;
+                const Cx<VS>* recb = rec + b * g.vol;
                 for (int e = tid; e < W2; e += kThreads) {
                     const int r = tr - LO + e / WC, c = tc - LO + e % WC;
                     vt[e] = CUBIC ? fetch2_cubic(recb, N, H, r, c) : fetch2(recb, N, H, r, c);
@@ -711,33 +714,37 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
     }
 }
 
-template <bool CUBIC, int KP, int GMODE, bool RS, bool WG>
+template <bool CUBIC, int KP, int GMODE, bool RS, bool WG, typename VS = float>
 hipError_t gather2_launch(const Geom& g, const TileSpec2& ts, const void* rec, const void* gw, const void* rot,
                           const void* shifts, void* out, void* wout, const void* gsrc, void* grot, void* gshift,
                           hipStream_t s) {
     const int64_t work = g.B * ts.gksplit * int64_t(ts.gnt) * ts.gnt;
     if (work == 0) return hipSuccess;
-    hipLaunchKernelGGL((k_gather2_tiled<CUBIC, KP, GMODE, RS, WG>), dim3(grid_for(kXcds * xcd_per<kRun>(work))),
-                       dim3(kThreads), 0, s, g, ts, (const Cx<float>*)rec, (const float*)gw, (const float*)rot,
+    hipLaunchKernelGGL((k_gather2_tiled<CUBIC, KP, GMODE, RS, WG, VS>), dim3(grid_for(kXcds * xcd_per<kRun>(work))),
+                       dim3(kThreads), 0, s, g, ts, (const Cx<VS>*)rec, (const float*)gw, (const float*)rot,
                        (const float*)shifts, (Cx<float>*)out, (float*)wout, (const Cx<float>*)gsrc, (float*)grot,
                        (float*)gshift);
     return hipGetLastError();
+}
+
+template <bool CUBIC, typename VS>
+hipError_t gather2_forw(const Geom& g, const TileSpec2& ts, const void* rec, const void* rot, const void* shifts,
+                        void* out, hipStream_t s) {
+    if (ts.kp_gather >= 4)
+        return gather2_launch<CUBIC, 4, 0, false, false, VS>(g, ts, rec, nullptr, rot, shifts, out, nullptr, nullptr,
+                                                             nullptr, nullptr, s);
+    if (ts.kp_gather == 2)
+        return gather2_launch<CUBIC, 2, 0, false, false, VS>(g, ts, rec, nullptr, rot, shifts, out, nullptr, nullptr,
+                                                             nullptr, nullptr, s);
+    return gather2_launch<CUBIC, 1, 0, false, false, VS>(g, ts, rec, nullptr, rot, shifts, out, nullptr, nullptr,
+                                                         nullptr, nullptr, s);
 }
 
 template <bool CUBIC>
 hipError_t gather2_modes(int mode, const Geom& g, const TileSpec2& ts, const void* rec, const void* gw,
                          const void* rot, const void* shifts, void* out, void* wout, const void* gsrc, void* grot,
                          void* gshift, hipStream_t s) {
-    if (mode == 0) {
-        if (ts.kp_gather >= 4)
-            return gather2_launch<CUBIC, 4, 0, false, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
-                                                             gshift, s);
-        if (ts.kp_gather == 2)
-            return gather2_launch<CUBIC, 2, 0, false, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
-                                                             gshift, s);
-        return gather2_launch<CUBIC, 1, 0, false, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift,
-                                                         s);
-    }
+    if (mode == 0) return gather2_forw<CUBIC, float>(g, ts, rec, rot, shifts, out, s);
     if (mode == 1)
         return gather2_launch<CUBIC, 1, 1, true, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift,
                                                         s);
@@ -757,7 +764,12 @@ hipError_t gather2_modes(int mode, const Geom& g, const TileSpec2& ts, const voi
 
 hipError_t launch_gather2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* rec,
                                 const void* gw, const void* rot, const void* shifts, void* out, void* wout,
-                                const void* gsrc, void* grot, void* gshift, hipStream_t s) {
+                                const void* gsrc, void* grot, void* gshift, hipStream_t s, bool rec_half) {
+    if (rec_half) {
+        if (mode != 0) return hipErrorInvalidValue;
+        return cubic ? gather2_forw<true, __half>(g, ts, rec, rot, shifts, out, s)
+                     : gather2_forw<false, __half>(g, ts, rec, rot, shifts, out, s);
+    }
     if (mode == 1 && !grot && !gshift) return hipSuccess;
     return cubic ? gather2_modes<true>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, s)
                  : gather2_modes<false>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, s);

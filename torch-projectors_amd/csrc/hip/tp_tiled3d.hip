@@ -34,6 +34,8 @@
 // Only poses whose first two rotation columns are orthonormal take this path
 // (pose_is_rotation); the per-pixel kernels handle the others and write the
 // masked pixels of the forward.
+#include <type_traits>
+
 #include "tp_device.hh"
 #include "tp_launch.hh"
 #include "tp_tiled_common.hh"
@@ -353,8 +355,8 @@ __device__ __forceinline__ Interp<float> cubic3_grads(F&& fetch, float d, float 
     return o;
 }
 
-template <bool CUBIC, int KP, bool OSX, int GMODE = 0, bool RS = true, bool WG = false>
-__global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ rec,
+template <bool CUBIC, int KP, bool OSX, int GMODE = 0, bool RS = true, bool WG = false, typename VS = float>
+__global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec ts, const Cx<VS>* __restrict__ rec,
                                                         const float* __restrict__ rot,
                                                         const float* __restrict__ shifts,
                                                         Cx<float>* __restrict__ out,
@@ -364,6 +366,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                                                         const float* __restrict__ gw = nullptr,
                                                         float* __restrict__ wout = nullptr) {
     static_assert(GMODE == 0 || KP == 1, "the gradient modes sum one pose per wave batch");
+    static_assert(GMODE == 0 || std::is_same<VS, float>::value, "complex-half volumes are read by the forward only");
     constexpr bool GRADS = GMODE == 1 || (GMODE == 2 && RS);
     constexpr int WW = (GMODE == 2 && WG) ? (L + 1) * (L + 1) * (LD + 1) : 1;  // trilinear weight taps
     __shared__ float wt[WW];
@@ -408,7 +411,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
         if (dist2 > rho2) continue;
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
         const float* rotb = rot + rb * g.P * 9;
-        const Cx<float>* recb = rec + b * g.vol;
+        const Cx<VS>* recb = rec + b * g.vol;
         auto lds = [&](int d, int r, int c) {
             return vt[((d - (td - LO)) * W + (r - (tr - LO))) * W + (c - (tc - LO))];
         };
@@ -439,7 +442,9 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                         const int d = td - LO + ld, r = tr - LO + lr, c = tc - LO + lc;
                         if (plain) {
                             const int dd = sg * d, rr = sg * r;
-                            v[q] = recb[(int64_t(dd < 0 ? dd + N : dd) * N + (rr < 0 ? rr + N : rr)) * H + sg * c];
+                            const int64_t idx = (int64_t(dd < 0 ? dd + N : dd) * N + (rr < 0 ? rr + N : rr)) * H + sg * c;
+                            if constexpr (kHalfVolume<VS>) v[q] = load_widened(recb, idx);
+                            else v[q] = recb[idx];
                             if (plain_neg) v[q].im = -v[q].im;
                         } else {
                             v[q] = CUBIC ? fetch3_cubic(recb, N, H, d, r, c) : fetch3(recb, N, H, d, r, c);
@@ -953,13 +958,14 @@ __global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<fl
     }
 }
 
-template <bool CUBIC, int KP, bool OSX>
+template <bool CUBIC, int KP, bool OSX, typename VS>
 hipError_t forw_launch(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts,
                        void* out, hipStream_t s) {
     const int64_t fcore = int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fd1 - ts.fd0) * ts.ksplit;
     const int64_t work = g.B * (fcore + int64_t(ts.nt) * ts.nt * ts.ntfd);
-    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP, OSX>), dim3(grid_for(kXcds * xcd_per<kRunForw>(work))), dim3(kForwThreads), 0, s, g, ts,
-                       (const Cx<float>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
+    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP, OSX, 0, true, false, VS>),
+                       dim3(grid_for(kXcds * xcd_per<kRunForw>(work))), dim3(kForwThreads), 0, s, g, ts,
+                       (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
     return hipGetLastError();
 }
 
@@ -1049,23 +1055,30 @@ hipError_t bpback_flags(const Geom& g, const TileSpec& ts, const void* gdata, co
                                                         gshift, s);
 }
 
-template <bool CUBIC, bool OSX>
+template <bool CUBIC, bool OSX, typename VS>
 hipError_t forw_kp(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts, void* out,
                    hipStream_t s) {
-    if (ts.kp_forw >= 4) return forw_launch<CUBIC, 4, OSX>(g, ts, rec, rot, shifts, out, s);
-    if (ts.kp_forw == 2) return forw_launch<CUBIC, 2, OSX>(g, ts, rec, rot, shifts, out, s);
-    return forw_launch<CUBIC, 1, OSX>(g, ts, rec, rot, shifts, out, s);
+    if (ts.kp_forw >= 4) return forw_launch<CUBIC, 4, OSX, VS>(g, ts, rec, rot, shifts, out, s);
+    if (ts.kp_forw == 2) return forw_launch<CUBIC, 2, OSX, VS>(g, ts, rec, rot, shifts, out, s);
+    return forw_launch<CUBIC, 1, OSX, VS>(g, ts, rec, rot, shifts, out, s);
+}
+
+template <typename VS>
+hipError_t forw_store(bool cubic, const Geom& g, const TileSpec& ts, const void* rec, const void* rot,
+                      const void* shifts, void* out, hipStream_t s) {
+    if (cubic)
+        return ts.os_exact ? forw_kp<true, true, VS>(g, ts, rec, rot, shifts, out, s)
+                           : forw_kp<true, false, VS>(g, ts, rec, rot, shifts, out, s);
+    return ts.os_exact ? forw_kp<false, true, VS>(g, ts, rec, rot, shifts, out, s)
+                       : forw_kp<false, false, VS>(g, ts, rec, rot, shifts, out, s);
 }
 
 }  // namespace
 
 hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* rec,
-                                      const void* rot, const void* shifts, void* out, hipStream_t s) {
-    if (cubic)
-        return ts.os_exact ? forw_kp<true, true>(g, ts, rec, rot, shifts, out, s)
-                           : forw_kp<true, false>(g, ts, rec, rot, shifts, out, s);
-    return ts.os_exact ? forw_kp<false, true>(g, ts, rec, rot, shifts, out, s)
-                       : forw_kp<false, false>(g, ts, rec, rot, shifts, out, s);
+                                      const void* rot, const void* shifts, void* out, hipStream_t s, bool rec_half) {
+    if (rec_half) return forw_store<__half>(cubic, g, ts, rec, rot, shifts, out, s);
+    return forw_store<float>(cubic, g, ts, rec, rot, shifts, out, s);
 }
 
 hipError_t launch_grads3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gproj, const void* rec,

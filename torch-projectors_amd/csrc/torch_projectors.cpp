@@ -71,6 +71,13 @@ int dtype_code(const Tensor& complex_tensor) {
     return st == at::kComplexFloat ? TP_F32 : TP_F64;
 }
 
+// Opt-in low-precision volume storage (no counterpart in the reference): a
+// complex32 reconstruction is projected natively (TP_F16S, widened to fp32 on
+// load, complex64 projections); the backward ops work on its exact complex64
+// widening and return the reconstruction gradient as complex32, the dtype
+// autograd expects for that input.
+bool is_half_volume(const Tensor& reconstruction) { return reconstruction.scalar_type() == at::kComplexHalf; }
+
 int interp_code(const std::string& s) { return s == "cubic" ? TP_CUBIC : TP_LINEAR; }
 
 void* current_stream(const c10::Device& dev) {
@@ -118,11 +125,13 @@ Tensor project_forw(int dim, const Tensor& reconstruction, const Tensor& rotatio
     const int64_t n = output_shape[0];
     const auto dev = reconstruction.device();
     c10::hip::HIPGuardMasqueradingAsCUDA guard(dev);
-    const int dt = dtype_code(reconstruction);
-    const auto real = c10::toRealValueType(reconstruction.scalar_type());
+    const bool half = is_half_volume(reconstruction);
+    const int dt = half ? TP_F16S : dtype_code(reconstruction);
+    const auto cplx = half ? at::kComplexFloat : reconstruction.scalar_type();
+    const auto real = c10::toRealValueType(cplx);
     const Tensor rec = reconstruction.contiguous();
     const Prep rot = prep(rotations, real, dev), sh = prep_opt(shifts, real, dev);
-    Tensor out = at::empty({B, P, n, n / 2 + 1}, reconstruction.options());
+    Tensor out = at::empty({B, P, n, n / 2 + 1}, reconstruction.options().dtype(cplx));
     const int has_cut = fourier_radius_cutoff.has_value();
     const double cut = fourier_radius_cutoff.value_or(0.0);
     int rc;
@@ -153,14 +162,17 @@ std::tuple<Tensor, Tensor, Tensor> project_back(int dim, const Tensor& grad_proj
     const int64_t B_rot = rotations.size(0);
     TORCH_CHECK(B_rot == B || B_rot == 1, "Batch size of rotations must be 1 or same as reconstruction");
     check_shift_batch(shifts, B, P, "reconstruction");
-    TORCH_CHECK(grad_projections.scalar_type() == reconstruction.scalar_type(),
-                "grad_projections and reconstruction must have the same dtype");
+    const bool half = is_half_volume(reconstruction);
+    TORCH_CHECK(grad_projections.scalar_type() == (half ? at::kComplexFloat : reconstruction.scalar_type()),
+                half ? "grad_projections must be complex64 for a complex32 reconstruction"
+                     : "grad_projections and reconstruction must have the same dtype");
     const auto dev = reconstruction.device();
     c10::hip::HIPGuardMasqueradingAsCUDA guard(dev);
-    const int dt = dtype_code(reconstruction);
-    const auto real = c10::toRealValueType(reconstruction.scalar_type());
     TORCH_CHECK(grad_projections.device() == dev, "all tensors must be on the same GPU");
-    const Tensor g = grad_projections.contiguous(), rec = reconstruction.contiguous();
+    const Tensor g = grad_projections.contiguous();
+    const Tensor rec = half ? reconstruction.to(at::kComplexFloat).contiguous() : reconstruction.contiguous();
+    const int dt = dtype_code(rec);
+    const auto real = c10::toRealValueType(rec.scalar_type());
     const Prep rot = prep(rotations, real, dev), sh = prep_opt(shifts, real, dev);
     PoseGrads pg = pose_grads(rotations, shifts, rot, sh);
     Tensor grec = at::empty(rec.sizes(), grad_projections.options());
@@ -179,7 +191,8 @@ std::tuple<Tensor, Tensor, Tensor> project_back(int dim, const Tensor& grad_proj
                                       rec.size(3), rot.ptr(), B_rot, sh.ptr(), Bs, interp_code(interpolation),
                                       oversampling, has_cut, cut, grec.data_ptr(), grot, gsh, current_stream(dev));
     check_rc(rc);
-    return {grec, finish_rot(pg, rotations), finish_shift(pg, rotations, shifts, grad_projections)};
+    return {half ? grec.to(at::kComplexHalf) : grec, finish_rot(pg, rotations),
+            finish_shift(pg, rotations, shifts, grad_projections)};
 }
 
 // ------------------------------------------------------------------ backprojection

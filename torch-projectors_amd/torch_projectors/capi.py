@@ -13,7 +13,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY_PATH = os.path.join(_HERE, "libtorch_projectors_hip.so")
 
 TP_OK, TP_ERR_INVALID, TP_ERR_HIP = 0, 1, 2
-TP_F32, TP_F64 = 0, 1
+TP_F32, TP_F64, TP_F16S = 0, 1, 2
 TP_LINEAR, TP_CUBIC = 0, 1
 
 _P, _I, _L, _D = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_double
