@@ -37,6 +37,7 @@ constexpr int kThreads = 256;
 constexpr int kRun = 128;         // XCD run length (items)
 constexpr int kChunk2 = 512;      // poses culled per phase
 constexpr int kInFlight = 2;      // rotations loaded together per lane in the cull
+constexpr double kPrivOs = 1.5;   // scatters from this oversampling on use wave-private accumulators
 static_assert((TC & (TC - 1)) == 0, "tile width must be a power of two");
 static_assert(kChunk2 <= 65535, "pose index must fit the list entries");
 
@@ -209,10 +210,75 @@ __device__ __forceinline__ void scatter_sample2(const Geom& g, const Slot2& sd, 
     }
 }
 
+// The same for a wave-private fp32 accumulator (PRIV): plain read-add-write
+// instead of LDS atomics, legal because the 64 lanes of a window hold
+// samples of one pose, whose positions are at least os > sqrt(2) apart and so
+// lie in distinct cells: the lanes of one tap never share a cell.  A wave's
+// LDS operations execute in order; the signal fence keeps the compiler from
+// moving one tap's read above the previous tap's write (another lane's tap
+// may have written that cell).  Products as the reference forms them:
+// (v * wr) * wc in fp32.
+template <bool CUBIC, int MODE, bool WEIGHTS>
+__device__ __forceinline__ void scatter_sample2_priv(const Geom& g, const Slot2& sd, int rr, int cc, Cx<float> v,
+                                                     float wpix, bool shifted, bool flip, const TapMap2& tm,
+                                                     float2* pc, float* pw) {
+    constexpr int K = CUBIC ? 4 : 2, LOW = CUBIC ? 1 : 0;
+    const float fr = float(rr), fc = float(cc);
+    float x[2];
+    rotate_pix(sd.R, fr, fc, g.os, x);
+    if (shifted) {
+        if (MODE == 0) v = cmul(v, cconj(phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k)));
+        else v = cmul(v, phase_hw(-fr, -fc, sd.s0, sd.s1, g.phase_k));
+    }
+    constexpr int S[2] = {TC, TR};
+    int loc[2][K];
+    float wt[2][K];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+        float f;
+        const int fl = split_as<false>(x[a], f);
+        const int l0 = (flip ? -fl : fl) + tm.off[a];
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            const int l = l0 + tm.sgn * j;
+            loc[a][j] = (unsigned)(l - tm.lmin[a]) < (unsigned)(S[a] - tm.lmin[a]) ? l : -1;
+            if (CUBIC) wt[a][j] = cubic_w<float>(f - float(j - LOW));
+        }
+        if (!CUBIC) {
+            wt[a][1] = f;
+            wt[a][0] = 1.0f - f;
+        }
+    }
+    const float vre = v.re, vim = flip ? -v.im : v.im;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        if (loc[1][i] < 0) continue;
+        const int row = loc[1][i] * TC, rot = swizzle2(loc[1][i]);
+        const float rre = vre * wt[1][i], rim = vim * wt[1][i];
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            if (loc[0][j] < 0) continue;
+            const int li = row + ((loc[0][j] + rot) & (TC - 1));
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            float2 t = pc[li];
+            t.x += rre * wt[0][j];
+            t.y += rim * wt[0][j];
+            pc[li] = t;
+            if (WEIGHTS) {
+                const float w = wt[1][i] * wt[0][j];
+                pw[li] += wpix * (CUBIC ? fabsf(w) : w);
+            }
+        }
+    }
+}
+
 // MODE 0: backprojection, v = proj * conj(phase(r, c)), optional weights.
 // MODE 1: reconstruction gradient of the projection, v = g * phase(-r, -c).
 // dst (and wdst) must be zero-filled: every item adds its partial tile.
-template <bool CUBIC, int MODE, bool WEIGHTS, int KP>
+// PRIV (one pose per window, KP = 1, os > sqrt(2) with margin): wave-private
+// fp32 accumulators without atomics, summed over the waves at write-out;
+// otherwise one fp64 accumulator per tile with LDS atomics.
+template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool PRIV = false>
 __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 ts, const Cx<float>* __restrict__ src,
                                                              const float* __restrict__ weights,
                                                              const float* __restrict__ rot,
@@ -222,8 +288,12 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
     constexpr int SLOW = CUBIC ? 1 : 0;                    // first tap at floor(x) - SLOW
     constexpr int RPS = 64 / KP;
     constexpr int NW = kThreads / 64;
-    __shared__ double acc_re[T2], acc_im[T2];
-    __shared__ double acc_w[WEIGHTS ? T2 : 1];
+    static_assert(!PRIV || KP == 1, "private accumulation needs one pose per window");
+    constexpr int TS = PRIV ? 1 : T2, TP = PRIV ? T2 : 1;
+    __shared__ double acc_re[TS], acc_im[TS];
+    __shared__ double acc_w[WEIGHTS ? TS : 1];
+    __shared__ float2 pacc[NW][TP];
+    __shared__ float pwacc[NW][WEIGHTS ? TP : 1];
     __shared__ unsigned short plist[2 * kChunk2];
     __shared__ int pcnt[2];
     __shared__ Slot2 slots[NW][KP];
@@ -253,9 +323,17 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
         const float lo2[2] = {float(fc0 - SL) - ts.eps, float(fr0 - SL) - ts.eps};
         const float hi2[2] = {float(fc0 + TC + SH) + ts.eps, float(fr0 + TR + SH) + ts.eps};
         for (int e = tid; e < T2; e += kThreads) {
-            acc_re[e] = 0.0;
-            acc_im[e] = 0.0;
-            if (WEIGHTS) acc_w[e] = 0.0;
+            if constexpr (PRIV) {
+#pragma unroll
+                for (int k = 0; k < NW; ++k) {
+                    pacc[k][e] = float2{0.f, 0.f};
+                    if (WEIGHTS) pwacc[k][e] = 0.f;
+                }
+            } else {
+                acc_re[e] = 0.0;
+                acc_im[e] = 0.0;
+                if (WEIGHTS) acc_w[e] = 0.0;
+            }
         }
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
         const float* rotb = rot + rb * g.P * 4;
@@ -359,10 +437,16 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
                             Cx<float> v2 = {0.f, 0.f};
                             float wv2 = 0.f;
                             if (e0 + 64 < total) fetch_sample(e0 + 64, rr2, cc2, sl2, ok2, v2, wv2);
-                            if (ok)
-                                scatter_sample2<CUBIC, MODE, WEIGHTS>(g, slots[wave][sl], rr, cc, v, wv,
-                                                                      shifts != nullptr, pass == 1, tm, acc_re,
-                                                                      acc_im, acc_w);
+                            if (ok) {
+                                if constexpr (PRIV)
+                                    scatter_sample2_priv<CUBIC, MODE, WEIGHTS>(g, slots[wave][sl], rr, cc, v, wv,
+                                                                               shifts != nullptr, pass == 1, tm,
+                                                                               pacc[wave], pwacc[wave]);
+                                else
+                                    scatter_sample2<CUBIC, MODE, WEIGHTS>(g, slots[wave][sl], rr, cc, v, wv,
+                                                                          shifts != nullptr, pass == 1, tm, acc_re,
+                                                                          acc_im, acc_w);
+                            }
                             rr = rr2;
                             cc = cc2;
                             sl = sl2;
@@ -386,10 +470,23 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
                 const int re = r < 0 ? r + N : r;
                 const int64_t idx = b * g.vol + int64_t(re) * H + c;
                 const int a = (e - lc) + ((lc + swizzle2(lr)) & (TC - 1));
-                const double vr = acc_re[a], vi = acc_im[a];
+                double vr, vi, vw = 0.0;
+                if constexpr (PRIV) {
+                    vr = vi = 0.0;
+#pragma unroll
+                    for (int k = 0; k < NW; ++k) {
+                        vr += double(pacc[k][a].x);
+                        vi += double(pacc[k][a].y);
+                        if (WEIGHTS) vw += double(pwacc[k][a]);
+                    }
+                } else {
+                    vr = acc_re[a];
+                    vi = acc_im[a];
+                    if (WEIGHTS) vw = acc_w[a];
+                }
                 if (vr != 0.0) atomic_add(&dst[idx].re, float(vr));
                 if (vi != 0.0) atomic_add(&dst[idx].im, float(vi));
-                if (WEIGHTS && acc_w[a] != 0.0) atomic_add(&wdst[idx], float(acc_w[a]));
+                if (WEIGHTS && vw != 0.0) atomic_add(&wdst[idx], float(vw));
             }
         }
         __syncthreads();
@@ -422,12 +519,13 @@ __global__ __launch_bounds__(kBlock) void k_mirror2_x0(Geom g, Cx<float>* __rest
     }
 }
 
-template <bool CUBIC, int MODE, bool WEIGHTS, int KP>
+template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool PRIV = false>
 hipError_t scatter2_launch(const Geom& g, const TileSpec2& ts, const void* src, const void* weights,
                            const void* rot, const void* shifts, void* dst, void* wdst, hipStream_t s) {
     const int64_t work = g.B * ts.ksplit * int64_t(ts.nr) * ts.nc;
     if (work > 0) {
-        hipLaunchKernelGGL((k_scatter2_tiled<CUBIC, MODE, WEIGHTS, KP>), dim3(grid_for(kXcds * xcd_per<kRun>(work))),
+        hipLaunchKernelGGL((k_scatter2_tiled<CUBIC, MODE, WEIGHTS, KP, PRIV>),
+                           dim3(grid_for(kXcds * xcd_per<kRun>(work))),
                            dim3(kThreads), 0, s, g, ts, (const Cx<float>*)src, (const float*)weights,
                            (const float*)rot, (const float*)shifts, (Cx<float>*)dst, (float*)wdst);
         const hipError_t e = hipGetLastError();
@@ -445,6 +543,10 @@ hipError_t scatter2_launch(const Geom& g, const TileSpec2& ts, const void* src, 
 template <bool CUBIC, int MODE, bool WEIGHTS>
 hipError_t scatter2_kp(const Geom& g, const TileSpec2& ts, const void* src, const void* weights, const void* rot,
                        const void* shifts, void* dst, void* wdst, hipStream_t s) {
+    // one pose per window keeps a window's samples >= os * (1 - 2 kRotationTol) - 1e-3 apart,
+    // beyond sqrt(2) (the diagonal of a cell) from os = 1.5 on
+    if (g.os >= kPrivOs)
+        return scatter2_launch<CUBIC, MODE, WEIGHTS, 1, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
     if (ts.kp >= 4) return scatter2_launch<CUBIC, MODE, WEIGHTS, 4>(g, ts, src, weights, rot, shifts, dst, wdst, s);
     if (ts.kp == 2) return scatter2_launch<CUBIC, MODE, WEIGHTS, 2>(g, ts, src, weights, rot, shifts, dst, wdst, s);
     return scatter2_launch<CUBIC, MODE, WEIGHTS, 1>(g, ts, src, weights, rot, shifts, dst, wdst, s);
