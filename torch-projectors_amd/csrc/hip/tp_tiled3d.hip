@@ -700,14 +700,18 @@ __device__ __forceinline__ void scatter_sample(const Geom& g, const Slot& sd, in
             if (loc[1][i] < 0) continue;
             const double wdr = wt[2][k] * wt[1][i];
             const int row = (loc[2][k] * SR + loc[1][i]) * SC, rot = acc_swizzle(loc[1][i], loc[2][k]);
+            // cubic: the value (and weight) times wd * wr once per (d, r) pair, one product per tap
+            // after that; linear keeps one weight product per tap (two taps per pair)
+            const double pre = CUBIC ? vre * wdr : vre, pim = CUBIC ? vim * wdr : vim,
+                         pw = CUBIC ? wp * fabs(wdr) : wp;
 #pragma unroll
             for (int j = 0; j < K; ++j) {
                 if (loc[0][j] < 0) continue;
-                const double w = wdr * wt[0][j];
+                const double w = CUBIC ? wt[0][j] : wdr * wt[0][j];
                 const int li = row + ((loc[0][j] + rot) & (SC - 1));
-                atomicAdd(&acc_re[li], vre * w);
-                atomicAdd(&acc_im[li], vim * w);
-                if (WEIGHTS) atomicAdd(&acc_w[li], wp * (CUBIC ? fabs(w) : w));
+                atomicAdd(&acc_re[li], pre * w);
+                atomicAdd(&acc_im[li], pim * w);
+                if (WEIGHTS) atomicAdd(&acc_w[li], pw * (CUBIC ? fabs(w) : w));
             }
         }
     }
