@@ -374,7 +374,9 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
     constexpr int RPS = 64 / KP;
     constexpr int NT = kForwThreads, NW = NT / 64;
     constexpr int LOADS = (W3 + NT - 1) / NT;
-    __shared__ Cx<float> vt[W3];
+    // the staged tile keeps the volume's storage type: a complex-half volume takes half the LDS
+    // (more workgroups per CU) and is widened on each tap read, to the same fp32 values
+    __shared__ Cx<VS> vt[W3];
     constexpr int CH = 2 * kChunk;  // poses culled per phase
     static_assert(CH <= int(kPoseMask) + 1, "pose index must fit below the flag bits");
     __shared__ unsigned short plist[CH];
@@ -413,7 +415,9 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
         const float* rotb = rot + rb * g.P * 9;
         const Cx<VS>* recb = rec + b * g.vol;
         auto lds = [&](int d, int r, int c) {
-            return vt[((d - (td - LO)) * W + (r - (tr - LO))) * W + (c - (tc - LO))];
+            const int e = ((d - (td - LO)) * W + (r - (tr - LO))) * W + (c - (tc - LO));
+            if constexpr (kHalfVolume<VS>) return Cx<float>{__half2float(vt[e].re), __half2float(vt[e].im)};
+            else return vt[e];
         };
         bool loaded = false;
         for (int pbase = it.p0; pbase < it.p1; pbase += CH) {
@@ -452,7 +456,13 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                     }
 #pragma unroll
                     for (int q = 0; q < STAGE; ++q)
-                        if (tid + (q0 + q) * NT < W3) vt[tid + (q0 + q) * NT] = v[q];
+                        if (tid + (q0 + q) * NT < W3) {
+                            // a widened half value (or its negation) narrows back exactly
+                            if constexpr (kHalfVolume<VS>)
+                                vt[tid + (q0 + q) * NT] = Cx<__half>{__float2half(v[q].re), __float2half(v[q].im)};
+                            else
+                                vt[tid + (q0 + q) * NT] = v[q];
+                        }
                 }
                 if constexpr (GMODE == 2 && WG) {
                     const float* gwb = gw + b * g.vol;
