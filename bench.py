@@ -530,11 +530,19 @@ def main():
     if a.copy_probe:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
+        torch.mul(src, 1.0, out=dst)  # warm-up
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
         for _ in range(5):  # an elementwise kernel (not a runtime blit) so counters see it
             torch.mul(src, 1.0, out=dst)
+        e1.record()
         torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 5
+        moved = 2 * src.numel() * 4
         print(json.dumps({"copy_probe_bytes_read": src.numel() * 4, "copy_probe_bytes_written": dst.numel() * 4,
-                          "calls": 5}))
+                          "calls": 6, "ms_per_copy": round(ms, 4), "copy_GBps": moved / (ms / 1e3) / 1e9,
+                          "copy_frac_of_peak": moved / (ms / 1e3) / 1e9 / HBM_PEAK_GBS}))
         return
     wl = WORKLOADS[a.config](dev)
     torch.cuda.synchronize()
