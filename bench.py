@@ -517,11 +517,12 @@ def main():
     ap.add_argument("--config", default="headline", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
-                    help="only run a plain 1 GiB copy kernel 5 times (calibrates HBM byte counters)")
+                    help="only run and time a plain 1 GiB copy kernel (calibrates HBM byte counters, measures the copy ceiling)")
     a = ap.parse_args()
     if a.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only (--gpus {a.gpus} requested); the multi-GPU "
-              "design (pose sharding + one volume all-reduce) is described in DESIGN.md", file=sys.stderr)
+        print(f"bench.py: this build runs on one GPU only (--gpus {a.gpus} requested); more GPUs would "
+              "shard the poses and all-reduce the backprojected volumes once, which is not built here",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch

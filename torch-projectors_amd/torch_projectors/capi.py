@@ -1,7 +1,7 @@
 """ctypes binding of the C ABI in include/torch_projectors_hip.h.
 
-This is the boundary a non-PyTorch host binds (see INTEGRATION.md at the repo
-root for the reference-side stubs).  `lib()` loads libtorch_projectors_hip.so
+This is the boundary a non-PyTorch host binds: plain pointers, sizes and a
+stream, no torch types.  `lib()` loads libtorch_projectors_hip.so
 and declares every entry point; `call(name, *args)` invokes one and raises
 RuntimeError with tp_last_error() on a non-zero return.  `EXPORTS` lists the
 symbols the header declares.
