@@ -58,11 +58,18 @@ def _done(*outs):
     return res[0] if len(res) == 1 else res
 
 
+def _poisoned(shape, dtype):
+    """An output buffer filled with NaN: every entry point writes every element of its outputs, so an
+    element left unwritten shows up as a NaN in the comparison instead of passing on stale zeros."""
+    fill = complex(float("nan"), float("nan")) if dtype.is_complex else float("nan")
+    return torch.full(tuple(shape), fill, dtype=dtype, device=DEV)
+
+
 def _grad_outputs(rotations, shifts, like):
     need_rot = rotations.requires_grad
     need_sh = shifts is not None and shifts.requires_grad
-    grot = torch.empty(rotations.shape, dtype=rotations.dtype, device=DEV) if need_rot else None
-    gsh = torch.empty(shifts.shape, dtype=shifts.dtype, device=DEV) if need_sh else None
+    grot = _poisoned(rotations.shape, rotations.dtype) if need_rot else None
+    gsh = _poisoned(shifts.shape, shifts.dtype) if need_sh else None
     return grot, gsh
 
 
@@ -75,7 +82,7 @@ def project_2d_forw(reconstruction, rotations, shifts, output_shape, interpolati
     rec, rot, sh = _g(reconstruction), _g(rotations), _g(shifts)
     B, N, H = rec.shape
     n = int(output_shape[0])
-    out = torch.empty(B, rot.shape[1], n, n // 2 + 1, dtype=_proj_dtype(rec), device=DEV)
+    out = _poisoned((B, rot.shape[1], n, n // 2 + 1), _proj_dtype(rec))
     capi.call("tp_project_2d_forw", _dt(rec), _p(rec), B, N, H, _p(rot), rot.shape[0], rot.shape[1], _p(sh),
               sh.shape[0] if sh is not None else 1, n, *_tail(interpolation, oversampling, fourier_radius_cutoff),
               _p(out), _stream())
@@ -87,7 +94,7 @@ def project_3d_to_2d_forw(reconstruction, rotations, shifts, output_shape, inter
     rec, rot, sh = _g(reconstruction), _g(rotations), _g(shifts)
     B, D, N, H = rec.shape
     n = int(output_shape[0])
-    out = torch.empty(B, rot.shape[1], n, n // 2 + 1, dtype=_proj_dtype(rec), device=DEV)
+    out = _poisoned((B, rot.shape[1], n, n // 2 + 1), _proj_dtype(rec))
     capi.call("tp_project_3d_to_2d_forw", _dt(rec), _p(rec), B, D, N, H, _p(rot), rot.shape[0], rot.shape[1],
               _p(sh), sh.shape[0] if sh is not None else 1, n,
               *_tail(interpolation, oversampling, fourier_radius_cutoff), _p(out), _stream())
@@ -98,7 +105,7 @@ def _project_back(name, dims, grad_projections, reconstruction, rotations, shift
                   fourier_radius_cutoff):
     g, rec, rot, sh = _g(grad_projections), _g(reconstruction), _g(rotations), _g(shifts)
     B, P, n, hp = g.shape
-    grec = torch.empty_like(rec)
+    grec = _poisoned(rec.shape, rec.dtype)
     grot, gsh = _grad_outputs(rotations, shifts, rec)
     rec_dims = list(rec.shape[1:])
     capi.call(name, _dt(rec), _p(g), B, P, n, hp, _p(rec), *rec_dims, _p(rot), rot.shape[0], _p(sh),
@@ -123,8 +130,8 @@ def _backproject_forw(name, dims, projections, weights, rotations, shifts, inter
     B, P, n, hp = pr.shape
     N = capi.rec_boxsize(n, oversampling)
     shape = (B, N, N // 2 + 1) if dims == 2 else (B, N, N, N // 2 + 1)
-    data = torch.empty(shape, dtype=pr.dtype, device=DEV)
-    wrec = torch.empty(shape, dtype=w.dtype, device=DEV) if w is not None else None
+    data = _poisoned(shape, pr.dtype)
+    wrec = _poisoned(shape, w.dtype) if w is not None else None
     capi.call(name, _dt(pr), _p(pr), B, P, n, hp, _p(w), _p(rot), rot.shape[0], _p(sh),
               sh.shape[0] if sh is not None else 1, *_tail(interpolation, oversampling, fourier_radius_cutoff),
               _p(data), _p(wrec), _stream())
@@ -146,8 +153,8 @@ def _backproject_back(name, grad_data_rec, grad_weight_rec, projections, weights
     rot, sh = _g(rotations), _g(shifts)
     B, P, n, hp = pr.shape
     N, H = gd.shape[-2], gd.shape[-1]
-    gproj = torch.empty_like(pr)
-    gweights = torch.empty_like(w) if w is not None else None
+    gproj = _poisoned(pr.shape, pr.dtype)
+    gweights = _poisoned(w.shape, w.dtype) if w is not None else None
     grot, gsh = _grad_outputs(rotations, shifts, pr)
     capi.call(name, _dt(pr), _p(gd), _p(gw), N, H, _p(pr), B, P, n, hp, _p(w), _p(rot), rot.shape[0], _p(sh),
               sh.shape[0] if sh is not None else 1, *_tail(interpolation, oversampling, fourier_radius_cutoff),
