@@ -218,5 +218,35 @@ def backproject_2d_to_3d_back(grad_data_rec, grad_weight_rec, projections, weigh
                              rotations, shifts, interpolation, oversampling, fourier_radius_cutoff, num_threads)
 
 
+def scatter_wide(op, args, num_threads=0):
+    """The scatter volumes of `op` (project_*_back's reconstruction gradient, backproject_*_forw's data and
+    weight volumes) for fp32 inputs, summed in double (tpo_*_wide in tp_oracle.cpp): the same fp32 tap
+    values as the op, each cell their exact sum.  `args` are the dispatcher op's positional arguments.
+    Returns a tuple of complex128 / float64 tensors in the op's output order (volumes only)."""
+    if op in ("project_2d_back", "project_3d_to_2d_back"):
+        gproj, rec, rot, sh, interp, os_, cut = args
+        g, rec, rot, sh = _c(gproj), _c(rec), _c(rot), _c(sh)
+        B, P, n, hp = g.shape
+        grec = torch.empty(rec.shape, dtype=torch.complex128)
+        shape = [_i(x) for x in rec.shape[1:]]
+        _call(f"tpo_{op}_wide", _p(g), _i(B), _i(P), _i(n), _i(hp), _p(rec), *shape, _p(rot), _i(rot.shape[0]),
+              _p(sh), _i(sh.shape[0] if sh is not None else 1), *_tail(interp, os_, cut, num_threads), _p(grec),
+              c_int(num_threads))
+        return (grec,)
+    if op in ("backproject_2d_forw", "backproject_2d_to_3d_forw"):
+        proj, w, rot, sh, interp, os_, cut = args
+        pr, w, rot, sh = _c(proj), _c(w), _c(rot), _c(sh)
+        B, P, n, hp = pr.shape
+        N = rec_boxsize(n, os_)
+        shape = (B, N, N // 2 + 1) if op == "backproject_2d_forw" else (B, N, N, N // 2 + 1)
+        data = torch.empty(shape, dtype=torch.complex128)
+        wrec = torch.empty(shape, dtype=torch.float64) if w is not None else None
+        _call(f"tpo_{op}_wide", _p(pr), _i(B), _i(P), _i(n), _i(hp), _p(w), _p(rot), _i(rot.shape[0]), _p(sh),
+              _i(sh.shape[0] if sh is not None else 1), *_tail(interp, os_, cut, num_threads), _p(data), _p(wrec),
+              c_int(num_threads))
+        return (data,) if wrec is None else (data, wrec)
+    raise ValueError(f"{op} has no scatter volume")
+
+
 OPS = ["project_2d_forw", "project_2d_back", "backproject_2d_forw", "backproject_2d_back",
        "project_3d_to_2d_forw", "project_3d_to_2d_back", "backproject_2d_to_3d_forw", "backproject_2d_to_3d_back"]

@@ -57,6 +57,8 @@ template <typename T> inline void atomic_add_cx(Cx<T>* dst, Cx<T> v) {  // atomi
     atomic_add(&dst->re, v.re);
     atomic_add(&dst->im, v.im);
 }
+// An accumulated value in the accumulator type (exact widening).
+template <typename A, typename T> inline Cx<A> widen(Cx<T> v) { return {A(v.re), A(v.im)}; }
 
 // ------------------------------------------------------------ cubic weights
 // cubic_kernels.h:25-43 / 50-67: Catmull-Rom a = -0.5.  `a` is of the real
@@ -426,13 +428,15 @@ void project_forw(const Common& cm, const Cx<T>* rec, int64_t B, int64_t N, int6
 
 // ------------------------------------------------------------ projection backward
 // cpu/2d/projection_2d_kernels.cpp:209-375, cpu/3d/projection_3d_to_2d_kernels.cpp:219-402
-template <int DIM, typename T>
+// A: accumulator type of the reconstruction gradient (T = the reference; double
+// for fp32 inputs = the exact sum of the same fp32 tap values, see tpo_*_wide).
+template <int DIM, typename T, typename A = T>
 void project_back(const Common& cm, const Cx<T>* gproj, int64_t B, int64_t P, int64_t n, int64_t hp,
                   const Cx<T>* rec, int64_t N, int64_t H, const T* rot, int64_t B_rot, const T* shifts,
-                  int64_t B_shift, Cx<T>* grec, T* grot, T* gshift, int nthreads) {
+                  int64_t B_shift, Cx<A>* grec, T* grot, T* gshift, int nthreads) {
     const int64_t RS = DIM == 2 ? 4 : 9;
     const int64_t vol = DIM == 2 ? N * H : N * N * H;
-    std::memset(grec, 0, sizeof(Cx<T>) * B * vol);
+    std::memset(grec, 0, sizeof(Cx<A>) * B * vol);
     if (grot) std::memset(grot, 0, sizeof(T) * B_rot * P * RS);
     if (gshift) std::memset(gshift, 0, sizeof(T) * B_shift * P * 2);
     const T cut2 = cutoff_sq<T>(cm, n);
@@ -442,7 +446,7 @@ void project_back(const Common& cm, const Cx<T>* gproj, int64_t B, int64_t P, in
         const T* R = rot + (rb_idx * P + p) * RS;
         const T* S = shifts ? shifts + (sb_idx * P + p) * 2 : nullptr;
         const Cx<T>* rb = rec + b * vol;
-        Cx<T>* gb = grec + b * vol;
+        Cx<A>* gb = grec + b * vol;
         T lrot[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
         T lsh[2] = {0, 0};
         for (int64_t i = 0; i < n; ++i) {
@@ -461,7 +465,7 @@ void project_back(const Common& cm, const Cx<T>* gproj, int64_t B, int64_t P, in
                     const int64_t idx = scatter_index<DIM>(N, H, d, rr, cc, cj);
                     if (idx < 0) return;
                     const Cx<T> v = tap_value<DIM, T>(g, wd, wr, wc);
-                    atomic_add_cx(&gb[idx], cj ? cconj(v) : v);
+                    atomic_add_cx(&gb[idx], widen<A>(cj ? cconj(v) : v));
                 });
                 if (grot) {
                     const Interp<T> it = interpolate<DIM>(rb, N, H, x, cm.cubic, true);
@@ -495,22 +499,23 @@ int64_t rec_box(int64_t n, double os) {
     return raw + (raw % 2);
 }
 
-template <int DIM, typename T>
+// A: accumulator type of the data and weight volumes (as project_back).
+template <int DIM, typename T, typename A = T>
 void backproject_forw(const Common& cm, const Cx<T>* proj, int64_t B, int64_t P, int64_t n, int64_t hp,
                       const T* weights, const T* rot, int64_t B_rot, const T* shifts, int64_t B_shift,
-                      Cx<T>* data, T* wrec, int nthreads) {
+                      Cx<A>* data, A* wrec, int nthreads) {
     const int64_t N = rec_box(n, cm.os), H = N / 2 + 1;
     const int64_t RS = DIM == 2 ? 4 : 9;
     const int64_t vol = DIM == 2 ? N * H : N * N * H;
-    std::memset(data, 0, sizeof(Cx<T>) * B * vol);
-    if (wrec) std::memset(wrec, 0, sizeof(T) * B * vol);
+    std::memset(data, 0, sizeof(Cx<A>) * B * vol);
+    if (wrec) std::memset(wrec, 0, sizeof(A) * B * vol);
     const T cut2 = cutoff_sq<T>(cm, n);
     parallel_for_bp(B * P, nthreads, [&](int64_t bp) {
         const int64_t b = bp / P, p = bp % P;
         const T* R = rot + ((B_rot == 1 ? 0 : b) * P + p) * RS;
         const T* S = shifts ? shifts + ((B_shift == 1 ? 0 : b) * P + p) * 2 : nullptr;
-        Cx<T>* db = data + b * vol;
-        T* wb = wrec ? wrec + b * vol : nullptr;
+        Cx<A>* db = data + b * vol;
+        A* wb = wrec ? wrec + b * vol : nullptr;
         for (int64_t i = 0; i < n; ++i) {
             for (int64_t j = 0; j < hp; ++j) {
                 const T r = freq_of<T>(i, n), c = T(j);
@@ -529,10 +534,10 @@ void backproject_forw(const Common& cm, const Cx<T>* proj, int64_t B, int64_t P,
                     if (idx < 0) return;
                     const Cx<T> tv = tap_value<DIM, T>(v, wd, wr, wc);
                     const Cx<T> fv = cj ? cconj(tv) : tv;
-                    atomic_add_cx(&db[idx], fv);
+                    atomic_add_cx(&db[idx], widen<A>(fv));
                     if (cc == 0) {
                         const int64_t m = mirror_index<DIM>(N, H, d, rr);
-                        if (m >= 0) atomic_add_cx(&db[m], cconj(fv));
+                        if (m >= 0) atomic_add_cx(&db[m], widen<A>(cconj(fv)));
                     }
                 });
                 // weight lambda (cpu/2d/backprojection_2d_kernels.cpp:236-264,
@@ -545,10 +550,10 @@ void backproject_forw(const Common& cm, const Cx<T>* proj, int64_t B, int64_t P,
                         bool cj;
                         const int64_t idx = scatter_index<DIM>(N, H, d, rr, cc, cj);
                         if (idx < 0) return;
-                        atomic_add(&wb[idx], fw);
+                        atomic_add(&wb[idx], A(fw));
                         if (cc == 0) {
                             const int64_t m = mirror_index<DIM>(N, H, d, rr);
-                            if (m >= 0) atomic_add(&wb[m], fw);
+                            if (m >= 0) atomic_add(&wb[m], A(fw));
                         }
                     });
                 }
@@ -791,6 +796,61 @@ int tpo_backproject_2d_to_3d_back(int dtype, const void* gdata, const void* gw, 
                                              n, hp, (const T*)weights, (const T*)rot, B_rot, (const T*)shifts,
                                              B_shift, (Cx<T>*)gproj, weights ? (T*)gweights : nullptr, (T*)grot,
                                              shifts ? (T*)gshift : nullptr, nthreads));
+    return 0;
+}
+
+// The scatters of fp32 inputs summed in double: every sample coordinate,
+// stencil decision and fp32 tap value is the reference's, and each cell is the
+// exact sum of those values (to double rounding) instead of one fp32 order of
+// it.  The reference's fp32 atomics may add in any order, so this is the value
+// every order approximates; the tests' per-cell scatter bar is taken against
+// it.  Outputs: complex128 / float64 volumes.
+int tpo_project_2d_back_wide(const void* gproj, int64_t B, int64_t P, int64_t n, int64_t hp, const void* rec,
+                             int64_t N, int64_t H, const void* rot, int64_t B_rot, const void* shifts,
+                             int64_t B_shift, int interp, double os, int has_cut, double cut, void* grec,
+                             int nthreads) {
+    if (!check_common(0, interp, B, B_rot, P, shifts, B_shift)) return 1;
+    const Common cm{interp == 1, os, has_cut, cut};
+    project_back<2, float, double>(cm, (const Cx<float>*)gproj, B, P, n, hp, (const Cx<float>*)rec, N, H,
+                                   (const float*)rot, B_rot, (const float*)shifts, B_shift, (Cx<double>*)grec,
+                                   nullptr, nullptr, nthreads);
+    return 0;
+}
+
+int tpo_project_3d_to_2d_back_wide(const void* gproj, int64_t B, int64_t P, int64_t n, int64_t hp,
+                                   const void* rec, int64_t D, int64_t N, int64_t H, const void* rot, int64_t B_rot,
+                                   const void* shifts, int64_t B_shift, int interp, double os, int has_cut,
+                                   double cut, void* grec, int nthreads) {
+    if (!check_common(0, interp, B, B_rot, P, shifts, B_shift)) return 1;
+    if (D != N) return fail("reconstruction depth must equal its height"), 1;
+    const Common cm{interp == 1, os, has_cut, cut};
+    project_back<3, float, double>(cm, (const Cx<float>*)gproj, B, P, n, hp, (const Cx<float>*)rec, N, H,
+                                   (const float*)rot, B_rot, (const float*)shifts, B_shift, (Cx<double>*)grec,
+                                   nullptr, nullptr, nthreads);
+    return 0;
+}
+
+int tpo_backproject_2d_forw_wide(const void* proj, int64_t B, int64_t P, int64_t n, int64_t hp,
+                                 const void* weights, const void* rot, int64_t B_rot, const void* shifts,
+                                 int64_t B_shift, int interp, double os, int has_cut, double cut, void* data,
+                                 void* wrec, int nthreads) {
+    if (!check_common(0, interp, B, B_rot, P, shifts, B_shift)) return 1;
+    const Common cm{interp == 1, os, has_cut, cut};
+    backproject_forw<2, float, double>(cm, (const Cx<float>*)proj, B, P, n, hp, (const float*)weights,
+                                       (const float*)rot, B_rot, (const float*)shifts, B_shift, (Cx<double>*)data,
+                                       (double*)wrec, nthreads);
+    return 0;
+}
+
+int tpo_backproject_2d_to_3d_forw_wide(const void* proj, int64_t B, int64_t P, int64_t n, int64_t hp,
+                                       const void* weights, const void* rot, int64_t B_rot, const void* shifts,
+                                       int64_t B_shift, int interp, double os, int has_cut, double cut, void* data,
+                                       void* wrec, int nthreads) {
+    if (!check_common(0, interp, B, B_rot, P, shifts, B_shift)) return 1;
+    const Common cm{interp == 1, os, has_cut, cut};
+    backproject_forw<3, float, double>(cm, (const Cx<float>*)proj, B, P, n, hp, (const float*)weights,
+                                       (const float*)rot, B_rot, (const float*)shifts, B_shift, (Cx<double>*)data,
+                                       (double*)wrec, nthreads);
     return 0;
 }
 

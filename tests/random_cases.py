@@ -47,3 +47,20 @@ def scale_poses(args, case):
     r[:, ::2] *= 1.05
     args[idx] = r.requires_grad_(rg)
     return args
+
+
+def nonfinite_cutoff_cases():
+    """Every op with a radius cutoff of +inf, NaN, 3e9 (a square beyond every int) and 1e30 (whose fp32
+    square overflows): the mask keeps every pixel (r^2 + c^2 > inf and > NaN are false), so the
+    results equal those without a cutoff but wider than the grid."""
+    out = []
+    seed = 5150
+    for op in OPS:
+        for tag, cut in (("inf", float("inf")), ("nan", float("nan")), ("3e9", 3e9), ("1e30", 1e30)):
+            seed += 1
+            interp = "cubic" if tag == "nan" else "linear"
+            n = 32 if "3d" in op else 48
+            c = _case(f"cut{tag}_{op}_{interp}", op, interp=interp, os=2.0, cutoff=cut, B=1, P=6, n=n, seed=seed)
+            c["scaled"] = False
+            out.append(c)
+    return out

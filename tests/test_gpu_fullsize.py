@@ -9,7 +9,9 @@ properties that hold at any size:
 * batch items are independent: a sampled item's volume sums equal the
   oracle's on that item's poses;
 * a volume sum over every pose is compared whole where the oracle finishes
-  in seconds (the headline backprojection).
+  in seconds (the headline and c3 backprojections, c1), and there also cell
+  by cell (tests/parity.py `check_cells`: untouched cells exactly 0, every
+  other cell within 1e-5 * max|v| * sum|tap weight|).
 
 Inputs follow bench.py's synthetic recipes (seeded).  Bars as tests/parity.py:
 gathers bit-identical without shifts, else relative L2 1e-5; scatters and
@@ -19,7 +21,7 @@ import pytest
 import torch
 
 import bench
-from tests.parity import GATHER_TOL, SCATTER_TOL, rel_l2
+from tests.parity import GATHER_TOL, SCATTER_TOL, check_scatter, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -81,9 +83,13 @@ def test_headline_backprojection_whole(headline, ops, O):
     proj = ops.project_3d_to_2d_forw(vol, rot, sh, [256, 256], "linear", 2.0, None)
     data, wrec = ops.backproject_2d_to_3d_forw(proj, w, rot, sh, "linear", 2.0, None)
     assert data.shape == (1, 512, 512, 257) and wrec.shape == (1, 512, 512, 257)
-    ed, ew = O.backproject_2d_to_3d_forw(proj.cpu(), w.cpu(), rot.cpu(), sh.cpu(), "linear", 2.0, None)
+    proj_c = proj.cpu()
+    ed, ew = O.backproject_2d_to_3d_forw(proj_c, w.cpu(), rot.cpu(), sh.cpu(), "linear", 2.0, None)
     close(data.cpu(), ed, SCATTER_TOL[F32], "backprojection data")
     close(wrec.cpu(), ew, SCATTER_TOL[F32], "backprojection weights")
+    say("headline backprojection, cell by cell")
+    check_scatter("backproject_2d_to_3d_forw", (data, wrec), [proj_c, w, rot, sh, "linear", 2.0, None], O,
+                  "headline backprojection")
 
 
 # ----------------------------------------------------------------------------- c1 - c3
@@ -122,9 +128,13 @@ def test_c3_backprojection_whole(ops, O, gpu):
     say("c3 backprojection, 8192 poses, whole volume against the oracle")
     data, wrec = ops.backproject_2d_to_3d_forw(proj, w, rot, sh, "linear", 2.0, None)
     assert data.shape == (1, 256, 256, 129)
-    ed, ew = O.backproject_2d_to_3d_forw(proj.cpu(), w.cpu(), rot.cpu(), sh.cpu(), "linear", 2.0, None)
+    proj_c = proj.cpu()
+    ed, ew = O.backproject_2d_to_3d_forw(proj_c, w.cpu(), rot.cpu(), sh.cpu(), "linear", 2.0, None)
     close(data.cpu(), ed, SCATTER_TOL[F32], "c3 backprojection data")
     close(wrec.cpu(), ew, SCATTER_TOL[F32], "c3 backprojection weights")
+    say("c3 backprojection, cell by cell")
+    check_scatter("backproject_2d_to_3d_forw", (data, wrec), [proj_c, w, rot, sh, "linear", 2.0, None], O,
+                  "c3 backprojection")
 
 
 # ----------------------------------------------------------------------------- c4 (3D cubic, forward + backward)
@@ -158,13 +168,18 @@ def test_c4_cubic_backward(c4, ops, O):
     _, er, es = O.project_3d_to_2d_back(g[:, POSES].cpu(), vol_c, r_c, s_c, "cubic", 2.0, None)
     close(grot[:, POSES].cpu(), er, SCATTER_TOL[F32], "rotation gradients, sampled poses")
     close(gsh[:, POSES].cpu(), es, SCATTER_TOL[F32], "shift gradients, sampled poses")
-    say("c4 reconstruction gradient over the first 48 poses, whole volume")
-    sub = slice(0, 48)
-    grec_s, _, _ = ops.project_3d_to_2d_back(g[:, sub].contiguous(), vol, rot[:, sub].contiguous(),
-                                             sh[:, sub].contiguous(), "cubic", 2.0, None)
-    eg, _, _ = O.project_3d_to_2d_back(g[:, sub].cpu(), vol_c, rot[:, sub].cpu(), sh[:, sub].cpu(), "cubic", 2.0,
-                                       None)
-    close(grec_s.cpu(), eg, SCATTER_TOL[F32], "reconstruction gradient")
+    for p0 in (0, 1000):
+        say(f"c4 reconstruction gradient over poses {p0}-{p0 + 47}, whole volume, also cell by cell")
+        sub = slice(p0, p0 + 48)
+        g_s = g[:, sub].contiguous()
+        grec_s, _, _ = ops.project_3d_to_2d_back(g_s, vol, rot[:, sub].contiguous(), sh[:, sub].contiguous(),
+                                                 "cubic", 2.0, None)
+        g_c = g_s.cpu()
+        eg, _, _ = O.project_3d_to_2d_back(g_c, vol_c, rot[:, sub].cpu(), sh[:, sub].cpu(), "cubic", 2.0, None)
+        close(grec_s.cpu(), eg, SCATTER_TOL[F32], f"reconstruction gradient, poses {p0}-{p0 + 47}")
+        check_scatter("project_3d_to_2d_back", (grec_s,),
+                      [g_c, vol_c, rot[:, sub], sh[:, sub], "cubic", 2.0, None], O,
+                      f"reconstruction gradient, poses {p0}-{p0 + 47}")
 
 
 # ----------------------------------------------------------------------------- c5 (batched 2D cubic)
@@ -201,6 +216,9 @@ def test_c5_batched_2d_cubic(c5, ops, O):
                                        sh[b:b + 1].cpu(), "cubic", 2.0, 64.0)
         close(data[b:b + 1].cpu(), ed, SCATTER_TOL[F32], f"backprojection data (item {b})")
         close(wrec[b:b + 1].cpu(), ew, SCATTER_TOL[F32], f"backprojection weights (item {b})")
+        check_scatter("backproject_2d_forw", (data[b:b + 1], wrec[b:b + 1]),
+                      [proj[b:b + 1], ones[b:b + 1], rot[b:b + 1], sh[b:b + 1], "cubic", 2.0, 64.0], O,
+                      f"backprojection (item {b})")
 
     say("c5 backward of a loss on (data, weight)")
     gen = torch.Generator().manual_seed(20261201 + 55)
@@ -220,11 +238,21 @@ def test_c5_batched_2d_cubic(c5, ops, O):
         close(gsh[b:b + 1, p:p + 1].cpu(), e[3], SCATTER_TOL[F32], f"grad_shifts (item {b}, pose {p})")
     del ones, gwts
 
-    say("c5 reconstruction gradient (project_2d_back), item 0 over all its poses")
-    grec, _, _ = ops.project_2d_back(gproj, rec, rot, sh, "cubic", 2.0, 64.0)
-    assert grec.shape == rec.shape
-    eg, _, _ = O.project_2d_back(gproj[0:1].cpu(), rec_c[0:1], rot[0:1].cpu(), sh[0:1].cpu(), "cubic", 2.0, 64.0)
+    say("c5 project_2d_back: reconstruction gradient of item 0 over all its poses, and the rotation and "
+        "shift gradients of sampled (item, pose) pairs")
+    grec, grot, gsh = ops.project_2d_back(gproj, rec, rg, sg, "cubic", 2.0, 64.0)
+    assert grec.shape == rec.shape and grot.shape == rot.shape and gsh.shape == sh.shape
+    g0 = gproj[0:1].cpu()
+    eg, _, _ = O.project_2d_back(g0, rec_c[0:1], rot[0:1].cpu(), sh[0:1].cpu(), "cubic", 2.0, 64.0)
     close(grec[0:1].cpu(), eg, SCATTER_TOL[F32], "reconstruction gradient (item 0)")
+    check_scatter("project_2d_back", (grec[0:1],), [g0, rec_c[0:1], rot[0:1], sh[0:1], "cubic", 2.0, 64.0], O,
+                  "reconstruction gradient (item 0)")
+    for b, p in PAIRS:
+        r_c = rot[b:b + 1, p:p + 1].cpu().requires_grad_(True)
+        s_c = sh[b:b + 1, p:p + 1].cpu().requires_grad_(True)
+        _, er, es = O.project_2d_back(gproj[b:b + 1, p:p + 1].cpu(), rec_c[b:b + 1], r_c, s_c, "cubic", 2.0, 64.0)
+        close(grot[b:b + 1, p:p + 1].cpu(), er, SCATTER_TOL[F32], f"project_2d_back grad_rotations ({b}, {p})")
+        close(gsh[b:b + 1, p:p + 1].cpu(), es, SCATTER_TOL[F32], f"project_2d_back grad_shifts ({b}, {p})")
 
 
 # ----------------------------------------------------------------------------- empty inputs

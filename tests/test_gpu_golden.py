@@ -11,16 +11,17 @@ import os
 import pytest
 
 from tests.golden.cases import build_args
-from tests.parity import check_outputs
+from tests.parity import check_outputs, scatter_cells
 from tests.test_oracle_golden import GOLDEN, load_fixture
 
 pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("path", GOLDEN, ids=[os.path.basename(p)[:-4] for p in GOLDEN])
-def test_hip_matches_reference_golden(path, hip):
+def test_hip_matches_reference_golden(path, hip, oracle):
     case, tensors, expected = load_fixture(path)
     args = build_args(case, tensors)
     print(f"[golden] {case['name']} op={case['op']} dtype={case['dtype']}", flush=True)
     got = getattr(hip, case["op"])(*args)
-    check_outputs(case["op"], got, expected, has_shifts=tensors.get("shifts") is not None, label=case["name"])
+    check_outputs(case["op"], got, expected, has_shifts=tensors.get("shifts") is not None, label=case["name"],
+                  cells=scatter_cells(case["op"], args, oracle))

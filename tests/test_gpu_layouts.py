@@ -6,10 +6,12 @@ an expanded (stride-0) pose tensor or a permuted shift tensor must give the
 result of the same values laid out densely: bit for bit for the forward
 projections (deterministic gathers), within rel-L2 1e-6 for the scatters
 (the order of fp64 partial sums may differ).  Poses in float64 with a
-complex64 volume are converted to the volume's real type (this library's
-choice; the reference's CUDA wrapper reads them through data_ptr<float>),
-and shifts whose dtype differs from the rotations' are rejected as in the
-reference (projection_utils.h:45-46).
+complex64 volume are rejected, as the reference's GPU path rejects them (its
+CUDA wrapper reads them through data_ptr<float>,
+cuda/3d/projection_3d_to_2d_kernels.cu:987-988), and so are shifts whose
+dtype differs from the rotations' (projection_utils.h:45-46) and weights
+whose dtype differs from the rotations' (the reference reads weights through
+the rotations' type, cpu/3d/backprojection_2d_to_3d_kernels.cpp:165-169).
 """
 import pytest
 import torch
@@ -44,9 +46,8 @@ def test_strided_inputs_forward(gpu, dim, interp):
     got = f(rec, rot, sh, [n, n], interp, 2.0, None)
     exp = f(rec.contiguous(), rot.contiguous(), sh.contiguous(), [n, n], interp, 2.0, None)
     assert torch.equal(got, exp)
-    # float64 poses are read in the volume's real type
-    got64 = f(rec, rot.double(), sh.double(), [n, n], interp, 2.0, None)
-    assert got64.dtype == torch.complex64 and torch.equal(got64, exp)
+    with pytest.raises(RuntimeError, match="needs float32 rotations"):
+        f(rec, rot.double(), sh.double(), [n, n], interp, 2.0, None)
     with pytest.raises(RuntimeError, match="same dtype"):
         f(rec, rot, sh.double(), [n, n], interp, 2.0, None)
 
@@ -68,3 +69,13 @@ def test_strided_inputs_backprojection(gpu, dim, interp):
     d1, w1 = f(proj, w, rot, sh, interp, 2.0, None)
     d2, w2 = f(proj.contiguous(), w.contiguous(), rot.contiguous(), sh.contiguous(), interp, 2.0, None)
     assert rel_l2(d1, d2) <= 1e-6 and rel_l2(w1, w2) <= 1e-6
+    with pytest.raises(RuntimeError, match="Weights must have the rotations' dtype"):
+        f(proj, w.double(), rot, sh, interp, 2.0, None)
+    with pytest.raises(RuntimeError, match="needs float32 rotations"):
+        f(proj, w.double(), rot.double(), sh.double(), interp, 2.0, None)
+    # complex128 takes float32 poses and weights: widened exactly, weight volume in the weights' dtype
+    p64 = proj.to(torch.complex128)
+    d3, w3 = f(p64, w, rot, sh, interp, 2.0, None)
+    d4, w4 = f(p64, w.double(), rot.double(), sh.double(), interp, 2.0, None)
+    assert w3.dtype == torch.float32 and w4.dtype == torch.float64
+    assert rel_l2(d3, d4) <= 1e-12 and rel_l2(w3.double(), w4) <= 1e-6

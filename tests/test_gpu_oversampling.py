@@ -8,7 +8,7 @@ Bar: tests/parity.py.
 import pytest
 
 from tests.golden.cases import _case, make_inputs
-from tests.parity import check_outputs
+from tests.parity import check_outputs, scatter_cells
 
 pytestmark = pytest.mark.gpu
 
@@ -35,4 +35,5 @@ def test_inexact_oversampling(case, hip, oracle):
     print(f"[osx] {case['name']}", flush=True)
     got = getattr(hip, case["op"])(*args)
     exp = getattr(oracle, case["op"])(*args)
-    check_outputs(case["op"], got, exp, has_shifts=tensors.get("shifts") is not None, label=case["name"])
+    check_outputs(case["op"], got, exp, has_shifts=tensors.get("shifts") is not None, label=case["name"],
+                  cells=scatter_cells(case["op"], args, oracle))

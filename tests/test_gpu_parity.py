@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from tests.golden.cases import _case, make_inputs
-from tests.parity import check_outputs
+from tests.parity import check_outputs, scatter_cells
 
 pytestmark = pytest.mark.gpu
 
@@ -60,4 +60,5 @@ def test_hip_matches_oracle(case, hip, oracle):
     print(f"[parity] {case['name']}", flush=True)
     got = getattr(hip, case["op"])(*args)
     exp = getattr(oracle, case["op"])(*args)
-    check_outputs(case["op"], got, exp, has_shifts=tensors.get("shifts") is not None, label=case["name"])
+    check_outputs(case["op"], got, exp, has_shifts=tensors.get("shifts") is not None, label=case["name"],
+                  cells=scatter_cells(case["op"], args, oracle))

@@ -2,17 +2,19 @@
 
 The same seeded configuration generator as tests/test_oracle_ref_random.py
 (where the oracle is pinned bit for bit to the reference's compiled CPU
-kernels), plus empty pose sets.  Bar: tests/parity.py.
+kernels), plus empty pose sets and cutoffs of +inf, NaN and beyond any int
+(the tiled kernels cap each row's columns by the disc only where that cap is
+a finite int).  Bar: tests/parity.py.
 """
 import pytest
 
 from tests.golden.cases import make_inputs
-from tests.parity import check_outputs
-from tests.random_cases import random_cases, scale_poses
+from tests.parity import check_outputs, scatter_cells
+from tests.random_cases import nonfinite_cutoff_cases, random_cases, scale_poses
 
 pytestmark = pytest.mark.gpu
 
-CASES = random_cases(160, seed=424242) + random_cases(40, seed=777, min_p=0)
+CASES = random_cases(160, seed=424242) + random_cases(40, seed=777, min_p=0) + nonfinite_cutoff_cases()
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c["name"] for c in CASES])
@@ -23,4 +25,5 @@ def test_hip_matches_oracle_random(case, hip, oracle):
     print(f"[random] {case['name']} n={case['n']} os={case['os']} cut={case['cutoff']} P={case['P']}", flush=True)
     got = getattr(hip, case["op"])(*args)
     exp = getattr(oracle, case["op"])(*args)
-    check_outputs(case["op"], got, exp, has_shifts=tensors.get("shifts") is not None, label=case["name"])
+    check_outputs(case["op"], got, exp, has_shifts=tensors.get("shifts") is not None, label=case["name"],
+                  cells=scatter_cells(case["op"], args, oracle))

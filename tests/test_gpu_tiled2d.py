@@ -13,7 +13,7 @@ oversampling factors that leave the tile grid ragged.  Bar: tests/parity.py.
 import pytest
 
 from tests.golden.cases import _case, make_inputs
-from tests.parity import check_outputs
+from tests.parity import check_outputs, scatter_cells
 
 pytestmark = pytest.mark.gpu
 
@@ -50,4 +50,5 @@ def test_tiled2d_matches_oracle(case, hip, oracle):
     print(f"[tiled2d] {case['name']} B={case['B']} B_rot={case['B_rot']}", flush=True)
     got = getattr(hip, case["op"])(*args)
     exp = getattr(oracle, case["op"])(*args)
-    check_outputs(case["op"], got, exp, has_shifts=tensors.get("shifts") is not None, label=case["name"])
+    check_outputs(case["op"], got, exp, has_shifts=tensors.get("shifts") is not None, label=case["name"],
+                  cells=scatter_cells(case["op"], args, oracle))

@@ -9,9 +9,9 @@ import torch
 
 from oracle import oracle as O
 from tests.golden.cases import make_inputs
-from tests.random_cases import random_cases, scale_poses
+from tests.random_cases import nonfinite_cutoff_cases, random_cases, scale_poses
 
-CASES = random_cases(160, seed=424242) + random_cases(40, seed=777, min_p=0)
+CASES = random_cases(160, seed=424242) + random_cases(40, seed=777, min_p=0) + nonfinite_cutoff_cases()
 
 
 @pytest.fixture(scope="module")
@@ -41,3 +41,5 @@ def test_oracle_matches_reference_build(case, ref):
         assert g.shape == e.shape, (k, g.shape, e.shape)
         assert g.dtype == e.dtype, (k, g.dtype, e.dtype)
         assert torch.equal(g, e), f"output {k}: max |d| = {(g - e).abs().max().item():.3e}"
+        if case["name"].startswith("cut"):
+            assert e.numel() == 0 or torch.count_nonzero(e) > 0, f"output {k} is all zero"

@@ -93,9 +93,7 @@ __device__ __forceinline__ void row_span2(const float* R, int r, const float* lo
     }
     c0 = max(0, to_int_clamped(ceilf(l * ts.inv_os - 1e-3f)));
     c1 = min(ts.cmax, to_int_clamped(floorf(h * ts.inv_os + 1e-3f)));
-    const float rem = cut2 - float(r) * float(r);
-    if (empty || rem < 0.f) c1 = -1;
-    else c1 = min(c1, int(sqrtf(rem)) + 1);
+    c1 = empty ? -1 : cap_to_disc(c1, cut2 - float(r) * float(r));
 }
 
 // Per-wave copy of the poses of one batch.

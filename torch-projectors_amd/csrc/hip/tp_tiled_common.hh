@@ -14,6 +14,18 @@ __device__ __forceinline__ int to_int_clamped(float v) {
     return int(v);
 }
 
+// Last column of row r that can lie inside the cutoff disc, applied to a row
+// span [c0, c1]: rem = cut2 - r*r.  A row beyond the disc (rem < 0) is empty.
+// The cap is an optimisation only (every sample is still tested against the
+// mask): it is skipped when rem is not a finite float below 1e16, so a cutoff
+// of +inf, NaN (which masks nothing, as r^2 + c^2 > NaN is false) or beyond
+// any int never reaches an undefined float-to-int conversion.
+__device__ __forceinline__ int cap_to_disc(int c1, float rem) {
+    if (rem < 0.f) return -1;
+    if (rem < 1.0e16f) return min(c1, int(sqrtf(rem)) + 1);
+    return c1;
+}
+
 // Wave-wide inclusive prefix sum / max with DPP row shifts and broadcasts
 // (register-to-register inside the SIMD, no LDS round trip).  Call with
 // every lane active.

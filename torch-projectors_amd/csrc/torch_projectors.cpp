@@ -49,8 +49,32 @@ void check_shift_batch(const optional<Tensor>& shifts, int64_t B, int64_t P, con
     TORCH_CHECK(shifts->size(1) == P, "Number of poses in shifts must match rotations");
 }
 
+// Real-valued inputs against the complex input's dtype, as the reference's two
+// paths accept them.  Rotations are dispatched as float or double
+// (AT_DISPATCH_FLOATING_TYPES, cpu/3d/projection_3d_to_2d_kernels.cpp:126), and
+// weights / grad_weight_rec are read through the rotations' type
+// (cpu/3d/backprojection_2d_to_3d_kernels.cpp:165-169, :388-397).  Complex64
+// calls take the reference's GPU path, which reads rotations, shifts and weights
+// as float (cuda/3d/projection_3d_to_2d_kernels.cu:987-988) and raises for
+// double; complex128 calls fall back to its CPU code, which also takes float
+// rotations: those are widened exactly to double here, the same values the
+// CPU code's promotion gives.
+void check_real_dtypes(c10::ScalarType cplx, const Tensor& rotations, const optional<Tensor>& weights,
+                       const optional<Tensor>& grad_weight_rec = c10::nullopt) {
+    const auto rt = rotations.scalar_type();
+    TORCH_CHECK(rt == at::kFloat || rt == at::kDouble, "Rotations must be float32 or float64, got ", rt);
+    TORCH_CHECK(cplx == at::kComplexDouble || rt == at::kFloat, "A ", cplx,
+                " input needs float32 rotations and shifts (the reference's GPU path reads them as float), got ", rt);
+    if (weights.has_value())
+        TORCH_CHECK(weights->scalar_type() == rt, "Weights must have the rotations' dtype (", rt, "), got ",
+                    weights->scalar_type());
+    if (grad_weight_rec.has_value())
+        TORCH_CHECK(grad_weight_rec->scalar_type() == rt, "grad_weight_rec must have the rotations' dtype (", rt,
+                    "), got ", grad_weight_rec->scalar_type());
+}
+
 // The kernels read every real-valued input in the complex tensor's value
-// type; inputs in another floating type are converted first.
+// type (check_real_dtypes admits only float32 -> float64 widening).
 struct Prep {
     Tensor t;
     const void* ptr() const { return t.defined() ? t.data_ptr() : nullptr; }
@@ -128,6 +152,7 @@ Tensor project_forw(int dim, const Tensor& reconstruction, const Tensor& rotatio
     const bool half = is_half_volume(reconstruction);
     const int dt = half ? TP_F16S : dtype_code(reconstruction);
     const auto cplx = half ? at::kComplexFloat : reconstruction.scalar_type();
+    check_real_dtypes(cplx, rotations, c10::nullopt);
     const auto real = c10::toRealValueType(cplx);
     const Tensor rec = reconstruction.contiguous();
     const Prep rot = prep(rotations, real, dev), sh = prep_opt(shifts, real, dev);
@@ -172,6 +197,7 @@ std::tuple<Tensor, Tensor, Tensor> project_back(int dim, const Tensor& grad_proj
     const Tensor g = grad_projections.contiguous();
     const Tensor rec = half ? reconstruction.to(at::kComplexFloat).contiguous() : reconstruction.contiguous();
     const int dt = dtype_code(rec);
+    check_real_dtypes(rec.scalar_type(), rotations, c10::nullopt);
     const auto real = c10::toRealValueType(rec.scalar_type());
     const Prep rot = prep(rotations, real, dev), sh = prep_opt(shifts, real, dev);
     PoseGrads pg = pose_grads(rotations, shifts, rot, sh);
@@ -217,6 +243,7 @@ std::tuple<Tensor, Tensor> backproject_forw(int dim, const Tensor& projections, 
     const auto dev = projections.device();
     c10::hip::HIPGuardMasqueradingAsCUDA guard(dev);
     const int dt = dtype_code(projections);
+    check_real_dtypes(projections.scalar_type(), rotations, weights);
     const auto real = c10::toRealValueType(projections.scalar_type());
     const Tensor pr = projections.contiguous();
     const Prep rot = prep(rotations, real, dev), sh = prep_opt(shifts, real, dev), w = prep_opt(weights, real, dev);
@@ -283,6 +310,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> backproject_back(
     const auto dev = projections.device();
     c10::hip::HIPGuardMasqueradingAsCUDA guard(dev);
     const int dt = dtype_code(projections);
+    check_real_dtypes(projections.scalar_type(), rotations, weights, grad_weight_rec);
     const auto real = c10::toRealValueType(projections.scalar_type());
     TORCH_CHECK(grad_data_rec.device() == dev, "all tensors must be on the same GPU");
     const Tensor gd = grad_data_rec.contiguous(), pr = projections.contiguous();
