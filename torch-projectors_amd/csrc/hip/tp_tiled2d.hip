@@ -93,7 +93,7 @@ __device__ __forceinline__ void row_span2(const float* R, int r, const float* lo
     }
     c0 = max(0, to_int_clamped(ceilf(l * ts.inv_os - 1e-3f)));
     c1 = min(ts.cmax, to_int_clamped(floorf(h * ts.inv_os + 1e-3f)));
-    c1 = empty ? -1 : cap_to_disc(c1, cut2 - float(r) * float(r));
+    c1 = empty ? -1 : cap_to_disc(c1, float(r), cut2);
 }
 
 // Per-wave copy of the poses of one batch.

@@ -113,7 +113,7 @@ __device__ __forceinline__ void row_span(const float* R, int r, const float* lo,
     }
     c0 = max(0, to_int_clamped(ceilf(l * ts.inv_os - 1e-3f)));
     c1 = min(ts.cmax, to_int_clamped(floorf(h * ts.inv_os + 1e-3f)));
-    c1 = empty ? -1 : cap_to_disc(c1, cut2 - float(r) * float(r));
+    c1 = empty ? -1 : cap_to_disc(c1, float(r), cut2);
 }
 
 // Sample position of pixel (r, c): rotate<3> without its R[k][2] * 0 terms.
@@ -412,19 +412,14 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
         const float* rotb = rot + rb * g.P * 9;
         const Cx<VS>* recb = rec + b * g.vol;
-        auto lds = [&](int d, int r, int c) {
-            const int e = ((d - (td - LO)) * W + (r - (tr - LO))) * W + (c - (tc - LO));
-            if constexpr (kHalfVolume<VS>) return Cx<float>{__half2float(vt[e].re), __half2float(vt[e].im)};
-            else return vt[e];
-        };
         bool loaded = false;
         for (int pbase = it.p0; pbase < it.p1; pbase += CH) {
             const int np = cull_chunk<NT, false, CH>(rotb, it.p1, pbase, lo, hi, lo, hi, plist, &pcount);
             if (np == 0) continue;
             if (!loaded) {
-                // stage the tile and its halo, STAGE loads in flight per lane.  When the staged
-                // box lies on one side of c = 0 and needs no clamping, a cell is a plain wrapped
-                // load (conjugated from the mirrored cell on the c < 0 side).
+                // stage the tile and its halo.  When the staged box lies on one side of c = 0 and
+                // needs no clamping, a cell is a plain wrapped load (conjugated from the mirrored
+                // cell on the c < 0 side); other boxes go through the reference's sampler rules.
                 const int c_lo = tc - LO, c_hi = tc - LO + W - 1, r_lo = tr - LO, r_hi = tr - LO + W - 1,
                           d_lo = td - LO, d_hi = td - LO + WD - 1, hn = N / 2;
                 const bool plain_pos = c_lo >= 0 && c_hi <= H - 1 && r_lo >= -hn + 1 && r_hi <= hn &&
@@ -533,18 +528,28 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                         const int fxc = int(floorf(x[0])), fxr = int(floorf(x[1])), fxd = int(floorf(x[2]));
                         if (fxc < tc || fxc >= tc + L || fxr < tr || fxr >= tr + L || fxd < td || fxd >= td + LD)
                             continue;
-                        const int i = rr >= 0 ? rr : rr + g.n;
+                        // staged cell of the tap at floor(x); the interpolation reads its taps at
+                        // constant offsets from it (the interpolators split x the same way)
+                        const unsigned eb = __umul24(__umul24(unsigned(fxd - (td - LO)), unsigned(W)) + unsigned(fxr - (tr - LO)),
+                                                     unsigned(W)) + unsigned(fxc - (tc - LO));
+                        auto lds = [&](int d, int r, int c) {
+                            const unsigned e = eb + unsigned(((d - fxd) * W + (r - fxr)) * W + (c - fxc));
+                            if constexpr (kHalfVolume<VS>) return Cx<float>{__half2float(vt[e].re), __half2float(vt[e].im)};
+                            else return vt[e];
+                        };
+                        // pixel offset in the pose's projection (i, hp < 2^24)
+                        const int pix = int(__umul24(unsigned(rr >= 0 ? rr : rr + g.n), unsigned(g.hp))) + cc;
                         if constexpr (GMODE == 0) {
                             Cx<float> v = CUBIC ? cubic3<float, false, false>(lds, x[2], x[1], x[0]).v
                                                 : lerp3<float, false, false>(lds, x[2], x[1], x[0]).v;
                             if (shifts) v = cmul(v, phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k));
-                            out[sd.base + i * g.hp + cc] = v;
+                            out[sd.base + pix] = v;
                         } else if constexpr (GMODE == 2) {
                             Interp<float> ip;
                             if constexpr (CUBIC && GRADS) ip = cubic3_grads<true>(lds, x[2], x[1], x[0]);
                             else if constexpr (CUBIC) ip = cubic3<float, false, false>(lds, x[2], x[1], x[0]);
                             else ip = lerp3<float, GRADS, false>(lds, x[2], x[1], x[0]);
-                            const int64_t pidx = sd.base + i * g.hp + cc;
+                            const int64_t pidx = sd.base + pix;
                             const Cx<float> ph = shifts ? phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k)
                                                         : Cx<float>{1.f, 0.f};
                             out[pidx] = shifts ? cmul(ip.v, ph) : ip.v;
@@ -591,7 +596,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                         } else {
                             const Interp<float> ip = CUBIC ? cubic3_grads<false>(lds, x[2], x[1], x[0])
                                                            : lerp3<float, true, false>(lds, x[2], x[1], x[0]);
-                            const Cx<float> g0 = gsrc[sd.base + i * g.hp + cc];
+                            const Cx<float> g0 = gsrc[sd.base + pix];
                             const Cx<float> ph = shifts ? phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k)
                                                         : Cx<float>{1.f, 0.f};
                             if (grot) {
@@ -849,9 +854,11 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                         const int excl = incl - cnt;
                         const int total = __builtin_amdgcn_readlane(incl, 63);
                         int carry = 0;
-                        // sample e0 + lane of this row block: owner lane, pixel, validity, and its loads
-                        auto fetch_sample = [&](int e0, int& rr, int& cc, int& sl, bool& ok, Cx<float>& v,
-                                                float& wv) {
+                        // sample e0 + lane of this row block: owner lane, pixel, validity and the
+                        // element to load (element 0 for lanes without a sample, so that every
+                        // load is issued on every path: a load under a branch makes the compiler
+                        // wait for it before the previous window's taps)
+                        auto locate = [&](int e0, int& rr, int& cc, int& sl, bool& ok, int64_t& pidx) {
                             const int e = e0 + lane;
                             const int lw = window_owner(cnt, excl, e0, carry, marks[wave]);
                             rr = __shfl(r, lw, 64);
@@ -861,23 +868,23 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                             const Slot& sd = slots[wave][sl];
                             ok = ok && !filtered(float(rr), float(cc), cut2) &&
                                  !(cc == 0 && (rr == g.n / 2 || rr < 0));  // Friedel half of x = 0
-                            const int i = rr >= 0 ? rr : rr + g.n;
-                            const int64_t pidx = sd.base + i * g.hp + cc;
-                            v = ok ? src[pidx] : Cx<float>{0.f, 0.f};
-                            wv = (WEIGHTS && ok) ? weights[pidx] : 0.f;
+                            const int pix = int(__umul24(unsigned(rr >= 0 ? rr : rr + g.n), unsigned(g.hp))) + cc;
+                            pidx = ok ? sd.base + pix : 0;
                         };
                         int rr, cc, sl;
                         bool ok;
-                        Cx<float> v;
-                        float wv;
-                        fetch_sample(0, rr, cc, sl, ok, v, wv);
+                        int64_t pidx;
+                        locate(0, rr, cc, sl, ok, pidx);
+                        Cx<float> v = src[pidx];
+                        float wv = WEIGHTS ? weights[pidx] : 0.f;
                         for (int e0 = 0; e0 < total; e0 += 64) {
                             // the next sample's loads are in flight while this one is spread
                             int rr2 = 0, cc2 = 0, sl2 = 0;
                             bool ok2 = false;
-                            Cx<float> v2 = {0.f, 0.f};
-                            float wv2 = 0.f;
-                            if (e0 + 64 < total) fetch_sample(e0 + 64, rr2, cc2, sl2, ok2, v2, wv2);
+                            int64_t pidx2 = 0;
+                            if (e0 + 64 < total) locate(e0 + 64, rr2, cc2, sl2, ok2, pidx2);
+                            const Cx<float> v2 = src[pidx2];
+                            const float wv2 = WEIGHTS ? weights[pidx2] : 0.f;
                             if (ok)
                                 scatter_sample<CUBIC, MODE, WEIGHTS, OSX>(g, slots[wave][sl], rr, cc, v, wv,
                                                                      shifts != nullptr, pass == 1, tm, acc_re,

@@ -15,14 +15,17 @@ __device__ __forceinline__ int to_int_clamped(float v) {
 }
 
 // Last column of row r that can lie inside the cutoff disc, applied to a row
-// span [c0, c1]: rem = cut2 - r*r.  A row beyond the disc (rem < 0) is empty.
-// The cap is an optimisation only (every sample is still tested against the
-// mask): it is skipped when rem is not a finite float below 1e16, so a cutoff
-// of +inf, NaN (which masks nothing, as r^2 + c^2 > NaN is false) or beyond
-// any int never reaches an undefined float-to-int conversion.
-__device__ __forceinline__ int cap_to_disc(int c1, float rem) {
+// span [c0, c1]: a row beyond the disc (cut2 - r^2 < 0) is empty, otherwise
+// the span ends at most one column past the disc (the hardware square root is
+// within an ulp, and the +1 covers it).  The cap is an optimisation only:
+// every sample is still tested against the mask.  It is skipped when
+// cut2 - r^2 is not a finite float below 1e16, so a cutoff of +inf, NaN (which
+// masks nothing, as r^2 + c^2 > NaN is false) or beyond any int never reaches
+// an undefined float-to-int conversion.
+__device__ __forceinline__ int cap_to_disc(int c1, float fr, float cut2) {
+    const float rem = cut2 - fr * fr;
     if (rem < 0.f) return -1;
-    if (rem < 1.0e16f) return min(c1, int(sqrtf(rem)) + 1);
+    if (rem < 1.0e16f) return min(c1, int(__builtin_amdgcn_sqrtf(rem)) + 1);
     return c1;
 }
 
