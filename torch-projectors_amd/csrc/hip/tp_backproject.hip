@@ -70,7 +70,7 @@ __global__ __launch_bounds__(kBlock) void k_backproject_forw(Geom g, const Cx<T>
     }
 }
 
-// The poses of an fp32 backprojection that are not rotations (the tiled
+// The poses of an fp32 backprojection that the tiled kernels do not take (the tiled
 // scatter has accumulated the others).  One block per pose.
 template <int DIM, bool CUBIC, bool WEIGHTS>
 __global__ __launch_bounds__(kBlock) void k_backproject_forw_rest(Geom g, const Cx<float>* __restrict__ proj,
@@ -84,7 +84,7 @@ __global__ __launch_bounds__(kBlock) void k_backproject_forw_rest(Geom g, const 
     for (int64_t bp = blockIdx.x; bp < g.B * g.P; bp += gridDim.x) {
         const int64_t b = bp / g.P, p = bp - b * g.P;
         const float* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * RS;
-        if (pose_is_rotation_d<DIM>(R)) continue;
+        if (pose_tiled_d<DIM>(R)) continue;
         const float* S = shifts ? shifts + ((g.B_shift == 1 ? 0 : b) * g.P + p) * 2 : nullptr;
         for (int q = threadIdx.x; q < g.rect; q += kBlock) {
             int i, j;
@@ -104,7 +104,7 @@ __global__ __launch_bounds__(kBlock) void k_backproject_forw_rest(Geom g, const 
 // Friedel flip without conjugation, zero outside); rotation and shift
 // gradients pair the conj-phased projection with the spatial derivative /
 // value of grad_data_rec (backprojection_2d_to_3d_kernels.cpp:451-567).
-// REST (fp32): poses that are rotations were computed by the tiled gather
+// REST (fp32): tiled poses (pose_tiled_d) were computed by the tiled gather
 // into zero-filled outputs and are skipped here.
 template <int DIM, typename T, bool CUBIC, bool WG, bool ROT, bool SHIFT, bool REST>
 __global__ __launch_bounds__(kBlock) void k_backproject_back(Geom g, const Cx<T>* __restrict__ gdata,
@@ -116,12 +116,12 @@ __global__ __launch_bounds__(kBlock) void k_backproject_back(Geom g, const Cx<T>
     constexpr int K = RS + 2;
     __shared__ T red[kBlock / 64][K];
     const T cut2 = T(g.cut2);
-    // REST: one pose per outer step, skipped at once when it is a rotation
+    // REST: one pose per outer step, skipped at once when it is a tiled pose
     const int64_t outer_n = REST ? g.B * g.P : g.work;
     for (int64_t outer = blockIdx.x; outer < outer_n; outer += gridDim.x) {
       if constexpr (REST) {
         const int64_t b0 = outer / g.P;
-        if (pose_is_rotation_d<DIM>(rot + ((g.B_rot == 1 ? 0 : b0) * g.P + (outer - b0 * g.P)) * RS)) continue;
+        if (pose_tiled_d<DIM>(rot + ((g.B_rot == 1 ? 0 : b0) * g.P + (outer - b0 * g.P)) * RS)) continue;
       }
       for (int ch = 0; ch < (REST ? g.chunks : 1); ++ch) {
         const int64_t w = REST ? outer * g.chunks + ch : outer;

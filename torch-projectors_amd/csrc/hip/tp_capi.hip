@@ -4,10 +4,17 @@
 // reference (validate_projection_inputs, projection_utils.h:23-48, and the
 // per-op TORCH_CHECKs), derives the launch geometry, zero-fills the outputs
 // that are accumulated, and enqueues the kernels on the caller's stream.
-// Nothing is synchronised and nothing is allocated.
+// Nothing is synchronised.  The only memory besides the caller's is a
+// 256-byte scratch area per (device, stream) that the tiled kernels' calls
+// use (the reach of their poses), allocated by the first such call on that
+// stream and kept for the life of the process.
 #include <algorithm>
 #include <cmath>
+#include <map>
+#include <memory>
+#include <mutex>
 #include <string>
+#include <utility>
 
 #include "../../../include/torch_projectors_hip.h"
 #include "tp_launch.hh"
@@ -119,13 +126,23 @@ tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
     const double grid_r = std::sqrt(2.0) * double(g.n / 2 + 1);
     double cutr = g.cut2 >= 0.0 ? std::sqrt(g.cut2) : grid_r;
     if (!std::isfinite(cutr) || cutr > grid_r) cutr = grid_r;
-    const double rho = g.os * cutr * 1.001 + 1.0;
-    const int half_tiles = int(std::ceil((rho + 2.0) / L));
+    // the grids reach the samples of every tiled pose (singular values up to kScaleMax);
+    // launch_pose_reach gives each call the radius its own poses reach
+    const double rho_unit = g.os * cutr * 1.001;
+    const double rho = rho_unit * tp::kScaleMax + 1.0;
+    // forward grids: one for unit-scale poses (launched one tile per workgroup), one for
+    // enlarging poses (visited after it); tiles of both are aligned
+    const int half_tiles = int(std::ceil((rho_unit + 3.0) / L));
     ts.nt = 2 * half_tiles;
     ts.org = -half_tiles * L;
-    const int half_tiles_d = int(std::ceil((rho + 2.0) / tp::kTileEdgeD));
+    const int half_tiles_d = int(std::ceil((rho_unit + 3.0) / tp::kTileEdgeD));
     ts.ntfd = 2 * half_tiles_d;
     ts.orgd = -half_tiles_d * tp::kTileEdgeD;
+    const int half2 = int(std::ceil((rho + 2.0) / L)), half2_d = int(std::ceil((rho + 2.0) / tp::kTileEdgeD));
+    ts.nt2 = 2 * half2;
+    ts.org2 = -half2 * L;
+    ts.ntfd2 = 2 * half2_d;
+    ts.orgd2 = -half2_d * tp::kTileEdgeD;
     const int half = g.N / 2;
     ts.ntd = (g.N + tp::kScTD - 1) / tp::kScTD;
     ts.ntr = (g.N + tp::kScTR - 1) / tp::kScTR;
@@ -149,6 +166,7 @@ tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
     ts.prange = int((g.P + ts.ksplit - 1) / ts.ksplit);
     if (ts.ksplit == 1) ts.fc1 = ts.fc0 = ts.fd1 = ts.fd0 = ts.sd1 = ts.sd0 = ts.sr1 = ts.sr0 = ts.sc1 = 0;  // nothing to split
     ts.rho = float(rho);
+    ts.rho_unit = float(rho_unit);
     ts.os = float(g.os);
     ts.inv_os = float(1.0 / g.os);
     ts.os_exact = double(float(g.os)) == g.os;
@@ -177,7 +195,8 @@ tp::TileSpec2 tile_spec2(const tp::Geom& g, bool cubic) {
     const double grid_r = std::sqrt(2.0) * double(g.n / 2 + 1);
     double cutr = g.cut2 >= 0.0 ? std::sqrt(g.cut2) : grid_r;
     if (!std::isfinite(cutr) || cutr > grid_r) cutr = grid_r;
-    const double rho = g.os * cutr * 1.001 + 1.0;
+    const double rho_unit = g.os * cutr * 1.001;
+    const double rho = rho_unit * tp::kScaleMax + 1.0;
     // tiles whose cells a tap can reach: |r| and c within rho plus the stencil
     const double reach = std::min(rho + 3.0, double(g.N));
     const int half = g.N / 2;
@@ -188,12 +207,17 @@ tp::TileSpec2 tile_spec2(const tp::Geom& g, bool cubic) {
     ts.nc = std::min(ntc, int(std::floor(reach / TC)) + 1);
     // Every pose reaches every tile of the disc: split the poses into ranges
     // until there are a few thousand work items, keeping >= 128 poses a range.
-    const int64_t tiles = g.B * int64_t(ts.nr) * ts.nc;
+    // (Counted over the tiles that unit-scale poses reach: the others are only
+    // worked on by calls with enlarging poses.)
+    const double reach_unit = std::min(rho_unit + 4.0, double(g.N));
+    const int64_t tiles = g.B * int64_t(std::min(ntr, int(std::floor(2.0 * reach_unit / TR)) + 2)) *
+                          std::min(ntc, int(std::floor(reach_unit / TC)) + 1);
     const int64_t want = tiles > 0 ? (4096 + tiles - 1) / tiles : 1;
     const int64_t most = std::max<int64_t>(1, g.P / 128);
     ts.ksplit = int(std::max<int64_t>(1, std::min(want, most)));
     ts.prange = int((g.P + ts.ksplit - 1) / ts.ksplit);
     ts.rho = float(rho);
+    ts.rho_unit = float(rho_unit);
     ts.os = float(g.os);
     ts.inv_os = float(1.0 / g.os);
     ts.smax = float(g.os * (g.n + 2));
@@ -211,7 +235,8 @@ tp::TileSpec2 tile_spec2(const tp::Geom& g, bool cubic) {
     const int half_g = int(std::ceil((rho + 2.0) / GT));
     ts.gnt = 2 * half_g;
     ts.gorg = -half_g * GT;
-    const int64_t gtiles = g.B * int64_t(ts.gnt) * ts.gnt;
+    const int64_t gunit = 2 * int64_t(std::ceil((rho_unit + 3.0) / GT));
+    const int64_t gtiles = g.B * std::min<int64_t>(ts.gnt, gunit) * std::min<int64_t>(ts.gnt, gunit);
     const int64_t gwant = gtiles > 0 ? (4096 + gtiles - 1) / gtiles : 1;
     ts.gksplit = int(std::max<int64_t>(1, std::min(gwant, most)));
     ts.gprange = int((g.P + ts.gksplit - 1) / ts.gksplit);
@@ -243,6 +268,47 @@ int need(const void* p, const char* name) {
 
 int launched(hipError_t e, const char* what) { return e == hipSuccess ? TP_OK : hip_fail(e, what); }
 
+// Scratch of the calls on one (device, stream): the reach word of
+// tp::launch_pose_reach.  Calls on one stream run in order on the GPU, so they
+// share it; `busy` is held while one call enqueues its kernels, so that calls
+// from several host threads on one stream do not interleave them.
+struct StreamScratch {
+    float* p = nullptr;
+    std::mutex busy;
+};
+std::mutex g_scratch_mu;
+std::map<std::pair<int, hipStream_t>, std::unique_ptr<StreamScratch>> g_scratch;
+
+struct CallScratch {
+    float* p = nullptr;
+    std::unique_lock<std::mutex> hold;
+    int get(hipStream_t st) {
+        if (p) return TP_OK;  // a call takes it once
+        int dev = 0;
+        TP_TRY(launched(hipGetDevice(&dev), "hipGetDevice"));
+        StreamScratch* e;
+        {
+            std::lock_guard<std::mutex> lk(g_scratch_mu);
+            std::unique_ptr<StreamScratch>& slot = g_scratch[{dev, st}];
+            if (!slot) {
+                std::unique_ptr<StreamScratch> fresh(new StreamScratch);
+                TP_TRY(launched(hipMalloc(reinterpret_cast<void**>(&fresh->p), 256), "scratch allocation"));
+                slot = std::move(fresh);
+            }
+            e = slot.get();
+        }
+        hold = std::unique_lock<std::mutex>(e->busy);
+        p = e->p;
+        return TP_OK;
+    }
+};
+
+// The reach of the call's tiled poses into the scratch word (the tiled kernels skip tiles beyond it).
+int pose_reach(int dim, const tp::Geom& g, const void* rot, float rho_unit, CallScratch& sc, hipStream_t s) {
+    TP_TRY(sc.get(s));
+    return launched(tp::launch_pose_reach(dim, g.B_rot * g.P, rot, rho_unit, sc.p, s), "pose reach launch");
+}
+
 // TP_F16S: the volume is stored as complex half; it is widened exactly to
 // fp32 on load and everything else (poses, arithmetic, projections) is the
 // TP_F32 path.
@@ -267,9 +333,11 @@ int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int6
     TP_TRY(need(out, "projections"));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool cubic = interp == TP_CUBIC;
+    CallScratch sc;
     if (use_tiles(dim, dt, os, n)) {
-        TP_TRY(launched(tp::launch_project3_forw_tiled(cubic, g, tile_spec(g, cubic), rec, rot, shifts, out, s,
-                                                       rec_half),
+        const tp::TileSpec ts = tile_spec(g, cubic);
+        TP_TRY(pose_reach(3, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_project3_forw_tiled(cubic, g, ts, rec, rot, shifts, out, sc.p, s, rec_half),
                         "tiled projection launch"));
         return launched(tp::launch_project_forw(dim, kdt, cubic, g, rec, rot, shifts, out, s, true),
                         "projection launch");
@@ -278,8 +346,10 @@ int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int6
         // zero-fill first: the tiled gather writes the active pixels of rotation poses, the
         // rest kernel the other poses
         TP_TRY(zero(out, cx_words(dt, g.B * g.P * int64_t(g.npix)), s));
-        TP_TRY(launched(tp::launch_gather2_tiled(cubic, 0, g, tile_spec2(g, cubic), rec, nullptr, rot, shifts, out,
-                                                 nullptr, nullptr, nullptr, nullptr, s, rec_half),
+        const tp::TileSpec2 ts = tile_spec2(g, cubic);
+        TP_TRY(pose_reach(2, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_gather2_tiled(cubic, 0, g, ts, rec, nullptr, rot, shifts, out, nullptr, nullptr,
+                                                 nullptr, nullptr, sc.p, s, rec_half),
                         "tiled projection launch"));
         return launched(tp::launch_project_forw(dim, kdt, cubic, g, rec, rot, shifts, out, s, true),
                         "projection launch");
@@ -312,19 +382,24 @@ int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, in
     TP_TRY(need(gproj, "grad_projections"));
     TP_TRY(need(rec, "reconstruction"));
     TP_TRY(need(rot, "rotations"));
+    CallScratch sc;
     if (tiles) {
         const tp::TileSpec ts = tile_spec(g, cubic);
-        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, s),
+        TP_TRY(pose_reach(3, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, sc.p,
+                                                  s),
                         "tiled reconstruction-gradient launch"));
-        TP_TRY(launched(tp::launch_grads3_tiled(cubic, g, ts, gproj, rec, rot, shifts, grot, gshift, s),
+        TP_TRY(launched(tp::launch_grads3_tiled(cubic, g, ts, gproj, rec, rot, shifts, grot, gshift, sc.p, s),
                         "tiled rotation/shift-gradient launch"));
     }
     if (tiles2) {
         const tp::TileSpec2 ts = tile_spec2(g, cubic);
-        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, s),
+        TP_TRY(pose_reach(2, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, sc.p,
+                                                  s),
                         "tiled reconstruction-gradient launch"));
         TP_TRY(launched(tp::launch_gather2_tiled(cubic, 1, g, ts, rec, nullptr, rot, shifts, nullptr, nullptr, gproj,
-                                                 grot, gshift, s),
+                                                 grot, gshift, sc.p, s),
                         "tiled rotation/shift-gradient launch"));
     }
     return launched(tp::launch_project_back(dim, dtype, cubic, g, gproj, rec, rot, shifts, grec, grot, gshift, s,
@@ -358,14 +433,19 @@ int backproject_forw(int dim, int dtype, const void* proj, int64_t B, int64_t P,
     if (g.work == 0) return TP_OK;
     TP_TRY(need(proj, "projections"));
     TP_TRY(need(rot, "rotations"));
-    if (tiles)
-        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 0, g, tile_spec(g, cubic), proj, weights, rot, shifts, data, wrec,
-                                                  s),
+    CallScratch sc;
+    if (tiles) {
+        const tp::TileSpec ts = tile_spec(g, cubic);
+        TP_TRY(pose_reach(3, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 0, g, ts, proj, weights, rot, shifts, data, wrec, sc.p, s),
                         "tiled backprojection launch"));
-    if (tiles2)
-        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 0, g, tile_spec2(g, cubic), proj, weights, rot, shifts, data,
-                                                  wrec, s),
+    }
+    if (tiles2) {
+        const tp::TileSpec2 ts = tile_spec2(g, cubic);
+        TP_TRY(pose_reach(2, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 0, g, ts, proj, weights, rot, shifts, data, wrec, sc.p, s),
                         "tiled backprojection launch"));
+    }
     return launched(
         tp::launch_backproject_forw(dim, dtype, cubic, g, proj, weights, rot, shifts, data, wrec, s, tiles || tiles2),
         "backprojection launch");
@@ -400,14 +480,21 @@ int backproject_back(int dim, int dtype, const void* gdata, const void* gw, int6
         TP_TRY(zero(gproj, cx_words(dtype, g.B * g.P * int64_t(g.npix)), s));
         TP_TRY(zero(gweights, re_words(dtype, g.B * g.P * int64_t(g.npix)), s));
     }
-    if (tiles)
-        TP_TRY(launched(tp::launch_bpback3_tiled(cubic, g, tile_spec(g, cubic), gdata, gw, proj, rot, shifts, gproj,
-                                                 gweights, grot, gshift, s),
+    CallScratch sc;
+    if (tiles) {
+        const tp::TileSpec ts = tile_spec(g, cubic);
+        TP_TRY(pose_reach(3, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_bpback3_tiled(cubic, g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
+                                                 gshift, sc.p, s),
                         "tiled backprojection backward launch"));
-    if (tiles2)
-        TP_TRY(launched(tp::launch_gather2_tiled(cubic, 2, g, tile_spec2(g, cubic), gdata, gw, rot, shifts, gproj,
-                                                 (gw && gweights) ? gweights : nullptr, proj, grot, gshift, s),
+    }
+    if (tiles2) {
+        const tp::TileSpec2 ts = tile_spec2(g, cubic);
+        TP_TRY(pose_reach(2, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_gather2_tiled(cubic, 2, g, ts, gdata, gw, rot, shifts, gproj,
+                                                 (gw && gweights) ? gweights : nullptr, proj, grot, gshift, sc.p, s),
                         "tiled backprojection backward launch"));
+    }
     return launched(tp::launch_backproject_back(dim, dtype, cubic, g, gdata, gw, proj, rot, shifts, gproj, gweights,
                                                 grot, gshift, s, tiles2 || tiles),
                     "backprojection backward launch");

@@ -515,29 +515,78 @@ __device__ __forceinline__ Cx<float> phase_hw(float r, float c, float s0, float 
 }
 
 // ---------------------------------------------------------------- pose classes
-// The tiled 3D kernels enumerate the samples of a pose through its slice
-// plane, which needs the first two rotation columns orthonormal (every
-// rotation matrix).  Other matrices (scaled, sheared, degenerate) take the
-// per-pixel kernels.  Both sides evaluate this same predicate.  Rotations
-// stored in fp32 are orthonormal to a few 1e-7; the tiled kernels' sample
-// bounds allow for kRotationTol (tp_launch.hh).
-__device__ __forceinline__ bool pose_is_rotation(const float* __restrict__ R) {
-    const float aa = R[0] * R[0] + R[3] * R[3] + R[6] * R[6];
-    const float bb = R[1] * R[1] + R[4] * R[4] + R[7] * R[7];
-    const float ab = R[0] * R[1] + R[3] * R[4] + R[6] * R[7];
-    return fabsf(aa - 1.0f) <= kRotationTol && fabsf(bb - 1.0f) <= kRotationTol && fabsf(ab) <= kRotationTol;
+// A sample of pixel (r, c) lies at x = sc a + sr b, with a and b the first two
+// columns of the pose matrix (3D) or its two columns (2D).  The tiled kernels
+// enumerate a pose's samples through the plane (3D) or the grid (2D) that a
+// and b span, which works for every matrix whose Gram matrix
+// G = [[a.a, a.b], [a.b, b.b]] has both eigenvalues (the squared singular
+// values) in [kScaleMin^2, kScaleMax^2] (tp_launch.hh): rotations, and scaled
+// or sheared matrices such as magnification corrections.  Other matrices
+// (degenerate ones, strong scalings) take the per-pixel kernels.  Both
+// families evaluate this same predicate, with multiplies and adds only, so
+// every pose is handled by exactly one of them.
+struct PoseGram {
+    float aa, bb, ab;
+};
+__device__ __forceinline__ PoseGram pose_gram3(const float* __restrict__ R) {
+    return {R[0] * R[0] + R[3] * R[3] + R[6] * R[6], R[1] * R[1] + R[4] * R[4] + R[7] * R[7],
+            R[0] * R[1] + R[3] * R[4] + R[6] * R[7]};
+}
+// 2D: row-major 2x2, columns (R[0], R[2]) and (R[1], R[3]).
+__device__ __forceinline__ PoseGram pose_gram2(const float* __restrict__ R) {
+    return {R[0] * R[0] + R[2] * R[2], R[1] * R[1] + R[3] * R[3], R[0] * R[1] + R[2] * R[3]};
+}
+// Both eigenvalues of G in [lo, hi]: the characteristic polynomial
+// p(t) = t^2 - tr t + det is >= 0 at lo and at hi, and its vertex tr/2 lies
+// between them.  (NaN matrices fail every comparison: per-pixel kernels.)
+__device__ __forceinline__ bool gram_tiled(PoseGram g) {
+    constexpr float lo = kScaleMin * kScaleMin, hi = kScaleMax * kScaleMax;
+    const float tr = g.aa + g.bb, det = g.aa * g.bb - g.ab * g.ab;
+    const float plo = (lo - tr) * lo + det, phi = (hi - tr) * hi + det;
+    return plo >= 0.f && phi >= 0.f && tr >= 2.f * lo && tr <= 2.f * hi;
+}
+// Columns orthonormal to kRotationTol: a rotation (which gram_tiled accepts
+// with a wide margin; testing it first spares rotations the other tests).
+__device__ __forceinline__ bool gram_is_rotation(PoseGram g) {
+    return fabsf(g.aa - 1.0f) <= kRotationTol && fabsf(g.bb - 1.0f) <= kRotationTol && fabsf(g.ab) <= kRotationTol;
+}
+// The class test of both kernel families.
+__device__ __forceinline__ bool gram_takes_tiles(PoseGram g) { return gram_is_rotation(g) || gram_tiled(g); }
+__device__ __forceinline__ bool pose_tiled3(const float* __restrict__ R) { return gram_takes_tiles(pose_gram3(R)); }
+__device__ __forceinline__ bool pose_tiled2(const float* __restrict__ R) { return gram_takes_tiles(pose_gram2(R)); }
+template <int DIM> __device__ __forceinline__ bool pose_tiled_d(const float* __restrict__ R) {
+    if constexpr (DIM == 2) return pose_tiled2(R);
+    else return pose_tiled3(R);
+}
+// Largest singular value of a tiled pose (an upper bound): the root of the
+// larger eigenvalue of G, slightly widened.
+__device__ __forceinline__ float gram_smax(PoseGram g) {
+    const float h = 0.5f * (g.aa - g.bb);
+    const float lmax = 0.5f * (g.aa + g.bb) + sqrtf(h * h + g.ab * g.ab);
+    return sqrtf(lmax) * 1.000001f;
 }
 
-// The same for a 2D pose matrix (row-major 2x2, columns (R[0], R[2]) and (R[1], R[3])).
-__device__ __forceinline__ bool pose_is_rotation2(const float* __restrict__ R) {
-    const float aa = R[0] * R[0] + R[2] * R[2];
-    const float bb = R[1] * R[1] + R[3] * R[3];
-    const float ab = R[0] * R[1] + R[2] * R[3];
-    return fabsf(aa - 1.0f) <= kRotationTol && fabsf(bb - 1.0f) <= kRotationTol && fabsf(ab) <= kRotationTol;
+// Dual basis of a tiled pose that is not a rotation: the vectors as, bs with
+// sc = as . x and sr = bs . x for every x = sc a + sr b of the pose's plane
+// (3D, N = 3) or grid (2D, N = 2), i.e. the rows of G^-1 [a b]^T.  A rotation
+// (a and b orthonormal to kRotationTol) uses its columns instead; the bounds
+// built on them carry a slack that covers that tolerance.
+template <int N>
+__device__ __forceinline__ void pose_dual(const float* a, const float* b, PoseGram g, float* as, float* bs) {
+    const float inv = __builtin_amdgcn_rcpf(g.aa * g.bb - g.ab * g.ab);  // det >= kScaleMin^4
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        as[k] = (g.bb * a[k] - g.ab * b[k]) * inv;
+        bs[k] = (g.aa * b[k] - g.ab * a[k]) * inv;
+    }
 }
-template <int DIM> __device__ __forceinline__ bool pose_is_rotation_d(const float* __restrict__ R) {
-    if constexpr (DIM == 2) return pose_is_rotation2(R);
-    else return pose_is_rotation(R);
+__device__ __forceinline__ void pose_dual3(const float* __restrict__ R, PoseGram g, float* as, float* bs) {
+    const float a[3] = {R[0], R[3], R[6]}, b[3] = {R[1], R[4], R[7]};
+    pose_dual<3>(a, b, g, as, bs);
+}
+__device__ __forceinline__ void pose_dual2(const float* __restrict__ R, PoseGram g, float* as, float* bs) {
+    const float a[2] = {R[0], R[2]}, b[2] = {R[1], R[3]};
+    pose_dual<2>(a, b, g, as, bs);
 }
 
 // ---------------------------------------------------------------- atomics

@@ -57,9 +57,9 @@ __global__ __launch_bounds__(kBlock) void k_project_forw(Geom g, const Cx<VS>* _
 }
 
 // Completes the fp32 forward after the tiled kernel, which has written the
-// active pixels of rotation poses: zeros on masked pixels, and every pixel of
+// active pixels of tiled poses: zeros on masked pixels, and every pixel of
 // the other poses.  One block per pose.  ZEROED: the output was zero-filled
-// first, so rotation poses are done.
+// first, so tiled poses are done.
 template <int DIM, bool CUBIC, bool ZEROED, typename VS = float>
 __global__ __launch_bounds__(kBlock) void k_project_forw_rest(Geom g, const Cx<VS>* __restrict__ rec,
                                                               const float* __restrict__ rot,
@@ -71,7 +71,7 @@ __global__ __launch_bounds__(kBlock) void k_project_forw_rest(Geom g, const Cx<V
         const int64_t b = bp / g.P, p = bp - b * g.P;
         const float* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * RS;
         const float* S = shifts ? shifts + ((g.B_shift == 1 ? 0 : b) * g.P + p) * 2 : nullptr;
-        const bool tiled = pose_is_rotation_d<DIM>(R);
+        const bool tiled = pose_tiled_d<DIM>(R);
         if (ZEROED && tiled) continue;  // block-uniform
         Cx<float>* outp = out + bp * g.npix;
         // one row per wave, lanes along the row (no per-pixel division)
@@ -92,9 +92,9 @@ __global__ __launch_bounds__(kBlock) void k_project_forw_rest(Geom g, const Cx<V
 // with out-of-range taps dropped and no x = 0 mirror
 // (projection_utils.h:336-362, 414-443).  Rotation and shift gradients are
 // per-pose sums, reduced across the block before one atomic per component.
-// REST (fp32) 1: the reconstruction gradient of rotation poses comes from the
+// REST (fp32) 1: the reconstruction gradient of tiled poses comes from the
 // tiled scatter; only the other poses are scattered here.  REST 2: the tiled
-// kernels also give the rotation/shift gradients of rotation poses, which are
+// kernels also give the rotation/shift gradients of tiled poses, which are
 // skipped here entirely.
 template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT, int REST>
 __global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __restrict__ gproj,
@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __
       bool scatter = true;
       if constexpr (REST != 0) {
         const int64_t b0 = outer / g.P;
-        scatter = !pose_is_rotation_d<DIM>(rot + ((g.B_rot == 1 ? 0 : b0) * g.P + (outer - b0 * g.P)) * RS);
+        scatter = !pose_tiled_d<DIM>(rot + ((g.B_rot == 1 ? 0 : b0) * g.P + (outer - b0 * g.P)) * RS);
         if (!scatter && (REST == 2 || (!ROT && !SHIFT))) continue;  // block-uniform
       }
       for (int ch = 0; ch < (REST != 0 ? g.chunks : 1); ++ch) {

@@ -20,8 +20,11 @@
 // range).  The x = 0 Hermitian completion of the backprojection is applied
 // afterwards by k_mirror2_x0.
 //
-// Only poses whose matrix is orthonormal (pose_is_rotation2) take this path;
-// the per-pixel kernels scatter the others.
+// Poses whose 2x2 matrix has singular values in [kScaleMin, kScaleMax]
+// (pose_tiled2: rotations, and scaled or sheared matrices) take this path;
+// the per-pixel kernels scatter the others.  A sample x = R (sc, sr) of such
+// a pose has sc = as . x and sr = bs . x with the dual basis (the rows of
+// R^-1), which bounds the rows and the half plane sc >= 0 that reach a box.
 #include <type_traits>
 
 #include "tp_device.hh"
@@ -37,7 +40,8 @@ constexpr int kThreads = 256;
 constexpr int kRun = 128;         // XCD run length (items)
 constexpr int kChunk2 = 512;      // poses culled per phase
 constexpr int kInFlight = 2;      // rotations loaded together per lane in the cull
-constexpr double kPrivOs = 1.5;   // scatters from this oversampling on use wave-private accumulators
+constexpr double kPrivOs = 1.5;   // scatters whose samples are this far apart (os * kScaleMin) use
+                                  // wave-private accumulators
 static_assert((TC & (TC - 1)) == 0, "tile width must be a power of two");
 static_assert(kChunk2 <= 65535, "pose index must fit the list entries");
 
@@ -48,21 +52,38 @@ __device__ __forceinline__ void rotate_pix(const float* __restrict__ R, float r,
     x[1] = R[2] * sc + R[3] * sr;
 }
 
-// Samples have sc >= 0, i.e. x . a >= 0 for a = (R[0], R[2]): does the box
-// reach that half plane?
-__device__ __forceinline__ bool half_plane_hits2(const float* R, const float* lo, const float* hi) {
-    const float a0 = R[0], a1 = R[2];
-    const float u = (a0 >= 0.f ? a0 * hi[0] : a0 * lo[0]) + (a1 >= 0.f ? a1 * hi[1] : a1 * lo[1]);
+// Samples have sc = as . x >= 0: does the box reach that half plane?
+__device__ __forceinline__ bool half_plane_hits2(const float* as, const float* lo, const float* hi) {
+    const float u = (as[0] >= 0.f ? as[0] * hi[0] : as[0] * lo[0]) + (as[1] >= 0.f ? as[1] * hi[1] : as[1] * lo[1]);
     return u >= 0.f;
 }
 
-// Rows r (sr = r*os = x . b, b = (R[1], R[3])) whose samples can lie in the box.
-__device__ __forceinline__ void box_rows2(const float* R, const float* lo, const float* hi, const TileSpec2& ts,
-                                          int& r0, int& r1) {
+// Pose-list entries: the pose index relative to its phase, and kGen2 when the
+// pose is not a rotation (box_rows2 then needs its dual basis).
+constexpr unsigned kGen2 = 1u << 13, kPose2Mask = kGen2 - 1;
+static_assert(2 * kChunk2 <= int(kPose2Mask) + 1 && 2048 <= int(kPose2Mask) + 1, "pose index must fit the entries");
+
+// Tiled pose whose half plane reaches the box (as of half_plane_hits2, from R);
+// `general`: not a rotation.
+__device__ __forceinline__ bool pose_hits2(const float* R, const float* lo, const float* hi, bool& general) {
+    const PoseGram gr = pose_gram2(R);
+    general = !gram_is_rotation(gr);
+    if (general && !gram_tiled(gr)) return false;
+    float as[2] = {R[0], R[2]}, bs[2];
+    if (general) pose_dual2(R, gr, as, bs);
+    return half_plane_hits2(as, lo, hi);
+}
+
+// Rows r (sr = r*os = bs . x) whose samples can lie in the box.  A rotation's
+// bs is its column 1; other poses (`general`) compute their dual basis.
+__device__ __forceinline__ void box_rows2(const float* R, bool general, const float* lo, const float* hi,
+                                          const TileSpec2& ts, int& r0, int& r1) {
+    float as[2], bs[2] = {R[1], R[3]};
+    if (general) pose_dual2(R, pose_gram2(R), as, bs);
     float vlo = 0.f, vhi = 0.f;
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-        const float b = R[2 * k + 1];
+        const float b = bs[k];
         vlo += b >= 0.f ? b * lo[k] : b * hi[k];
         vhi += b >= 0.f ? b * hi[k] : b * lo[k];
     }
@@ -132,10 +153,14 @@ __device__ __forceinline__ void cull2(const float* __restrict__ rotb, int pend, 
 #pragma unroll
         for (int q = 0; q < kInFlight; ++q) {
             const int p = pbase + int(threadIdx.x) + (q0 + q) * kThreads;
-            if (p >= pend || !pose_is_rotation2(R[q])) continue;
-            if (half_plane_hits2(R[q], lo1, hi1)) plist[atomicAdd(&pcnt[0], 1)] = (unsigned short)(p - pbase);
-            if (half_plane_hits2(R[q], lo2, hi2))
-                plist[2 * kChunk2 - 1 - atomicAdd(&pcnt[1], 1)] = (unsigned short)(p - pbase);
+            const PoseGram gr = pose_gram2(R[q]);
+            const bool general = !gram_is_rotation(gr);
+            if (p >= pend || (general && !gram_tiled(gr))) continue;
+            float as[2] = {R[q][0], R[q][2]}, bs[2];
+            if (general) pose_dual2(R[q], gr, as, bs);
+            const unsigned short e = (unsigned short)((p - pbase) | (general ? kGen2 : 0u));
+            if (half_plane_hits2(as, lo1, hi1)) plist[atomicAdd(&pcnt[0], 1)] = e;
+            if (half_plane_hits2(as, lo2, hi2)) plist[2 * kChunk2 - 1 - atomicAdd(&pcnt[1], 1)] = e;
         }
     }
     __syncthreads();
@@ -281,7 +306,8 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
                                                              const float* __restrict__ weights,
                                                              const float* __restrict__ rot,
                                                              const float* __restrict__ shifts,
-                                                             Cx<float>* __restrict__ dst, float* __restrict__ wdst) {
+                                                             Cx<float>* __restrict__ dst, float* __restrict__ wdst,
+                                                             const float* __restrict__ reach) {
     constexpr int SL = CUBIC ? 2 : 1, SH = CUBIC ? 1 : 0;  // stencil reach below / above floor(x)
     constexpr int SLOW = CUBIC ? 1 : 0;                    // first tap at floor(x) - SLOW
     constexpr int RPS = 64 / KP;
@@ -301,6 +327,7 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
     const int N = g.N, H = g.H, half = N / 2;
     const int64_t items = g.B * ts.ksplit * int64_t(ts.nr) * ts.nc;
     const float cut2 = float(g.cut2);
+    const float rho_k = fminf(ts.rho, *reach);  // tiles beyond the call's reach hold no sample
     const int64_t per = xcd_per<kRun>(items);
     for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
         const int64_t w = xcd_item<kRun>(slot_i);
@@ -337,14 +364,14 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
         const float* rotb = rot + rb * g.P * 4;
         const float* shb = shifts ? shifts + sb * g.P * 2 : nullptr;
         const int64_t pose0 = b * g.P;
-        // samples lie within |x| <= rho; box 2 is box 1 mirrored, so one test serves both
+        // samples lie within |x| <= rho_k; box 2 is box 1 mirrored, so one test serves both
         float dist2 = 0.f;
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const float d = lo1[k] > 0.f ? lo1[k] : (hi1[k] < 0.f ? -hi1[k] : 0.f);
             dist2 += d * d;
         }
-        const int pend = dist2 > ts.rho * ts.rho ? p0 : p1;
+        const int pend = dist2 > rho_k * rho_k ? p0 : p1;
 
         for (int pbase = p0; pbase < pend; pbase += kChunk2) {
             int n1, n2;
@@ -352,7 +379,8 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
 #pragma unroll 1
             for (int pass = 0; pass < 2; ++pass) {
                 const int np = pass == 0 ? n1 : n2;
-                auto pose_at = [&](int k) { return pbase + int(plist[pass == 0 ? k : 2 * kChunk2 - 1 - k]); };
+                auto entry_at = [&](int k) { return unsigned(plist[pass == 0 ? k : 2 * kChunk2 - 1 - k]); };
+                auto pose_at = [&](int k) { return pbase + int(entry_at(k) & kPose2Mask); };
                 float lo[2], hi[2];
 #pragma unroll
                 for (int k = 0; k < 2; ++k) {
@@ -372,7 +400,8 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
                 if (base < np) load_pose2(rotb, shb, pose_at(min(base + slot, np - 1)), Rn, Sn);
                 for (; base < np; base += NW * KP) {
                     const bool sv = base + slot < np;
-                    const int pp = pose_at(min(base + slot, np - 1));
+                    const unsigned pe = entry_at(min(base + slot, np - 1));
+                    const int pp = pbase + int(pe & kPose2Mask);
                     float R[4], Sh[2];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) R[e] = Rn[e];
@@ -390,7 +419,7 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
                     }
                     __builtin_amdgcn_wave_barrier();
                     int r0, r1;
-                    box_rows2(R, lo, hi, ts, r0, r1);
+                    box_rows2(R, (pe & kGen2) != 0, lo, hi, ts, r0, r1);
                     const int nr = sv ? max(0, r1 - r0 + 1) : 0;
                     const int maxnr = wave_max(nr);
                     for (int rbase = 0; rbase < maxnr; rbase += RPS) {
@@ -519,13 +548,13 @@ __global__ __launch_bounds__(kBlock) void k_mirror2_x0(Geom g, Cx<float>* __rest
 
 template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool PRIV = false>
 hipError_t scatter2_launch(const Geom& g, const TileSpec2& ts, const void* src, const void* weights,
-                           const void* rot, const void* shifts, void* dst, void* wdst, hipStream_t s) {
+                           const void* rot, const void* shifts, void* dst, void* wdst, const float* reach, hipStream_t s) {
     const int64_t work = g.B * ts.ksplit * int64_t(ts.nr) * ts.nc;
     if (work > 0) {
         hipLaunchKernelGGL((k_scatter2_tiled<CUBIC, MODE, WEIGHTS, KP, PRIV>),
                            dim3(grid_for(kXcds * xcd_per<kRun>(work))),
                            dim3(kThreads), 0, s, g, ts, (const Cx<float>*)src, (const float*)weights,
-                           (const float*)rot, (const float*)shifts, (Cx<float>*)dst, (float*)wdst);
+                           (const float*)rot, (const float*)shifts, (Cx<float>*)dst, (float*)wdst, reach);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -540,14 +569,14 @@ hipError_t scatter2_launch(const Geom& g, const TileSpec2& ts, const void* src, 
 
 template <bool CUBIC, int MODE, bool WEIGHTS>
 hipError_t scatter2_kp(const Geom& g, const TileSpec2& ts, const void* src, const void* weights, const void* rot,
-                       const void* shifts, void* dst, void* wdst, hipStream_t s) {
-    // one pose per window keeps a window's samples >= os * (1 - 2 kRotationTol) - 1e-3 apart,
-    // beyond sqrt(2) (the diagonal of a cell) from os = 1.5 on
-    if (g.os >= kPrivOs)
-        return scatter2_launch<CUBIC, MODE, WEIGHTS, 1, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-    if (ts.kp >= 4) return scatter2_launch<CUBIC, MODE, WEIGHTS, 4>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-    if (ts.kp == 2) return scatter2_launch<CUBIC, MODE, WEIGHTS, 2>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-    return scatter2_launch<CUBIC, MODE, WEIGHTS, 1>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+                       const void* shifts, void* dst, void* wdst, const float* reach, hipStream_t s) {
+    // one pose per window keeps a window's samples >= os * kScaleMin (less rounding) apart,
+    // beyond sqrt(2) (the diagonal of a cell) when that is 1.5 or more
+    if (g.os * kScaleMin >= kPrivOs)
+        return scatter2_launch<CUBIC, MODE, WEIGHTS, 1, true>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
+    if (ts.kp >= 4) return scatter2_launch<CUBIC, MODE, WEIGHTS, 4>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
+    if (ts.kp == 2) return scatter2_launch<CUBIC, MODE, WEIGHTS, 2>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
+    return scatter2_launch<CUBIC, MODE, WEIGHTS, 1>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
 }
 
 // ----------------------------------------------------------------------------- gather
@@ -612,7 +641,8 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
                                                             const float* __restrict__ shifts,
                                                             Cx<float>* __restrict__ out, float* __restrict__ wout,
                                                             const Cx<float>* __restrict__ gsrc,
-                                                            float* __restrict__ grot, float* __restrict__ gshift) {
+                                                            float* __restrict__ grot, float* __restrict__ gshift,
+                                                            const float* __restrict__ reach) {
     static_assert(GMODE == 0 || KP == 1, "the gradient modes sum one pose per wave batch");
     static_assert(GMODE == 0 || std::is_same<VS, float>::value, "complex-half volumes are read by the forward only");
     constexpr int LO = CUBIC ? 1 : 0, HI = CUBIC ? 2 : 1, WC = GC + LO + HI, WR = GR + LO + HI, W2 = WC * WR;
@@ -630,6 +660,7 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
     const int N = g.N, H = g.H;
     const int64_t items = g.B * ts.gksplit * int64_t(ts.gnt) * ts.gnt;
     const float cut2 = float(g.cut2);
+    const float rho_k = fminf(ts.rho, *reach);  // tiles beyond the call's reach hold no sample
     const int64_t per = xcd_per<kRun>(items);
     for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
         const int64_t w = xcd_item<kRun>(slot_i);
@@ -651,7 +682,7 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
             const float d = lo[k] > 0.f ? lo[k] : (hi[k] < 0.f ? -hi[k] : 0.f);
             dist2 += d * d;
         }
-        if (dist2 > ts.rho * ts.rho || p1 <= p0) continue;
+        if (dist2 > rho_k * rho_k || p1 <= p0) continue;
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
         const float* rotb = rot + rb * g.P * 4;
         const float* shb = shifts ? shifts + sb * g.P * 2 : nullptr;
@@ -667,7 +698,8 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
                 float R[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) R[e] = rotb[int64_t(pbase + k) * 4 + e];
-                if (pose_is_rotation2(R) && half_plane_hits2(R, lo, hi)) plist[atomicAdd(&pcnt[0], 1)] = k;
+                bool gen = false;
+                if (pose_hits2(R, lo, hi, gen)) plist[atomicAdd(&pcnt[0], 1)] = (unsigned short)(k | (gen ? kGen2 : 0u));
             }
             __syncthreads();
             const int np = pcnt[0];
@@ -686,13 +718,15 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
                 __syncthreads();
                 loaded = true;
             }
-            auto pose_at = [&](int k) { return pbase + int(plist[k]); };
+            auto entry_at = [&](int k) { return unsigned(plist[k]); };
+            auto pose_at = [&](int k) { return pbase + int(entry_at(k) & kPose2Mask); };
             int base = wave * KP;
             float Rn[4], Sn[2];
             if (base < np) load_pose2(rotb, shb, pose_at(min(base + slot, np - 1)), Rn, Sn);
             for (; base < np; base += NW * KP) {
                 const bool sv = base + slot < np;
-                const int pp = pose_at(min(base + slot, np - 1));
+                const unsigned pe = entry_at(min(base + slot, np - 1));
+                const int pp = pbase + int(pe & kPose2Mask);
                 float R[4], Sh[2];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) R[e] = Rn[e];
@@ -712,7 +746,7 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
 #pragma unroll
                 for (int k = 0; k < 6; ++k) acc[k] = 0.f;
                 int r0, r1;
-                box_rows2(R, lo, hi, ts, r0, r1);
+                box_rows2(R, (pe & kGen2) != 0, lo, hi, ts, r0, r1);
                 const int nr = sv ? max(0, r1 - r0 + 1) : 0;
                 const int maxnr = wave_max(nr);
                 for (int rbase = 0; rbase < maxnr; rbase += RPS) {
@@ -817,76 +851,74 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
 template <bool CUBIC, int KP, int GMODE, bool RS, bool WG, typename VS = float>
 hipError_t gather2_launch(const Geom& g, const TileSpec2& ts, const void* rec, const void* gw, const void* rot,
                           const void* shifts, void* out, void* wout, const void* gsrc, void* grot, void* gshift,
-                          hipStream_t s) {
+                          const float* reach, hipStream_t s) {
     const int64_t work = g.B * ts.gksplit * int64_t(ts.gnt) * ts.gnt;
     if (work == 0) return hipSuccess;
     hipLaunchKernelGGL((k_gather2_tiled<CUBIC, KP, GMODE, RS, WG, VS>), dim3(grid_for(kXcds * xcd_per<kRun>(work))),
                        dim3(kThreads), 0, s, g, ts, (const Cx<VS>*)rec, (const float*)gw, (const float*)rot,
                        (const float*)shifts, (Cx<float>*)out, (float*)wout, (const Cx<float>*)gsrc, (float*)grot,
-                       (float*)gshift);
+                       (float*)gshift, reach);
     return hipGetLastError();
 }
 
 template <bool CUBIC, typename VS>
 hipError_t gather2_forw(const Geom& g, const TileSpec2& ts, const void* rec, const void* rot, const void* shifts,
-                        void* out, hipStream_t s) {
+                        void* out, const float* reach, hipStream_t s) {
     if (ts.kp_gather >= 4)
         return gather2_launch<CUBIC, 4, 0, false, false, VS>(g, ts, rec, nullptr, rot, shifts, out, nullptr, nullptr,
-                                                             nullptr, nullptr, s);
+                                                             nullptr, nullptr, reach, s);
     if (ts.kp_gather == 2)
         return gather2_launch<CUBIC, 2, 0, false, false, VS>(g, ts, rec, nullptr, rot, shifts, out, nullptr, nullptr,
-                                                             nullptr, nullptr, s);
+                                                             nullptr, nullptr, reach, s);
     return gather2_launch<CUBIC, 1, 0, false, false, VS>(g, ts, rec, nullptr, rot, shifts, out, nullptr, nullptr,
-                                                         nullptr, nullptr, s);
+                                                         nullptr, nullptr, reach, s);
 }
 
 template <bool CUBIC>
 hipError_t gather2_modes(int mode, const Geom& g, const TileSpec2& ts, const void* rec, const void* gw,
                          const void* rot, const void* shifts, void* out, void* wout, const void* gsrc, void* grot,
-                         void* gshift, hipStream_t s) {
-    if (mode == 0) return gather2_forw<CUBIC, float>(g, ts, rec, rot, shifts, out, s);
+                         void* gshift, const float* reach, hipStream_t s) {
+    if (mode == 0) return gather2_forw<CUBIC, float>(g, ts, rec, rot, shifts, out, reach, s);
     if (mode == 1)
-        return gather2_launch<CUBIC, 1, 1, true, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift,
-                                                        s);
+        return gather2_launch<CUBIC, 1, 1, true, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, reach, s);
     const bool rs = grot || gshift;
     if (wout)
         return rs ? gather2_launch<CUBIC, 1, 2, true, true>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
-                                                            gshift, s)
+                                                            gshift, reach, s)
                   : gather2_launch<CUBIC, 1, 2, false, true>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
-                                                             gshift, s);
-    return rs ? gather2_launch<CUBIC, 1, 2, true, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift,
-                                                         s)
+                                                             gshift, reach, s);
+    return rs ? gather2_launch<CUBIC, 1, 2, true, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, reach, s)
               : gather2_launch<CUBIC, 1, 2, false, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
-                                                          gshift, s);
+                                                          gshift, reach, s);
 }
 
 }  // namespace
 
 hipError_t launch_gather2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* rec,
                                 const void* gw, const void* rot, const void* shifts, void* out, void* wout,
-                                const void* gsrc, void* grot, void* gshift, hipStream_t s, bool rec_half) {
+                                const void* gsrc, void* grot, void* gshift, const float* reach, hipStream_t s, bool rec_half) {
     if (rec_half) {
         if (mode != 0) return hipErrorInvalidValue;
-        return cubic ? gather2_forw<true, __half>(g, ts, rec, rot, shifts, out, s)
-                     : gather2_forw<false, __half>(g, ts, rec, rot, shifts, out, s);
+        return cubic ? gather2_forw<true, __half>(g, ts, rec, rot, shifts, out, reach, s)
+                     : gather2_forw<false, __half>(g, ts, rec, rot, shifts, out, reach, s);
     }
     if (mode == 1 && !grot && !gshift) return hipSuccess;
-    return cubic ? gather2_modes<true>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, s)
-                 : gather2_modes<false>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, s);
+    return cubic ? gather2_modes<true>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, reach, s)
+                 : gather2_modes<false>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, reach, s);
 }
 
 hipError_t launch_scatter2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* src,
                                  const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
-                                 hipStream_t s) {
+                                 const float* reach, hipStream_t s) {
     if (mode == 0) {
         if (weights)
-            return cubic ? scatter2_kp<true, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s)
-                         : scatter2_kp<false, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-        return cubic ? scatter2_kp<true, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
-                     : scatter2_kp<false, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
+            return cubic ? scatter2_kp<true, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s)
+                         : scatter2_kp<false, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
+        return cubic ? scatter2_kp<true, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s)
+                     : scatter2_kp<false, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s);
     }
-    return cubic ? scatter2_kp<true, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
-                 : scatter2_kp<false, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
+    return cubic ? scatter2_kp<true, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s)
+                 : scatter2_kp<false, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s);
 }
 
 }  // namespace tp

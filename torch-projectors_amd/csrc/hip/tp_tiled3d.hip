@@ -31,9 +31,12 @@
 //                     into a zeroed region.  The Hermitian x = 0 mirror of
 //                     the backprojection is applied afterwards by k_mirror_x0.
 //
-// Only poses whose first two rotation columns are orthonormal take this path
-// (pose_is_rotation); the per-pixel kernels handle the others and write the
-// masked pixels of the forward.
+// Poses whose first two matrix columns a, b have singular values in
+// [kScaleMin, kScaleMax] take this path (pose_tiled3: rotations, and scaled or
+// sheared matrices); the per-pixel kernels handle the others and write the
+// masked pixels of the forward.  A sample x = sc a + sr b of such a pose has
+// sc = as . x and sr = bs . x with the dual basis (as, bs) of a, b, which
+// bounds the rows and the half plane sc >= 0 that can reach a box.
 #include <type_traits>
 
 #include "tp_device.hh"
@@ -60,28 +63,35 @@ __device__ __forceinline__ bool plane_hits(const float* R, const float* lo, cons
     return fabsf(n0 * m0 + n1 * m1 + n2 * m2) <= fabsf(n0) * h0 + fabsf(n1) * h1 + fabsf(n2) * h2;
 }
 
-// Range of sc = a.x (column 0) over the box; samples have sc >= 0.
-__device__ __forceinline__ bool half_plane_hits(const float* R, const float* hi, const float* lo) {
+// Largest sc = as . x over the box; samples have sc >= 0.
+__device__ __forceinline__ bool half_plane_hits(const float* as, const float* hi, const float* lo) {
     float uhi = 0.f;
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        const float a = R[3 * k];
-        uhi += a >= 0.f ? a * hi[k] : a * lo[k];
-    }
+    for (int k = 0; k < 3; ++k) uhi += as[k] >= 0.f ? as[k] * hi[k] : as[k] * lo[k];
     return uhi >= 0.f;
 }
 
-__device__ __forceinline__ bool pose_hits(const float* R, const float* lo, const float* hi) {
-    return pose_is_rotation(R) && plane_hits(R, lo, hi) && half_plane_hits(R, hi, lo);
+// Tiled pose whose plane and half plane reach the box; `general`: not a
+// rotation (its bounds need the dual basis, carried as a flag in the pose list).
+__device__ __forceinline__ bool pose_hits(const float* R, const float* lo, const float* hi, bool& general) {
+    const PoseGram gr = pose_gram3(R);
+    general = !gram_is_rotation(gr);
+    if ((general && !gram_tiled(gr)) || !plane_hits(R, lo, hi)) return false;
+    float as[3] = {R[0], R[3], R[6]}, bs[3];
+    if (general) pose_dual3(R, gr, as, bs);
+    return half_plane_hits(as, hi, lo);
 }
 
-// Rows r (sr = r*os = b.x, b = column 1) whose samples can lie in the box.
-__device__ __forceinline__ void box_rows(const float* R, const float* lo, const float* hi, const TileSpec& ts,
-                                         int& r0, int& r1) {
+// Rows r (sr = r*os = bs . x) whose samples can lie in the box.  A rotation's
+// bs is its column 1; other poses (`general`) compute their dual basis.
+__device__ __forceinline__ void box_rows(const float* R, bool general, const float* lo, const float* hi,
+                                         const TileSpec& ts, int& r0, int& r1) {
+    float as[3], bs[3] = {R[1], R[4], R[7]};
+    if (general) pose_dual3(R, pose_gram3(R), as, bs);
     float vlo = 0.f, vhi = 0.f;
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-        const float b = R[3 * k + 1];
+        const float b = bs[k];
         vlo += b >= 0.f ? b * lo[k] : b * hi[k];
         vhi += b >= 0.f ? b * hi[k] : b * lo[k];
     }
@@ -219,8 +229,9 @@ constexpr int kCullInFlight = 2;  // rotations loaded together per lane
 constexpr int kChunk = 1024;      // poses culled per phase
 
 // List entries: pose index relative to the phase, plus which boxes it crosses.
-constexpr unsigned kHit1 = 1u << 14, kHit2 = 1u << 15, kPoseMask = kHit1 - 1;
-static_assert(kChunk <= int(kPoseMask) + 1, "pose index must fit below the flag bits");
+// kGeneral: the pose is not a rotation (box_rows needs its dual basis).
+constexpr unsigned kHit1 = 1u << 14, kHit2 = 1u << 15, kGeneral = 1u << 13, kPoseMask = kGeneral - 1;
+static_assert(2 * kChunk <= int(kPoseMask) + 1, "pose index must fit below the flag bits");
 
 // Cull poses [pbase, pend) (at most kChunk) against up to two boxes with a
 // workgroup of NT lanes; returns the count.
@@ -243,8 +254,11 @@ __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pe
         for (int q = 0; q < kCullInFlight; ++q) {
             const int p = pbase + int(threadIdx.x) + (q0 + q) * NT;
             if (p >= pend) continue;
-                const bool h1 = pose_hits(R[q], lo1, hi1), h2 = TWO && pose_hits(R[q], lo2, hi2);
-            if (h1 || h2) plist[atomicAdd(pcount, 1)] = (unsigned short)((p - pbase) | (h1 ? kHit1 : 0) | (h2 ? kHit2 : 0));
+            bool gen = false;
+            const bool h1 = pose_hits(R[q], lo1, hi1, gen), h2 = TWO && pose_hits(R[q], lo2, hi2, gen);
+            if (h1 || h2)
+                plist[atomicAdd(pcount, 1)] =
+                    (unsigned short)((p - pbase) | (h1 ? kHit1 : 0) | (h2 ? kHit2 : 0) | (gen ? kGeneral : 0));
         }
     }
     __syncthreads();
@@ -279,10 +293,14 @@ __device__ __forceinline__ void cull_chunk_boxes(const float* __restrict__ rotb,
             const int p = pbase + int(threadIdx.x) + (q0 + q) * NT;
             // box 2 is box 1 negated (bit for bit), which a plane through the origin
             // crosses exactly when it crosses box 1: one plane test serves both
-            if (p >= pend || !pose_is_rotation(R[q]) || !plane_hits(R[q], lo1, hi1)) continue;
-            if (half_plane_hits(R[q], hi1, lo1)) plist[atomicAdd(&pcnt[0], 1)] = (unsigned short)(p - pbase);
-            if (half_plane_hits(R[q], hi2, lo2))
-                plist[kChunk - 1 - atomicAdd(&pcnt[1], 1)] = (unsigned short)(p - pbase);
+            const PoseGram gr = pose_gram3(R[q]);
+            const bool general = !gram_is_rotation(gr);
+            if (p >= pend || (general && !gram_tiled(gr)) || !plane_hits(R[q], lo1, hi1)) continue;
+            float as[3] = {R[q][0], R[q][3], R[q][6]}, bs[3];
+            if (general) pose_dual3(R[q], gr, as, bs);
+            const unsigned short e = (unsigned short)((p - pbase) | (general ? kGeneral : 0u));
+            if (half_plane_hits(as, hi1, lo1)) plist[atomicAdd(&pcnt[0], 1)] = e;
+            if (half_plane_hits(as, hi2, lo2)) plist[kChunk - 1 - atomicAdd(&pcnt[1], 1)] = e;
         }
     }
     __syncthreads();
@@ -362,7 +380,8 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                                                         float* __restrict__ grot = nullptr,
                                                         float* __restrict__ gshift = nullptr,
                                                         const float* __restrict__ gw = nullptr,
-                                                        float* __restrict__ wout = nullptr) {
+                                                        float* __restrict__ wout = nullptr,
+                                                        const float* __restrict__ reach = nullptr) {
     static_assert(GMODE == 0 || KP == 1, "the gradient modes sum one pose per wave batch");
     static_assert(GMODE == 0 || std::is_same<VS, float>::value, "complex-half volumes are read by the forward only");
     constexpr bool GRADS = GMODE == 1 || (GMODE == 2 && RS);
@@ -385,20 +404,48 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slot = lane / RPS, jrow = lane % RPS;
     const int nt = ts.nt;
-    const int64_t items = g.B * (int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fd1 - ts.fd0) * ts.ksplit +
-                                 int64_t(nt) * nt * ts.ntfd);
+    // items: the core pieces and tiles of the grid that unit-scale poses reach (one launch slot
+    // each), then the tiles of the wider grid for enlarging poses, which the grid-stride loop
+    // visits after them and which are skipped when inside the first grid or beyond the reach
+    const int64_t items1 = g.B * (int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fd1 - ts.fd0) * ts.ksplit +
+                                  int64_t(nt) * nt * ts.ntfd);
+    const int64_t per_b2 = int64_t(ts.nt2) * ts.nt2 * ts.ntfd2;
     const float cut2 = float(g.cut2);
-    const float rho2 = ts.rho * ts.rho;
+    // tiles beyond the call's reach (launch_pose_reach) hold no sample; the wider grid's slots
+    // follow the first grid's and are visited only when the reach leaves the first grid
+    const float rho_k = fminf(ts.rho, *reach), rho2 = rho_k * rho_k;
     const int N = g.N, H = g.H;
-    const int64_t per = xcd_per<kRunForw>(items);
-    for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
-        const int64_t w = xcd_item<kRunForw>(slot_i);
-        if (w >= items) continue;
-        const Item it = item_of(w, g.B, int(g.P), ts.ntfd, nt, nt, ts.fd0, ts.fd1, ts.fc0, ts.fc1, ts.fc0, ts.fc1,
-                                ts.ksplit, ts.prange);
-        if (it.skip) continue;
-        const int64_t b = it.b;
-        const int tc = ts.org + it.kc * L, tr = ts.org + it.kr * L, td = ts.orgd + it.kd * LD;
+    const int64_t nslot1 = kXcds * xcd_per<kRunForw>(items1);
+    const int64_t nslot = nslot1 + kXcds * xcd_per<kRunForw>(g.B * per_b2);
+    for (int64_t slot_i = blockIdx.x; slot_i < nslot; slot_i += gridDim.x) {
+        if (slot_i >= nslot1 && rho_k + 2.0f <= float(-ts.org) && rho_k + 2.0f <= float(-ts.orgd)) break;
+        const int64_t w = slot_i < nslot1 ? xcd_item<kRunForw>(slot_i) : items1 + xcd_item<kRunForw>(slot_i - nslot1);
+        if (w >= items1 + g.B * per_b2 || (slot_i < nslot1 && w >= items1)) continue;
+        int64_t b;
+        int tc, tr, td, p0, p1;
+        if (w < items1) {
+            const Item it = item_of(w, g.B, int(g.P), ts.ntfd, nt, nt, ts.fd0, ts.fd1, ts.fc0, ts.fc1, ts.fc0, ts.fc1,
+                                    ts.ksplit, ts.prange);
+            if (it.skip) continue;
+            b = it.b;
+            tc = ts.org + it.kc * L;
+            tr = ts.org + it.kr * L;
+            td = ts.orgd + it.kd * LD;
+            p0 = it.p0;
+            p1 = it.p1;
+        } else {
+            const int64_t q = w - items1;
+            b = q / per_b2;
+            const int t = int(q - b * per_b2);
+            tc = ts.org2 + (t % ts.nt2) * L;
+            tr = ts.org2 + ((t / ts.nt2) % ts.nt2) * L;
+            td = ts.orgd2 + (t / (ts.nt2 * ts.nt2)) * LD;
+            if (tc >= ts.org && tc < ts.org + nt * L && tr >= ts.org && tr < ts.org + nt * L && td >= ts.orgd &&
+                td < ts.orgd + ts.ntfd * LD)
+                continue;
+            p0 = 0;
+            p1 = int(g.P);
+        }
         // samples owned by this tile: floor(x) in [t, t + edge) on every axis (+ slack)
         const float lo[3] = {float(tc) - ts.eps, float(tr) - ts.eps, float(td) - ts.eps};
         const float hi[3] = {float(tc + L) + ts.eps, float(tr + L) + ts.eps, float(td + LD) + ts.eps};
@@ -413,8 +460,8 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
         const float* rotb = rot + rb * g.P * 9;
         const Cx<VS>* recb = rec + b * g.vol;
         bool loaded = false;
-        for (int pbase = it.p0; pbase < it.p1; pbase += CH) {
-            const int np = cull_chunk<NT, false, CH>(rotb, it.p1, pbase, lo, hi, lo, hi, plist, &pcount);
+        for (int pbase = p0; pbase < p1; pbase += CH) {
+            const int np = cull_chunk<NT, false, CH>(rotb, p1, pbase, lo, hi, lo, hi, plist, &pcount);
             if (np == 0) continue;
             if (!loaded) {
                 // stage the tile and its halo.  When the staged box lies on one side of c = 0 and
@@ -474,7 +521,8 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                       Rn, Sn);
             for (; base < np; base += NW * KP) {
                 const bool sv = base + slot < np;
-                const int pp = pbase + (plist[min(base + slot, np - 1)] & kPoseMask);
+                const unsigned pe = plist[min(base + slot, np - 1)];
+                const int pp = pbase + int(pe & kPoseMask);
                 float R[9], Sh[2];
 #pragma unroll
                 for (int e = 0; e < 9; ++e) R[e] = Rn[e];
@@ -496,7 +544,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
 #pragma unroll
                 for (int k = 0; k < 11; ++k) acc[k] = 0.f;
                 int r0, r1;
-                box_rows(R, lo, hi, ts, r0, r1);
+                box_rows(R, (pe & kGeneral) != 0, lo, hi, ts, r0, r1);
                 const int nr = sv ? max(0, r1 - r0 + 1) : 0;
                 const int maxnr = wave_max(nr);
                 for (int rbase = 0; rbase < maxnr; rbase += RPS) {
@@ -737,7 +785,8 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                                                            const float* __restrict__ weights,
                                                            const float* __restrict__ rot,
                                                            const float* __restrict__ shifts,
-                                                           Cx<float>* __restrict__ dst, float* __restrict__ wdst) {
+                                                           Cx<float>* __restrict__ dst, float* __restrict__ wdst,
+                                                           const float* __restrict__ reach) {
     constexpr int SL = CUBIC ? 2 : 1, SH = CUBIC ? 1 : 0;  // stencil reach below / above floor(x)
     constexpr int SLOW = CUBIC ? 1 : 0;                    // first tap at floor(x) - SLOW
     constexpr int RPS = 64 / KP;
@@ -754,6 +803,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
     const int64_t items = g.B * (int64_t(ts.sd1 - ts.sd0) * (ts.sr1 - ts.sr0) * ts.sc1 * ts.ksplit +
                                  int64_t(ts.ntd) * ts.ntr * ts.ntc);
     const float cut2 = float(g.cut2);
+    const float rho_k = fminf(ts.rho, *reach);  // tiles beyond the call's reach hold no sample
     const int64_t per = xcd_per<kRunScatter>(items);
     for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
         const int64_t w = xcd_item<kRunScatter>(slot_i);
@@ -782,14 +832,14 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
         const float* rotb = rot + rb * g.P * 9;
         const int64_t pose0 = b * g.P;
-        // samples lie within |x| <= rho; box 2 is box 1 mirrored, so one test serves both
+        // samples lie within |x| <= rho_k; box 2 is box 1 mirrored, so one test serves both
         float dist2 = 0.f;
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
             const float q = lo1[k] > 0.f ? lo1[k] : (hi1[k] < 0.f ? -hi1[k] : 0.f);
             dist2 += q * q;
         }
-        const int pend = dist2 > ts.rho * ts.rho ? it.p0 : it.p1;
+        const int pend = dist2 > rho_k * rho_k ? it.p0 : it.p1;
 
         const float* shb = shifts ? shifts + sb * g.P * 2 : nullptr;
         for (int pbase = it.p0; pbase < pend; pbase += kChunkSc) {
@@ -799,7 +849,8 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
             for (int pass = 0; pass < 2; ++pass) {
                 const int np = pass == 0 ? n1 : n2;
                 // pose of list entry k of this pass (box-2 entries are stored from the back)
-                auto pose_at = [&](int k) { return pbase + int(plist[pass == 0 ? k : kChunk - 1 - k]); };
+                auto entry_at = [&](int k) { return unsigned(plist[pass == 0 ? k : kChunk - 1 - k]); };
+                auto pose_at = [&](int k) { return pbase + int(entry_at(k) & kPoseMask); };
                 float lo[3], hi[3];
 #pragma unroll
                 for (int k = 0; k < 3; ++k) {
@@ -820,7 +871,8 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                 if (base < np) load_pose(rotb, shb, pose_at(min(base + slot, np - 1)), Rn, Sn);
                 for (; base < np; base += NW * KP) {
                     const bool sv = base + slot < np;
-                    const int pp = pose_at(min(base + slot, np - 1));
+                    const unsigned pe = entry_at(min(base + slot, np - 1));
+                    const int pp = pbase + int(pe & kPoseMask);
                     float R[9], Sh[2];
 #pragma unroll
                     for (int e = 0; e < 9; ++e) R[e] = Rn[e];
@@ -838,7 +890,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                     __builtin_amdgcn_wave_barrier();
                     {
                     int r0, r1;
-                    box_rows(R, lo, hi, ts, r0, r1);
+                    box_rows(R, (pe & kGeneral) != 0, lo, hi, ts, r0, r1);
                     const int nr = sv ? max(0, r1 - r0 + 1) : 0;
                     const int maxnr = wave_max(nr);
                     for (int rbase = 0; rbase < maxnr; rbase += RPS) {
@@ -979,18 +1031,18 @@ __global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<fl
 
 template <bool CUBIC, int KP, bool OSX, typename VS>
 hipError_t forw_launch(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts,
-                       void* out, hipStream_t s) {
+                       void* out, const float* reach, hipStream_t s) {
     const int64_t fcore = int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fd1 - ts.fd0) * ts.ksplit;
     const int64_t work = g.B * (fcore + int64_t(ts.nt) * ts.nt * ts.ntfd);
     hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP, OSX, 0, true, false, VS>),
                        dim3(grid_for(kXcds * xcd_per<kRunForw>(work))), dim3(kForwThreads), 0, s, g, ts,
-                       (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
+                       (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out, nullptr, nullptr, nullptr, nullptr, nullptr, reach);
     return hipGetLastError();
 }
 
 template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool OSX>
 hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
-                          const void* shifts, void* dst, void* wdst, hipStream_t s) {
+                          const void* shifts, void* dst, void* wdst, const float* reach, hipStream_t s) {
     const int64_t score = int64_t(ts.sd1 - ts.sd0) * (ts.sr1 - ts.sr0) * ts.sc1 * ts.ksplit;
     if (score > 0) {
         const int64_t cells = g.B * int64_t((ts.sd1 - ts.sd0) * SD) * ((ts.sr1 - ts.sr0) * SR) * (ts.sc1 * SC);
@@ -1005,7 +1057,7 @@ hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, co
     hipLaunchKernelGGL((k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP, OSX>), dim3(grid_for(kXcds * xcd_per<kRunScatter>(work))),
                        dim3(kScatterThreads), 0, s, g,
                        ts, (const Cx<float>*)src, (const float*)weights, (const float*)rot, (const float*)shifts,
-                       (Cx<float>*)dst, (float*)wdst);
+                       (Cx<float>*)dst, (float*)wdst, reach);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || MODE != 0) return e;
     const int64_t pairs = g.B * int64_t(g.N) * g.N;
@@ -1018,120 +1070,120 @@ hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, co
 
 template <bool CUBIC, int MODE, bool WEIGHTS, bool OSX>
 hipError_t scatter_kp_osx(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
-                          const void* shifts, void* dst, void* wdst, hipStream_t s) {
+                          const void* shifts, void* dst, void* wdst, const float* reach, hipStream_t s) {
     if (ts.kp_scatter >= 4)
-        return scatter_launch<CUBIC, MODE, WEIGHTS, 4, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+        return scatter_launch<CUBIC, MODE, WEIGHTS, 4, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
     if (ts.kp_scatter == 2)
-        return scatter_launch<CUBIC, MODE, WEIGHTS, 2, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-    return scatter_launch<CUBIC, MODE, WEIGHTS, 1, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+        return scatter_launch<CUBIC, MODE, WEIGHTS, 2, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
+    return scatter_launch<CUBIC, MODE, WEIGHTS, 1, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
 }
 
 template <bool CUBIC, int MODE, bool WEIGHTS>
 hipError_t scatter_kp(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
-                      const void* shifts, void* dst, void* wdst, hipStream_t s) {
-    if (ts.os_exact) return scatter_kp_osx<CUBIC, MODE, WEIGHTS, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-    return scatter_kp_osx<CUBIC, MODE, WEIGHTS, false>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+                      const void* shifts, void* dst, void* wdst, const float* reach, hipStream_t s) {
+    if (ts.os_exact) return scatter_kp_osx<CUBIC, MODE, WEIGHTS, true>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
+    return scatter_kp_osx<CUBIC, MODE, WEIGHTS, false>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
 }
 
 template <bool CUBIC, bool OSX>
 hipError_t grads_launch(const Geom& g, const TileSpec& ts, const void* gproj, const void* rec, const void* rot,
-                        const void* shifts, void* grot, void* gshift, hipStream_t s) {
+                        const void* shifts, void* grot, void* gshift, const float* reach, hipStream_t s) {
     const int64_t fcore = int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fd1 - ts.fd0) * ts.ksplit;
     const int64_t work = g.B * (fcore + int64_t(ts.nt) * ts.nt * ts.ntfd);
     hipLaunchKernelGGL((k_forw3_tiled<CUBIC, 1, OSX, 1>), dim3(grid_for(kXcds * xcd_per<kRunForw>(work))),
                        dim3(kForwThreads), 0, s, g, ts, (const Cx<float>*)rec, (const float*)rot,
                        (const float*)shifts, (Cx<float>*)nullptr, (const Cx<float>*)gproj, (float*)grot,
-                       (float*)gshift);
+                       (float*)gshift, nullptr, nullptr, reach);
     return hipGetLastError();
 }
 
 template <bool CUBIC, bool OSX, bool RS, bool WG>
 hipError_t bpback_launch(const Geom& g, const TileSpec& ts, const void* gdata, const void* gw, const void* proj,
                          const void* rot, const void* shifts, void* gproj, void* gweights, void* grot, void* gshift,
-                         hipStream_t s) {
+                         const float* reach, hipStream_t s) {
     const int64_t fcore = int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fd1 - ts.fd0) * ts.ksplit;
     const int64_t work = g.B * (fcore + int64_t(ts.nt) * ts.nt * ts.ntfd);
     hipLaunchKernelGGL((k_forw3_tiled<CUBIC, 1, OSX, 2, RS, WG>), dim3(grid_for(kXcds * xcd_per<kRunForw>(work))),
                        dim3(kForwThreads), 0, s, g, ts, (const Cx<float>*)gdata, (const float*)rot,
                        (const float*)shifts, (Cx<float>*)gproj, (const Cx<float>*)proj, (float*)grot, (float*)gshift,
-                       (const float*)gw, (float*)gweights);
+                       (const float*)gw, (float*)gweights, reach);
     return hipGetLastError();
 }
 
 template <bool CUBIC, bool OSX>
 hipError_t bpback_flags(const Geom& g, const TileSpec& ts, const void* gdata, const void* gw, const void* proj,
                         const void* rot, const void* shifts, void* gproj, void* gweights, void* grot, void* gshift,
-                        hipStream_t s) {
+                        const float* reach, hipStream_t s) {
     const bool rs = grot || gshift, wg = gw && gweights;
     if (rs)
         return wg ? bpback_launch<CUBIC, OSX, true, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
-                                                          gshift, s)
+                                                          gshift, reach, s)
                   : bpback_launch<CUBIC, OSX, true, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, nullptr, grot,
-                                                           gshift, s);
+                                                           gshift, reach, s);
     return wg ? bpback_launch<CUBIC, OSX, false, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
-                                                       gshift, s)
+                                                       gshift, reach, s)
               : bpback_launch<CUBIC, OSX, false, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, nullptr, grot,
-                                                        gshift, s);
+                                                        gshift, reach, s);
 }
 
 template <bool CUBIC, bool OSX, typename VS>
 hipError_t forw_kp(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts, void* out,
-                   hipStream_t s) {
-    if (ts.kp_forw >= 4) return forw_launch<CUBIC, 4, OSX, VS>(g, ts, rec, rot, shifts, out, s);
-    if (ts.kp_forw == 2) return forw_launch<CUBIC, 2, OSX, VS>(g, ts, rec, rot, shifts, out, s);
-    return forw_launch<CUBIC, 1, OSX, VS>(g, ts, rec, rot, shifts, out, s);
+                   const float* reach, hipStream_t s) {
+    if (ts.kp_forw >= 4) return forw_launch<CUBIC, 4, OSX, VS>(g, ts, rec, rot, shifts, out, reach, s);
+    if (ts.kp_forw == 2) return forw_launch<CUBIC, 2, OSX, VS>(g, ts, rec, rot, shifts, out, reach, s);
+    return forw_launch<CUBIC, 1, OSX, VS>(g, ts, rec, rot, shifts, out, reach, s);
 }
 
 template <typename VS>
 hipError_t forw_store(bool cubic, const Geom& g, const TileSpec& ts, const void* rec, const void* rot,
-                      const void* shifts, void* out, hipStream_t s) {
+                      const void* shifts, void* out, const float* reach, hipStream_t s) {
     if (cubic)
-        return ts.os_exact ? forw_kp<true, true, VS>(g, ts, rec, rot, shifts, out, s)
-                           : forw_kp<true, false, VS>(g, ts, rec, rot, shifts, out, s);
-    return ts.os_exact ? forw_kp<false, true, VS>(g, ts, rec, rot, shifts, out, s)
-                       : forw_kp<false, false, VS>(g, ts, rec, rot, shifts, out, s);
+        return ts.os_exact ? forw_kp<true, true, VS>(g, ts, rec, rot, shifts, out, reach, s)
+                           : forw_kp<true, false, VS>(g, ts, rec, rot, shifts, out, reach, s);
+    return ts.os_exact ? forw_kp<false, true, VS>(g, ts, rec, rot, shifts, out, reach, s)
+                       : forw_kp<false, false, VS>(g, ts, rec, rot, shifts, out, reach, s);
 }
 
 }  // namespace
 
 hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* rec,
-                                      const void* rot, const void* shifts, void* out, hipStream_t s, bool rec_half) {
-    if (rec_half) return forw_store<__half>(cubic, g, ts, rec, rot, shifts, out, s);
-    return forw_store<float>(cubic, g, ts, rec, rot, shifts, out, s);
+                                      const void* rot, const void* shifts, void* out, const float* reach, hipStream_t s, bool rec_half) {
+    if (rec_half) return forw_store<__half>(cubic, g, ts, rec, rot, shifts, out, reach, s);
+    return forw_store<float>(cubic, g, ts, rec, rot, shifts, out, reach, s);
 }
 
 hipError_t launch_grads3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gproj, const void* rec,
-                               const void* rot, const void* shifts, void* grot, void* gshift, hipStream_t s) {
+                               const void* rot, const void* shifts, void* grot, void* gshift, const float* reach, hipStream_t s) {
     if (!grot && !gshift) return hipSuccess;
     if (cubic)
-        return ts.os_exact ? grads_launch<true, true>(g, ts, gproj, rec, rot, shifts, grot, gshift, s)
-                           : grads_launch<true, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, s);
-    return ts.os_exact ? grads_launch<false, true>(g, ts, gproj, rec, rot, shifts, grot, gshift, s)
-                       : grads_launch<false, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, s);
+        return ts.os_exact ? grads_launch<true, true>(g, ts, gproj, rec, rot, shifts, grot, gshift, reach, s)
+                           : grads_launch<true, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, reach, s);
+    return ts.os_exact ? grads_launch<false, true>(g, ts, gproj, rec, rot, shifts, grot, gshift, reach, s)
+                       : grads_launch<false, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, reach, s);
 }
 
 hipError_t launch_bpback3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gdata, const void* gw,
                                 const void* proj, const void* rot, const void* shifts, void* gproj, void* gweights,
-                                void* grot, void* gshift, hipStream_t s) {
+                                void* grot, void* gshift, const float* reach, hipStream_t s) {
     if (cubic)
-        return ts.os_exact ? bpback_flags<true, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s)
-                           : bpback_flags<true, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
-    return ts.os_exact ? bpback_flags<false, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s)
-                       : bpback_flags<false, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+        return ts.os_exact ? bpback_flags<true, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, reach, s)
+                           : bpback_flags<true, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, reach, s);
+    return ts.os_exact ? bpback_flags<false, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, reach, s)
+                       : bpback_flags<false, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, reach, s);
 }
 
 hipError_t launch_scatter3_tiled(bool cubic, int mode, const Geom& g, const TileSpec& ts, const void* src,
                                  const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
-                                 hipStream_t s) {
+                                 const float* reach, hipStream_t s) {
     if (mode == 0) {
         if (weights)
-            return cubic ? scatter_kp<true, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s)
-                         : scatter_kp<false, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-        return cubic ? scatter_kp<true, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
-                     : scatter_kp<false, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
+            return cubic ? scatter_kp<true, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s)
+                         : scatter_kp<false, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
+        return cubic ? scatter_kp<true, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s)
+                     : scatter_kp<false, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s);
     }
-    return cubic ? scatter_kp<true, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
-                 : scatter_kp<false, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
+    return cubic ? scatter_kp<true, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s)
+                 : scatter_kp<false, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s);
 }
 
 }  // namespace tp
