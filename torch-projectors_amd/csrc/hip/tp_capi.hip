@@ -4,17 +4,10 @@
 // reference (validate_projection_inputs, projection_utils.h:23-48, and the
 // per-op TORCH_CHECKs), derives the launch geometry, zero-fills the outputs
 // that are accumulated, and enqueues the kernels on the caller's stream.
-// Nothing is synchronised.  The only memory besides the caller's is a
-// 256-byte scratch area per (device, stream) that the tiled kernels' calls
-// use (the reach of their poses), allocated by the first such call on that
-// stream and kept for the life of the process.
+// Nothing is synchronised and nothing is allocated.
 #include <algorithm>
 #include <cmath>
-#include <map>
-#include <memory>
-#include <mutex>
 #include <string>
-#include <utility>
 
 #include "../../../include/torch_projectors_hip.h"
 #include "tp_launch.hh"
@@ -104,7 +97,7 @@ int64_t rec_box(int64_t n, double os) {
     return raw + (raw % 2);
 }
 
-// The fp32 3D operators run the tile-owner kernels for rotation poses.
+// The fp32 3D operators run the tile-owner kernels for tiled poses (pose_tiled3).
 // (Their per-wave sample queues pack a column index into 14 bits: n <= 32766.)
 bool use_tiles(int dim, int dtype, double os, int64_t n) {
     return dim == 3 && dtype == TP_F32 && os > 0.0 && std::isfinite(os) && n <= 32766;
@@ -126,12 +119,10 @@ tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
     const double grid_r = std::sqrt(2.0) * double(g.n / 2 + 1);
     double cutr = g.cut2 >= 0.0 ? std::sqrt(g.cut2) : grid_r;
     if (!std::isfinite(cutr) || cutr > grid_r) cutr = grid_r;
-    // the grids reach the samples of every tiled pose (singular values up to kScaleMax);
-    // launch_pose_reach gives each call the radius its own poses reach
+    // samples of rotations lie within rho_unit + 1; those of the other tiled poses (singular
+    // values up to kScaleMax) within rho, on a second, wider forward grid
     const double rho_unit = g.os * cutr * 1.001;
     const double rho = rho_unit * tp::kScaleMax + 1.0;
-    // forward grids: one for unit-scale poses (launched one tile per workgroup), one for
-    // enlarging poses (visited after it); tiles of both are aligned
     const int half_tiles = int(std::ceil((rho_unit + 3.0) / L));
     ts.nt = 2 * half_tiles;
     ts.org = -half_tiles * L;
@@ -156,6 +147,10 @@ tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
     ts.fc1 = std::min(ts.nt, (rc - ts.org) / L + 1);
     ts.fd0 = std::max(0, (-rc - ts.orgd) / tp::kTileEdgeD);
     ts.fd1 = std::min(ts.ntfd, (rc - ts.orgd) / tp::kTileEdgeD + 1);
+    ts.fc0_2 = std::max(0, (-rc - ts.org2) / L);
+    ts.fc1_2 = std::min(ts.nt2, (rc - ts.org2) / L + 1);
+    ts.fd0_2 = std::max(0, (-rc - ts.orgd2) / tp::kTileEdgeD);
+    ts.fd1_2 = std::min(ts.ntfd2, (rc - ts.orgd2) / tp::kTileEdgeD + 1);
     ts.sd0 = std::max(0, (-rc + half - 1) / tp::kScTD);
     ts.sd1 = std::min(ts.ntd, (rc + half - 1) / tp::kScTD + 1);
     ts.sr0 = std::max(0, (-rc + half - 1) / tp::kScTR);
@@ -164,15 +159,18 @@ tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
     const int64_t pk = 512;  // poses per range
     ts.ksplit = int(std::max<int64_t>(1, (g.P + pk - 1) / pk));
     ts.prange = int((g.P + ts.ksplit - 1) / ts.ksplit);
-    if (ts.ksplit == 1) ts.fc1 = ts.fc0 = ts.fd1 = ts.fd0 = ts.sd1 = ts.sd0 = ts.sr1 = ts.sr0 = ts.sc1 = 0;  // nothing to split
+    if (ts.ksplit == 1)  // nothing to split
+        ts.fc1 = ts.fc0 = ts.fd1 = ts.fd0 = ts.fc1_2 = ts.fc0_2 = ts.fd1_2 = ts.fd0_2 = ts.sd1 = ts.sd0 = ts.sr1 =
+            ts.sr0 = ts.sc1 = 0;
     ts.rho = float(rho);
     ts.rho_unit = float(rho_unit);
     ts.os = float(g.os);
     ts.inv_os = float(1.0 / g.os);
     ts.os_exact = double(float(g.os)) == g.os;
     ts.smax = float(g.os * (g.n + 2));
-    // Slack of the sample boxes: the row and half-plane bounds use the
-    // rotation's orthonormality (off by at most kRotationTol * |sc, sr| each),
+    // Slack of the sample boxes: the row and half-plane bounds of a rotation
+    // use its orthonormality (off by at most kRotationTol * |sc, sr| each), those
+    // of the other tiled poses their fp32 dual basis (relative error ~1e-6),
     // plus fp32 rounding of the bounds themselves.
     ts.eps = 0.01f + 2.0f * tp::kRotationTol * ts.smax;
     ts.kp_forw = poses_per_batch(L, ts.eps, g.os);
@@ -184,7 +182,7 @@ tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
     return ts;
 }
 
-// fp32 2D scatters take the tile-owner kernel (tp_tiled2d.hip) for rotation poses.
+// fp32 2D operators take the tile-owner kernels (tp_tiled2d.hip) for tiled poses (pose_tiled2).
 bool use_tiles2(int dim, int dtype, double os, int64_t n) {
     return dim == 2 && dtype == TP_F32 && os > 0.0 && std::isfinite(os) && n <= 32766;
 }
@@ -195,23 +193,24 @@ tp::TileSpec2 tile_spec2(const tp::Geom& g, bool cubic) {
     const double grid_r = std::sqrt(2.0) * double(g.n / 2 + 1);
     double cutr = g.cut2 >= 0.0 ? std::sqrt(g.cut2) : grid_r;
     if (!std::isfinite(cutr) || cutr > grid_r) cutr = grid_r;
+    // samples of rotations lie within rho_unit + 1, those of the other tiled poses within rho
     const double rho_unit = g.os * cutr * 1.001;
     const double rho = rho_unit * tp::kScaleMax + 1.0;
-    // tiles whose cells a tap can reach: |r| and c within rho plus the stencil
-    const double reach = std::min(rho + 3.0, double(g.N));
+    // tiles whose cells a tap can reach: |r| and c within the radius plus the stencil
     const int half = g.N / 2;
     const int ntr = (g.N + TR - 1) / TR, ntc = (g.H + TC - 1) / TC;
-    ts.kr0 = std::max(0, int(std::floor((-reach + half - 1) / TR)));
-    const int kr1 = std::min(ntr, int(std::floor((reach + half - 1) / TR)) + 1);
-    ts.nr = std::max(0, kr1 - ts.kr0);
-    ts.nc = std::min(ntc, int(std::floor(reach / TC)) + 1);
+    auto tiles_within = [&](double radius, int& kr0, int& nr, int& nc) {
+        const double reach = std::min(radius + 3.0, double(g.N));
+        kr0 = std::max(0, int(std::floor((-reach + half - 1) / TR)));
+        const int kr1 = std::min(ntr, int(std::floor((reach + half - 1) / TR)) + 1);
+        nr = std::max(0, kr1 - kr0);
+        nc = std::min(ntc, int(std::floor(reach / TC)) + 1);
+    };
+    tiles_within(rho_unit + 1.0, ts.kr0, ts.nr, ts.nc);
+    tiles_within(rho, ts.kr0_2, ts.nr_2, ts.nc_2);
     // Every pose reaches every tile of the disc: split the poses into ranges
     // until there are a few thousand work items, keeping >= 128 poses a range.
-    // (Counted over the tiles that unit-scale poses reach: the others are only
-    // worked on by calls with enlarging poses.)
-    const double reach_unit = std::min(rho_unit + 4.0, double(g.N));
-    const int64_t tiles = g.B * int64_t(std::min(ntr, int(std::floor(2.0 * reach_unit / TR)) + 2)) *
-                          std::min(ntc, int(std::floor(reach_unit / TC)) + 1);
+    const int64_t tiles = g.B * int64_t(ts.nr) * ts.nc;
     const int64_t want = tiles > 0 ? (4096 + tiles - 1) / tiles : 1;
     const int64_t most = std::max<int64_t>(1, g.P / 128);
     ts.ksplit = int(std::max<int64_t>(1, std::min(want, most)));
@@ -230,13 +229,14 @@ tp::TileSpec2 tile_spec2(const tp::Geom& g, bool cubic) {
     ts.cmax = std::min(g.n / 2, cl);
     ts.rmin = std::max(g.n / 2 + 1 - g.n, -cl);
     ts.rmax = std::min(g.n / 2, cl);
-    // gather: square tiles over the signed plane |x| <= rho (+2), pose ranges as the scatter
+    // gather: square tiles over the signed plane within the radius (+2), pose ranges as the scatter
     constexpr int GT = tp::kGat2;
-    const int half_g = int(std::ceil((rho + 2.0) / GT));
+    const int half_g = int(std::ceil((rho_unit + 3.0) / GT)), half_g2 = int(std::ceil((rho + 2.0) / GT));
     ts.gnt = 2 * half_g;
     ts.gorg = -half_g * GT;
-    const int64_t gunit = 2 * int64_t(std::ceil((rho_unit + 3.0) / GT));
-    const int64_t gtiles = g.B * std::min<int64_t>(ts.gnt, gunit) * std::min<int64_t>(ts.gnt, gunit);
+    ts.gnt2 = 2 * half_g2;
+    ts.gorg2 = -half_g2 * GT;
+    const int64_t gtiles = g.B * int64_t(ts.gnt) * ts.gnt;
     const int64_t gwant = gtiles > 0 ? (4096 + gtiles - 1) / gtiles : 1;
     ts.gksplit = int(std::max<int64_t>(1, std::min(gwant, most)));
     ts.gprange = int((g.P + ts.gksplit - 1) / ts.gksplit);
@@ -268,47 +268,6 @@ int need(const void* p, const char* name) {
 
 int launched(hipError_t e, const char* what) { return e == hipSuccess ? TP_OK : hip_fail(e, what); }
 
-// Scratch of the calls on one (device, stream): the reach word of
-// tp::launch_pose_reach.  Calls on one stream run in order on the GPU, so they
-// share it; `busy` is held while one call enqueues its kernels, so that calls
-// from several host threads on one stream do not interleave them.
-struct StreamScratch {
-    float* p = nullptr;
-    std::mutex busy;
-};
-std::mutex g_scratch_mu;
-std::map<std::pair<int, hipStream_t>, std::unique_ptr<StreamScratch>> g_scratch;
-
-struct CallScratch {
-    float* p = nullptr;
-    std::unique_lock<std::mutex> hold;
-    int get(hipStream_t st) {
-        if (p) return TP_OK;  // a call takes it once
-        int dev = 0;
-        TP_TRY(launched(hipGetDevice(&dev), "hipGetDevice"));
-        StreamScratch* e;
-        {
-            std::lock_guard<std::mutex> lk(g_scratch_mu);
-            std::unique_ptr<StreamScratch>& slot = g_scratch[{dev, st}];
-            if (!slot) {
-                std::unique_ptr<StreamScratch> fresh(new StreamScratch);
-                TP_TRY(launched(hipMalloc(reinterpret_cast<void**>(&fresh->p), 256), "scratch allocation"));
-                slot = std::move(fresh);
-            }
-            e = slot.get();
-        }
-        hold = std::unique_lock<std::mutex>(e->busy);
-        p = e->p;
-        return TP_OK;
-    }
-};
-
-// The reach of the call's tiled poses into the scratch word (the tiled kernels skip tiles beyond it).
-int pose_reach(int dim, const tp::Geom& g, const void* rot, float rho_unit, CallScratch& sc, hipStream_t s) {
-    TP_TRY(sc.get(s));
-    return launched(tp::launch_pose_reach(dim, g.B_rot * g.P, rot, rho_unit, sc.p, s), "pose reach launch");
-}
-
 // TP_F16S: the volume is stored as complex half; it is widened exactly to
 // fp32 on load and everything else (poses, arithmetic, projections) is the
 // TP_F32 path.
@@ -333,23 +292,19 @@ int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int6
     TP_TRY(need(out, "projections"));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool cubic = interp == TP_CUBIC;
-    CallScratch sc;
     if (use_tiles(dim, dt, os, n)) {
-        const tp::TileSpec ts = tile_spec(g, cubic);
-        TP_TRY(pose_reach(3, g, rot, ts.rho_unit, sc, s));
-        TP_TRY(launched(tp::launch_project3_forw_tiled(cubic, g, ts, rec, rot, shifts, out, sc.p, s, rec_half),
+        TP_TRY(launched(tp::launch_project3_forw_tiled(cubic, g, tile_spec(g, cubic), rec, rot, shifts, out, s,
+                                                       rec_half),
                         "tiled projection launch"));
         return launched(tp::launch_project_forw(dim, kdt, cubic, g, rec, rot, shifts, out, s, true),
                         "projection launch");
     }
     if (use_tiles2(dim, dt, os, n)) {
-        // zero-fill first: the tiled gather writes the active pixels of rotation poses, the
+        // zero-fill first: the tiled gather writes the active pixels of tiled poses, the
         // rest kernel the other poses
         TP_TRY(zero(out, cx_words(dt, g.B * g.P * int64_t(g.npix)), s));
-        const tp::TileSpec2 ts = tile_spec2(g, cubic);
-        TP_TRY(pose_reach(2, g, rot, ts.rho_unit, sc, s));
-        TP_TRY(launched(tp::launch_gather2_tiled(cubic, 0, g, ts, rec, nullptr, rot, shifts, out, nullptr, nullptr,
-                                                 nullptr, nullptr, sc.p, s, rec_half),
+        TP_TRY(launched(tp::launch_gather2_tiled(cubic, 0, g, tile_spec2(g, cubic), rec, nullptr, rot, shifts, out,
+                                                 nullptr, nullptr, nullptr, nullptr, s, rec_half),
                         "tiled projection launch"));
         return launched(tp::launch_project_forw(dim, kdt, cubic, g, rec, rot, shifts, out, s, true),
                         "projection launch");
@@ -382,24 +337,19 @@ int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, in
     TP_TRY(need(gproj, "grad_projections"));
     TP_TRY(need(rec, "reconstruction"));
     TP_TRY(need(rot, "rotations"));
-    CallScratch sc;
     if (tiles) {
         const tp::TileSpec ts = tile_spec(g, cubic);
-        TP_TRY(pose_reach(3, g, rot, ts.rho_unit, sc, s));
-        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, sc.p,
-                                                  s),
+        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, s),
                         "tiled reconstruction-gradient launch"));
-        TP_TRY(launched(tp::launch_grads3_tiled(cubic, g, ts, gproj, rec, rot, shifts, grot, gshift, sc.p, s),
+        TP_TRY(launched(tp::launch_grads3_tiled(cubic, g, ts, gproj, rec, rot, shifts, grot, gshift, s),
                         "tiled rotation/shift-gradient launch"));
     }
     if (tiles2) {
         const tp::TileSpec2 ts = tile_spec2(g, cubic);
-        TP_TRY(pose_reach(2, g, rot, ts.rho_unit, sc, s));
-        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, sc.p,
-                                                  s),
+        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, s),
                         "tiled reconstruction-gradient launch"));
         TP_TRY(launched(tp::launch_gather2_tiled(cubic, 1, g, ts, rec, nullptr, rot, shifts, nullptr, nullptr, gproj,
-                                                 grot, gshift, sc.p, s),
+                                                 grot, gshift, s),
                         "tiled rotation/shift-gradient launch"));
     }
     return launched(tp::launch_project_back(dim, dtype, cubic, g, gproj, rec, rot, shifts, grec, grot, gshift, s,
@@ -433,19 +383,14 @@ int backproject_forw(int dim, int dtype, const void* proj, int64_t B, int64_t P,
     if (g.work == 0) return TP_OK;
     TP_TRY(need(proj, "projections"));
     TP_TRY(need(rot, "rotations"));
-    CallScratch sc;
-    if (tiles) {
-        const tp::TileSpec ts = tile_spec(g, cubic);
-        TP_TRY(pose_reach(3, g, rot, ts.rho_unit, sc, s));
-        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 0, g, ts, proj, weights, rot, shifts, data, wrec, sc.p, s),
+    if (tiles)
+        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 0, g, tile_spec(g, cubic), proj, weights, rot, shifts, data, wrec,
+                                                  s),
                         "tiled backprojection launch"));
-    }
-    if (tiles2) {
-        const tp::TileSpec2 ts = tile_spec2(g, cubic);
-        TP_TRY(pose_reach(2, g, rot, ts.rho_unit, sc, s));
-        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 0, g, ts, proj, weights, rot, shifts, data, wrec, sc.p, s),
+    if (tiles2)
+        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 0, g, tile_spec2(g, cubic), proj, weights, rot, shifts, data,
+                                                  wrec, s),
                         "tiled backprojection launch"));
-    }
     return launched(
         tp::launch_backproject_forw(dim, dtype, cubic, g, proj, weights, rot, shifts, data, wrec, s, tiles || tiles2),
         "backprojection launch");
@@ -476,25 +421,18 @@ int backproject_back(int dim, int dtype, const void* gdata, const void* gw, int6
     const bool tiles2 = use_tiles2(dim, dtype, os, n);
     const bool tiles = use_tiles(dim, dtype, os, n);
     if (tiles2 || tiles) {
-        // the tiled gathers write the active pixels of rotation poses, the per-pixel kernel the rest
+        // the tiled gathers write the active pixels of tiled poses, the per-pixel kernel the rest
         TP_TRY(zero(gproj, cx_words(dtype, g.B * g.P * int64_t(g.npix)), s));
         TP_TRY(zero(gweights, re_words(dtype, g.B * g.P * int64_t(g.npix)), s));
     }
-    CallScratch sc;
-    if (tiles) {
-        const tp::TileSpec ts = tile_spec(g, cubic);
-        TP_TRY(pose_reach(3, g, rot, ts.rho_unit, sc, s));
-        TP_TRY(launched(tp::launch_bpback3_tiled(cubic, g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
-                                                 gshift, sc.p, s),
+    if (tiles)
+        TP_TRY(launched(tp::launch_bpback3_tiled(cubic, g, tile_spec(g, cubic), gdata, gw, proj, rot, shifts, gproj,
+                                                 gweights, grot, gshift, s),
                         "tiled backprojection backward launch"));
-    }
-    if (tiles2) {
-        const tp::TileSpec2 ts = tile_spec2(g, cubic);
-        TP_TRY(pose_reach(2, g, rot, ts.rho_unit, sc, s));
-        TP_TRY(launched(tp::launch_gather2_tiled(cubic, 2, g, ts, gdata, gw, rot, shifts, gproj,
-                                                 (gw && gweights) ? gweights : nullptr, proj, grot, gshift, sc.p, s),
+    if (tiles2)
+        TP_TRY(launched(tp::launch_gather2_tiled(cubic, 2, g, tile_spec2(g, cubic), gdata, gw, rot, shifts, gproj,
+                                                 (gw && gweights) ? gweights : nullptr, proj, grot, gshift, s),
                         "tiled backprojection backward launch"));
-    }
     return launched(tp::launch_backproject_back(dim, dtype, cubic, g, gdata, gw, proj, rot, shifts, gproj, gweights,
                                                 grot, gshift, s, tiles2 || tiles),
                     "backprojection backward launch");

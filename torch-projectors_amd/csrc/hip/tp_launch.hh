@@ -40,9 +40,10 @@ constexpr int kScTC = 16, kScTR = 8, kScTD = 12;        // scatter tiles (c, r, 
 struct TileSpec {
     int nt, org;              // forward: tiles along c and r, and the signed origin of the grid there,
                               // laid out for unit-scale poses (|x| <= rho_unit + 1)
-    int nt2, org2, ntfd2, orgd2;  // forward: the same for the grid that enlarging poses reach (|x| <= rho)
     int fc0, fc1;             // forward core tiles (split by pose range): [fc0, fc1) along c and r
     int ntfd, orgd, fd0, fd1;  // forward: the same along d (tiles of kTileEdgeD)
+    int nt2, org2, ntfd2, orgd2;  // forward: the grid that the other tiled poses reach (|x| <= rho)
+    int fc0_2, fc1_2, fd0_2, fd1_2;  // and its core tiles (the same voxels as fc0.. fd1)
     int ntd, ntr, ntc;        // scatter: tiles along d, r, c of the stored half volume
     int sd0, sd1, sr0, sr1, sc1;  // scatter core tiles: [sd0, sd1) x [sr0, sr1) x [0, sc1)
     int ksplit, prange;       // pose ranges per core tile, poses per range
@@ -60,7 +61,8 @@ struct TileSpec {
 constexpr int kTile2C = 32, kTile2R = 16;  // scatter tile edges (c, r): fp64 accumulators
 constexpr int kGat2 = 32;                  // gather tile edge (c and r)
 struct TileSpec2 {
-    int kr0, nr, nc;        // tiles that samples can reach: rows [kr0, kr0 + nr), columns [0, nc)
+    int kr0, nr, nc;        // tiles that rotations' taps reach: rows [kr0, kr0 + nr), columns [0, nc)
+    int kr0_2, nr_2, nc_2;  // the same for the other tiled poses
     int ksplit, prange;     // pose ranges per tile, poses per range
     int kp;                 // poses per wavefront batch (1, 2 or 4)
     float rho;              // bound on |x| of every active sample of a tiled pose (singular values <= kScaleMax)
@@ -69,7 +71,8 @@ struct TileSpec2 {
     float os, inv_os;       // oversampling and its inverse
     float smax;             // bound on |c*os| over the pixel grid
     int cmax, rmin, rmax;   // pixel-grid limits of c and r (grid and cutoff)
-    int gnt, gorg;          // gather: tiles per axis over the signed plane, and its origin
+    int gnt, gorg;          // gather: tiles per axis over the signed plane, and its origin (rotations)
+    int gnt2, gorg2;        // gather: the same for the other tiled poses
     int gksplit, gprange;   // gather: pose ranges per tile, poses per range
     int kp_gather;          // gather (forward): poses per wavefront batch
 };
@@ -85,57 +88,52 @@ hipError_t launch_zero(void* p, int64_t words, hipStream_t s);
 // (out complex, wout real; either may be null).
 hipError_t launch_zero_outside(int dt, const Geom& g, void* out, void* wout, hipStream_t s);
 
-// Reach of one call's tiled poses: out[0] = rho_unit * (largest singular value
-// over the B_rot * P poses that take the tiled kernels) + 1, or 0 when none
-// does.  The tiled kernels skip the tiles beyond it (their grids are laid out
-// for singular values up to kScaleMax).  `out` is a device scratch word.
-hipError_t launch_pose_reach(int dim, int64_t poses, const void* rot, float rho_unit, float* out, hipStream_t s);
-
 // Kernel launchers; `dim` is 2 or 3, `dt` 0 (fp32) or 1 (fp64); launch_project_forw
 // also takes `dt` 2: a complex-half volume with fp32 arithmetic and output.
-// `rest_only` (fp32): only masked pixels and poses that are not rotations.
+// `rest_only` (fp32): only masked pixels and the poses that the tiled kernels
+// do not take (pose_tiled3 / pose_tiled2).
 hipError_t launch_project_forw(int dim, int dt, bool cubic, const Geom& g, const void* rec, const void* rot,
                                const void* shifts, void* out, hipStream_t s, bool rest_only = false);
-// `rest` != 0 (fp32): poses that are rotations are left to the tiled kernels
+// `rest` != 0 (fp32): tiled poses are left to the tiled kernels
 // entirely (the tiled scatter gives their reconstruction gradient,
 // launch_grads3_tiled / launch_gather2_tiled their rotation/shift gradients).
 hipError_t launch_project_back(int dim, int dt, bool cubic, const Geom& g, const void* gproj, const void* rec,
                                const void* rot, const void* shifts, void* grec, void* grot, void* gshift,
                                hipStream_t s, int rest = 0);
-// `rest_only` (fp32 2D and 3D): only poses that are not rotations.
+// `rest_only` (fp32 2D and 3D): only the poses that the tiled kernels do not take.
 hipError_t launch_backproject_forw(int dim, int dt, bool cubic, const Geom& g, const void* proj, const void* weights,
                                    const void* rot, const void* shifts, void* data, void* wrec, hipStream_t s,
                                    bool rest_only = false);
 // fp32 3D tile-owner paths (tiled poses only; the per-pixel kernels with
-// `rest_only` complete the other poses and the masked pixels).  `reach`: the
-// device word written by launch_pose_reach for this call.  `rec_half`:
-// the volume is stored as complex half and widened to fp32 on load.
+// `rest_only` complete the other poses and the masked pixels).  Each launches
+// the rotation kernel and then the kernel of the other tiled poses.
+// `rec_half`: the volume is stored as complex half and widened to fp32 on load.
 hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* rec,
-                                      const void* rot, const void* shifts, void* out, const float* reach, hipStream_t s,
+                                      const void* rot, const void* shifts, void* out, hipStream_t s,
                                       bool rec_half = false);
-// Rotation/shift gradients of project_3d_to_2d_back for rotation poses, added
+// Rotation/shift gradients of project_3d_to_2d_back for tiled poses, added
 // into zero-filled grot / gshift (either may be null).
 hipError_t launch_grads3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gproj, const void* rec,
-                               const void* rot, const void* shifts, void* grot, void* gshift, const float* reach, hipStream_t s);
-// backproject_2d_to_3d_back for rotation poses into zero-filled outputs:
+                               const void* rot, const void* shifts, void* grot, void* gshift, hipStream_t s);
+// backproject_2d_to_3d_back for tiled poses into zero-filled outputs:
 // grad_projections from grad_data_rec, grad_weights from grad_weight_rec (when
 // both gw and gweights are given), rotation/shift gradients (either may be null).
 hipError_t launch_bpback3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gdata, const void* gw,
                                 const void* proj, const void* rot, const void* shifts, void* gproj, void* gweights,
-                                void* grot, void* gshift, const float* reach, hipStream_t s);
+                                void* grot, void* gshift, hipStream_t s);
 // mode 0: backprojection into data (+ weights), with the x = 0 Hermitian completion;
 // mode 1: reconstruction gradient of the projection.
 hipError_t launch_scatter3_tiled(bool cubic, int mode, const Geom& g, const TileSpec& ts, const void* src,
                                  const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
-                                 const float* reach, hipStream_t s);
+                                 hipStream_t s);
 
-// fp32 2D tile-owner scatter (rotation poses only), into zero-filled dst / wdst.
+// fp32 2D tile-owner scatter (tiled poses only), into zero-filled dst / wdst.
 // mode 0: backprojection with the x = 0 Hermitian completion; mode 1:
 // reconstruction gradient of the projection.
 hipError_t launch_scatter2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* src,
                                  const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
-                                 const float* reach, hipStream_t s);
-// fp32 2D tile-owner gathers (rotation poses only; the per-pixel kernels with
+                                 hipStream_t s);
+// fp32 2D tile-owner gathers (tiled poses only; the per-pixel kernels with
 // `rest` complete the other poses and the masked pixels).  mode 0: forward
 // (rec -> out); mode 1: rotation/shift gradients of project_2d_back (gsrc =
 // grad_projections) into zero-filled grot / gshift; mode 2:
@@ -144,7 +142,7 @@ hipError_t launch_scatter2_tiled(bool cubic, int mode, const Geom& g, const Tile
 // `rec_half` (mode 0): the volume is stored as complex half and widened to fp32 on load.
 hipError_t launch_gather2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* rec,
                                 const void* gw, const void* rot, const void* shifts, void* out, void* wout,
-                                const void* gsrc, void* grot, void* gshift, const float* reach, hipStream_t s, bool rec_half = false);
+                                const void* gsrc, void* grot, void* gshift, hipStream_t s, bool rec_half = false);
 
 // Reference preparation (tp_fourier.hip).  Elements are opaque words of
 // elem_bytes (2, 4, 8 or 16); `dim` spatial axes (2 or 3) after the batch.
@@ -164,7 +162,7 @@ hipError_t launch_normalize(int dt, const void* data, const void* weights, int64
 int fft_forward(int dt, int dim, int64_t batch, int64_t N, const void* real, void* spec, hipStream_t s);
 int fft_inverse(int dt, int dim, int64_t batch, int64_t N, void* spec, void* real, hipStream_t s);
 
-// `rest_only` (fp32): rotation poses were computed by the tiled gathers into
+// `rest_only` (fp32): tiled poses were computed by the tiled gathers into
 // zero-filled outputs and are skipped; other poses everything.
 hipError_t launch_backproject_back(int dim, int dt, bool cubic, const Geom& g, const void* gdata, const void* gw,
                                    const void* proj, const void* rot, const void* shifts, void* gproj,

@@ -22,9 +22,13 @@
 //
 // Poses whose 2x2 matrix has singular values in [kScaleMin, kScaleMax]
 // (pose_tiled2: rotations, and scaled or sheared matrices) take this path;
-// the per-pixel kernels scatter the others.  A sample x = R (sc, sr) of such
-// a pose has sc = as . x and sr = bs . x with the dual basis (the rows of
-// R^-1), which bounds the rows and the half plane sc >= 0 that reach a box.
+// the per-pixel kernels scatter the others.  Each kernel comes in two
+// instantiations: GEN = false takes the rotations, GEN = true (launched
+// after it on a small persistent grid that exits at once when the call has
+// no such pose) the other tiled matrices.  A sample x = R (sc, sr) of those
+// has sc = as . x and sr = bs . x with the dual basis (the rows of R^-1),
+// which bounds the rows and the half plane sc >= 0 that reach a box; their
+// tiles reach up to kScaleMax times farther out.
 #include <type_traits>
 
 #include "tp_device.hh"
@@ -58,28 +62,30 @@ __device__ __forceinline__ bool half_plane_hits2(const float* as, const float* l
     return u >= 0.f;
 }
 
-// Pose-list entries: the pose index relative to its phase, and kGen2 when the
-// pose is not a rotation (box_rows2 then needs its dual basis).
-constexpr unsigned kGen2 = 1u << 13, kPose2Mask = kGen2 - 1;
-static_assert(2 * kChunk2 <= int(kPose2Mask) + 1 && 2048 <= int(kPose2Mask) + 1, "pose index must fit the entries");
-
-// Tiled pose whose half plane reaches the box (as of half_plane_hits2, from R);
-// `general`: not a rotation.
-__device__ __forceinline__ bool pose_hits2(const float* R, const float* lo, const float* hi, bool& general) {
+// Is the pose of this instantiation's class (rotation, or GEN: another tiled
+// matrix)?  `as` receives the half-plane vector (column 0, or its dual).
+template <bool GEN>
+__device__ __forceinline__ bool pose_of_class2(const float* R, float* as) {
     const PoseGram gr = pose_gram2(R);
-    general = !gram_is_rotation(gr);
-    if (general && !gram_tiled(gr)) return false;
-    float as[2] = {R[0], R[2]}, bs[2];
-    if (general) pose_dual2(R, gr, as, bs);
-    return half_plane_hits2(as, lo, hi);
+    if constexpr (GEN) {
+        if (gram_is_rotation(gr) || !gram_tiled(gr)) return false;
+        float bs[2];
+        pose_dual2(R, gr, as, bs);
+        return true;
+    } else {
+        as[0] = R[0];
+        as[1] = R[2];
+        return gram_is_rotation(gr);
+    }
 }
 
-// Rows r (sr = r*os = bs . x) whose samples can lie in the box.  A rotation's
-// bs is its column 1; other poses (`general`) compute their dual basis.
-__device__ __forceinline__ void box_rows2(const float* R, bool general, const float* lo, const float* hi,
-                                          const TileSpec2& ts, int& r0, int& r1) {
+// Rows r (sr = r*os = bs . x) whose samples can lie in the box: bs is a
+// rotation's column 1, or (GEN) the dual basis vector.
+template <bool GEN>
+__device__ __forceinline__ void box_rows2(const float* R, const float* lo, const float* hi, const TileSpec2& ts,
+                                          int& r0, int& r1) {
     float as[2], bs[2] = {R[1], R[3]};
-    if (general) pose_dual2(R, pose_gram2(R), as, bs);
+    if constexpr (GEN) pose_dual2(R, pose_gram2(R), as, bs);
     float vlo = 0.f, vhi = 0.f;
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -134,6 +140,7 @@ __device__ __forceinline__ void load_pose2(const float* __restrict__ rotb, const
 
 // Cull poses [pbase, pend) (at most kChunk2) against box 1 and box 2.  Box-1
 // survivors fill plist from the front, box-2 survivors from the back.
+template <bool GEN>
 __device__ __forceinline__ void cull2(const float* __restrict__ rotb, int pend, int pbase, const float* lo1,
                                       const float* hi1, const float* lo2, const float* hi2, unsigned short* plist,
                                       int* pcnt, int& n1, int& n2) {
@@ -153,14 +160,11 @@ __device__ __forceinline__ void cull2(const float* __restrict__ rotb, int pend, 
 #pragma unroll
         for (int q = 0; q < kInFlight; ++q) {
             const int p = pbase + int(threadIdx.x) + (q0 + q) * kThreads;
-            const PoseGram gr = pose_gram2(R[q]);
-            const bool general = !gram_is_rotation(gr);
-            if (p >= pend || (general && !gram_tiled(gr))) continue;
-            float as[2] = {R[q][0], R[q][2]}, bs[2];
-            if (general) pose_dual2(R[q], gr, as, bs);
-            const unsigned short e = (unsigned short)((p - pbase) | (general ? kGen2 : 0u));
-            if (half_plane_hits2(as, lo1, hi1)) plist[atomicAdd(&pcnt[0], 1)] = e;
-            if (half_plane_hits2(as, lo2, hi2)) plist[2 * kChunk2 - 1 - atomicAdd(&pcnt[1], 1)] = e;
+            float as[2];
+            if (p >= pend || !pose_of_class2<GEN>(R[q], as)) continue;
+            if (half_plane_hits2(as, lo1, hi1)) plist[atomicAdd(&pcnt[0], 1)] = (unsigned short)(p - pbase);
+            if (half_plane_hits2(as, lo2, hi2))
+                plist[2 * kChunk2 - 1 - atomicAdd(&pcnt[1], 1)] = (unsigned short)(p - pbase);
         }
     }
     __syncthreads();
@@ -301,13 +305,12 @@ __device__ __forceinline__ void scatter_sample2_priv(const Geom& g, const Slot2&
 // PRIV (one pose per window, KP = 1, os > sqrt(2) with margin): wave-private
 // fp32 accumulators without atomics, summed over the waves at write-out;
 // otherwise one fp64 accumulator per tile with LDS atomics.
-template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool PRIV = false>
+template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool PRIV, bool GEN>
 __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 ts, const Cx<float>* __restrict__ src,
                                                              const float* __restrict__ weights,
                                                              const float* __restrict__ rot,
                                                              const float* __restrict__ shifts,
-                                                             Cx<float>* __restrict__ dst, float* __restrict__ wdst,
-                                                             const float* __restrict__ reach) {
+                                                             Cx<float>* __restrict__ dst, float* __restrict__ wdst) {
     constexpr int SL = CUBIC ? 2 : 1, SH = CUBIC ? 1 : 0;  // stencil reach below / above floor(x)
     constexpr int SLOW = CUBIC ? 1 : 0;                    // first tap at floor(x) - SLOW
     constexpr int RPS = 64 / KP;
@@ -322,21 +325,29 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
     __shared__ int pcnt[2];
     __shared__ Slot2 slots[NW][KP];
     __shared__ int marks[NW][64];
+    __shared__ int part[NW];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slot = lane / RPS, jrow = lane % RPS;
     const int N = g.N, H = g.H, half = N / 2;
-    const int64_t items = g.B * ts.ksplit * int64_t(ts.nr) * ts.nc;
+    // samples lie within |x| <= rho_k: rotations reach rho_unit + 1, GEN poses up to kScaleMax
+    // times farther (the call's own largest singular value), over a wider range of tiles
+    float rho_k = ts.rho_unit + 1.0f;
+    if constexpr (GEN) {
+        rho_k = fminf(ts.rho, general_reach<2, kThreads>(rot, g.B_rot * g.P, ts.rho_unit, part));
+        if (rho_k <= 0.f) return;  // no such pose in this call
+    }
+    const int tkr0 = GEN ? ts.kr0_2 : ts.kr0, tnr = GEN ? ts.nr_2 : ts.nr, tnc = GEN ? ts.nc_2 : ts.nc;
+    const int64_t items = g.B * ts.ksplit * int64_t(tnr) * tnc;
     const float cut2 = float(g.cut2);
-    const float rho_k = fminf(ts.rho, *reach);  // tiles beyond the call's reach hold no sample
     const int64_t per = xcd_per<kRun>(items);
     for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
         const int64_t w = xcd_item<kRun>(slot_i);
         if (w >= items) continue;
         // items: tile column fastest, then tile row, pose range, batch
-        const int kc = int(w % ts.nc);
-        int64_t q = w / ts.nc;
-        const int kr = ts.kr0 + int(q % ts.nr);
-        q /= ts.nr;
+        const int kc = int(w % tnc);
+        int64_t q = w / tnc;
+        const int kr = tkr0 + int(q % tnr);
+        q /= tnr;
         const int jr = int(q % ts.ksplit);
         const int64_t b = q / ts.ksplit;
         const int p0 = jr * ts.prange, p1 = min(int(g.P), p0 + ts.prange);
@@ -375,12 +386,11 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
 
         for (int pbase = p0; pbase < pend; pbase += kChunk2) {
             int n1, n2;
-            cull2(rotb, pend, pbase, lo1, hi1, lo2, hi2, plist, pcnt, n1, n2);
+            cull2<GEN>(rotb, pend, pbase, lo1, hi1, lo2, hi2, plist, pcnt, n1, n2);
 #pragma unroll 1
             for (int pass = 0; pass < 2; ++pass) {
                 const int np = pass == 0 ? n1 : n2;
-                auto entry_at = [&](int k) { return unsigned(plist[pass == 0 ? k : 2 * kChunk2 - 1 - k]); };
-                auto pose_at = [&](int k) { return pbase + int(entry_at(k) & kPose2Mask); };
+                auto pose_at = [&](int k) { return pbase + int(plist[pass == 0 ? k : 2 * kChunk2 - 1 - k]); };
                 float lo[2], hi[2];
 #pragma unroll
                 for (int k = 0; k < 2; ++k) {
@@ -400,8 +410,7 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
                 if (base < np) load_pose2(rotb, shb, pose_at(min(base + slot, np - 1)), Rn, Sn);
                 for (; base < np; base += NW * KP) {
                     const bool sv = base + slot < np;
-                    const unsigned pe = entry_at(min(base + slot, np - 1));
-                    const int pp = pbase + int(pe & kPose2Mask);
+                    const int pp = pose_at(min(base + slot, np - 1));
                     float R[4], Sh[2];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) R[e] = Rn[e];
@@ -419,7 +428,7 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
                     }
                     __builtin_amdgcn_wave_barrier();
                     int r0, r1;
-                    box_rows2(R, (pe & kGen2) != 0, lo, hi, ts, r0, r1);
+                    box_rows2<GEN>(R, lo, hi, ts, r0, r1);
                     const int nr = sv ? max(0, r1 - r0 + 1) : 0;
                     const int maxnr = wave_max(nr);
                     for (int rbase = 0; rbase < maxnr; rbase += RPS) {
@@ -546,37 +555,52 @@ __global__ __launch_bounds__(kBlock) void k_mirror2_x0(Geom g, Cx<float>* __rest
     }
 }
 
-template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool PRIV = false>
-hipError_t scatter2_launch(const Geom& g, const TileSpec2& ts, const void* src, const void* weights,
-                           const void* rot, const void* shifts, void* dst, void* wdst, const float* reach, hipStream_t s) {
-    const int64_t work = g.B * ts.ksplit * int64_t(ts.nr) * ts.nc;
-    if (work > 0) {
-        hipLaunchKernelGGL((k_scatter2_tiled<CUBIC, MODE, WEIGHTS, KP, PRIV>),
-                           dim3(grid_for(kXcds * xcd_per<kRun>(work))),
-                           dim3(kThreads), 0, s, g, ts, (const Cx<float>*)src, (const float*)weights,
-                           (const float*)rot, (const float*)shifts, (Cx<float>*)dst, (float*)wdst, reach);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-    }
-    if (MODE != 0) return hipSuccess;
+// Workgroups of a launch over `items`: one per item (rotations), or the persistent GEN grid.
+template <bool GEN>
+unsigned grid2_of(int64_t items) {
+    const int64_t slots = kXcds * xcd_per<kRun>(items);
+    return grid_for(GEN && slots > kGenGrid ? kGenGrid : slots);
+}
+
+template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool PRIV, bool GEN>
+hipError_t scatter2_one(const Geom& g, const TileSpec2& ts, const void* src, const void* weights, const void* rot,
+                        const void* shifts, void* dst, void* wdst, hipStream_t s) {
+    const int64_t work = g.B * ts.ksplit * (GEN ? int64_t(ts.nr_2) * ts.nc_2 : int64_t(ts.nr) * ts.nc);
+    if (work == 0) return hipSuccess;
+    hipLaunchKernelGGL((k_scatter2_tiled<CUBIC, MODE, WEIGHTS, KP, PRIV, GEN>), dim3(grid2_of<GEN>(work)),
+                       dim3(kThreads), 0, s, g, ts, (const Cx<float>*)src, (const float*)weights, (const float*)rot,
+                       (const float*)shifts, (Cx<float>*)dst, (float*)wdst);
+    return hipGetLastError();
+}
+
+// Poses per wave batch, and wave-private accumulation: one pose per window keeps a window's
+// samples >= os * (smallest singular value) apart (less rounding), beyond sqrt(2) (the diagonal
+// of a cell) when that is 1.5 or more.
+template <bool CUBIC, int MODE, bool WEIGHTS, bool GEN>
+hipError_t scatter2_kp(const Geom& g, const TileSpec2& ts, const void* src, const void* weights, const void* rot,
+                       const void* shifts, void* dst, void* wdst, hipStream_t s) {
+    if (g.os * (GEN ? kScaleMin : 1.0) >= kPrivOs)
+        return scatter2_one<CUBIC, MODE, WEIGHTS, 1, true, GEN>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    if (ts.kp >= 4) return scatter2_one<CUBIC, MODE, WEIGHTS, 4, false, GEN>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    if (ts.kp == 2) return scatter2_one<CUBIC, MODE, WEIGHTS, 2, false, GEN>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    return scatter2_one<CUBIC, MODE, WEIGHTS, 1, false, GEN>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+}
+
+// Rotations, then the other tiled poses (both add into the zero-filled image), then the
+// x = 0 completion of the backprojection.
+template <bool CUBIC, int MODE, bool WEIGHTS>
+hipError_t scatter2_all(const Geom& g, const TileSpec2& ts, const void* src, const void* weights, const void* rot,
+                        const void* shifts, void* dst, void* wdst, hipStream_t s) {
+    hipError_t e = scatter2_kp<CUBIC, MODE, WEIGHTS, false>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    if (e != hipSuccess) return e;
+    e = scatter2_kp<CUBIC, MODE, WEIGHTS, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    if (e != hipSuccess || MODE != 0) return e;
     int64_t blocks = (g.B * g.N + kBlock - 1) / kBlock;
     if (blocks > 65536) blocks = 65536;
     if (blocks < 1) return hipSuccess;
     hipLaunchKernelGGL(k_mirror2_x0<WEIGHTS>, dim3(unsigned(blocks)), dim3(kBlock), 0, s, g, (Cx<float>*)dst,
                        (float*)wdst);
     return hipGetLastError();
-}
-
-template <bool CUBIC, int MODE, bool WEIGHTS>
-hipError_t scatter2_kp(const Geom& g, const TileSpec2& ts, const void* src, const void* weights, const void* rot,
-                       const void* shifts, void* dst, void* wdst, const float* reach, hipStream_t s) {
-    // one pose per window keeps a window's samples >= os * kScaleMin (less rounding) apart,
-    // beyond sqrt(2) (the diagonal of a cell) when that is 1.5 or more
-    if (g.os * kScaleMin >= kPrivOs)
-        return scatter2_launch<CUBIC, MODE, WEIGHTS, 1, true>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
-    if (ts.kp >= 4) return scatter2_launch<CUBIC, MODE, WEIGHTS, 4>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
-    if (ts.kp == 2) return scatter2_launch<CUBIC, MODE, WEIGHTS, 2>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
-    return scatter2_launch<CUBIC, MODE, WEIGHTS, 1>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
 }
 
 // ----------------------------------------------------------------------------- gather
@@ -634,15 +658,14 @@ __device__ __forceinline__ Interp<float> cubic2_grads(F&& fetch, float r, float 
     return o;
 }
 
-template <bool CUBIC, int KP, int GMODE, bool RS, bool WG, typename VS = float>
+template <bool CUBIC, int KP, int GMODE, bool RS, bool WG, typename VS, bool GEN>
 __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts, const Cx<VS>* __restrict__ rec,
                                                             const float* __restrict__ gw,
                                                             const float* __restrict__ rot,
                                                             const float* __restrict__ shifts,
                                                             Cx<float>* __restrict__ out, float* __restrict__ wout,
                                                             const Cx<float>* __restrict__ gsrc,
-                                                            float* __restrict__ grot, float* __restrict__ gshift,
-                                                            const float* __restrict__ reach) {
+                                                            float* __restrict__ grot, float* __restrict__ gshift) {
     static_assert(GMODE == 0 || KP == 1, "the gradient modes sum one pose per wave batch");
     static_assert(GMODE == 0 || std::is_same<VS, float>::value, "complex-half volumes are read by the forward only");
     constexpr int LO = CUBIC ? 1 : 0, HI = CUBIC ? 2 : 1, WC = GC + LO + HI, WR = GR + LO + HI, W2 = WC * WR;
@@ -655,24 +678,32 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
     __shared__ int pcnt[2];
     __shared__ Slot2 slots[NW][KP];
     __shared__ int marks[NW][64];
+    __shared__ int part[NW];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slot = lane / RPS, jrow = lane % RPS;
     const int N = g.N, H = g.H;
-    const int64_t items = g.B * ts.gksplit * int64_t(ts.gnt) * ts.gnt;
+    // samples lie within |x| <= rho_k: rotations reach rho_unit + 1, GEN poses up to kScaleMax
+    // times farther (the call's own largest singular value), on a wider grid of tiles
+    float rho_k = ts.rho_unit + 1.0f;
+    if constexpr (GEN) {
+        rho_k = fminf(ts.rho, general_reach<2, kThreads>(rot, g.B_rot * g.P, ts.rho_unit, part));
+        if (rho_k <= 0.f) return;  // no such pose in this call
+    }
+    const int gnt = GEN ? ts.gnt2 : ts.gnt, gorg = GEN ? ts.gorg2 : ts.gorg;
+    const int64_t items = g.B * ts.gksplit * int64_t(gnt) * gnt;
     const float cut2 = float(g.cut2);
-    const float rho_k = fminf(ts.rho, *reach);  // tiles beyond the call's reach hold no sample
     const int64_t per = xcd_per<kRun>(items);
     for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
         const int64_t w = xcd_item<kRun>(slot_i);
         if (w >= items) continue;
-        const int kc = int(w % ts.gnt);
-        int64_t q = w / ts.gnt;
-        const int kr = int(q % ts.gnt);
-        q /= ts.gnt;
+        const int kc = int(w % gnt);
+        int64_t q = w / gnt;
+        const int kr = int(q % gnt);
+        q /= gnt;
         const int jr = int(q % ts.gksplit);
         const int64_t b = q / ts.gksplit;
         const int p0 = jr * ts.gprange, p1 = min(int(g.P), p0 + ts.gprange);
-        const int tc = ts.gorg + kc * GC, tr = ts.gorg + kr * GR;
+        const int tc = gorg + kc * GC, tr = gorg + kr * GR;
         // samples owned by this tile: floor(x) in [t, t + edge) on both axes (+ slack)
         const float lo[2] = {float(tc) - ts.eps, float(tr) - ts.eps};
         const float hi[2] = {float(tc + GC) + ts.eps, float(tr + GR) + ts.eps};
@@ -698,8 +729,8 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
                 float R[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) R[e] = rotb[int64_t(pbase + k) * 4 + e];
-                bool gen = false;
-                if (pose_hits2(R, lo, hi, gen)) plist[atomicAdd(&pcnt[0], 1)] = (unsigned short)(k | (gen ? kGen2 : 0u));
+                float as[2];
+                if (pose_of_class2<GEN>(R, as) && half_plane_hits2(as, lo, hi)) plist[atomicAdd(&pcnt[0], 1)] = k;
             }
             __syncthreads();
             const int np = pcnt[0];
@@ -718,15 +749,13 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
                 __syncthreads();
                 loaded = true;
             }
-            auto entry_at = [&](int k) { return unsigned(plist[k]); };
-            auto pose_at = [&](int k) { return pbase + int(entry_at(k) & kPose2Mask); };
+            auto pose_at = [&](int k) { return pbase + int(plist[k]); };
             int base = wave * KP;
             float Rn[4], Sn[2];
             if (base < np) load_pose2(rotb, shb, pose_at(min(base + slot, np - 1)), Rn, Sn);
             for (; base < np; base += NW * KP) {
                 const bool sv = base + slot < np;
-                const unsigned pe = entry_at(min(base + slot, np - 1));
-                const int pp = pbase + int(pe & kPose2Mask);
+                const int pp = pose_at(min(base + slot, np - 1));
                 float R[4], Sh[2];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) R[e] = Rn[e];
@@ -746,7 +775,7 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
 #pragma unroll
                 for (int k = 0; k < 6; ++k) acc[k] = 0.f;
                 int r0, r1;
-                box_rows2(R, (pe & kGen2) != 0, lo, hi, ts, r0, r1);
+                box_rows2<GEN>(R, lo, hi, ts, r0, r1);
                 const int nr = sv ? max(0, r1 - r0 + 1) : 0;
                 const int maxnr = wave_max(nr);
                 for (int rbase = 0; rbase < maxnr; rbase += RPS) {
@@ -851,74 +880,84 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
 template <bool CUBIC, int KP, int GMODE, bool RS, bool WG, typename VS = float>
 hipError_t gather2_launch(const Geom& g, const TileSpec2& ts, const void* rec, const void* gw, const void* rot,
                           const void* shifts, void* out, void* wout, const void* gsrc, void* grot, void* gshift,
-                          const float* reach, hipStream_t s) {
+                          hipStream_t s) {
+    // rotations, then the other tiled poses (their samples and gradient terms are their own)
     const int64_t work = g.B * ts.gksplit * int64_t(ts.gnt) * ts.gnt;
-    if (work == 0) return hipSuccess;
-    hipLaunchKernelGGL((k_gather2_tiled<CUBIC, KP, GMODE, RS, WG, VS>), dim3(grid_for(kXcds * xcd_per<kRun>(work))),
+    if (work > 0) {
+        hipLaunchKernelGGL((k_gather2_tiled<CUBIC, KP, GMODE, RS, WG, VS, false>), dim3(grid2_of<false>(work)),
+                           dim3(kThreads), 0, s, g, ts, (const Cx<VS>*)rec, (const float*)gw, (const float*)rot,
+                           (const float*)shifts, (Cx<float>*)out, (float*)wout, (const Cx<float>*)gsrc,
+                           (float*)grot, (float*)gshift);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    const int64_t work2 = g.B * ts.gksplit * int64_t(ts.gnt2) * ts.gnt2;
+    if (work2 == 0) return hipSuccess;
+    hipLaunchKernelGGL((k_gather2_tiled<CUBIC, KP, GMODE, RS, WG, VS, true>), dim3(grid2_of<true>(work2)),
                        dim3(kThreads), 0, s, g, ts, (const Cx<VS>*)rec, (const float*)gw, (const float*)rot,
                        (const float*)shifts, (Cx<float>*)out, (float*)wout, (const Cx<float>*)gsrc, (float*)grot,
-                       (float*)gshift, reach);
+                       (float*)gshift);
     return hipGetLastError();
 }
 
 template <bool CUBIC, typename VS>
 hipError_t gather2_forw(const Geom& g, const TileSpec2& ts, const void* rec, const void* rot, const void* shifts,
-                        void* out, const float* reach, hipStream_t s) {
+                        void* out, hipStream_t s) {
     if (ts.kp_gather >= 4)
         return gather2_launch<CUBIC, 4, 0, false, false, VS>(g, ts, rec, nullptr, rot, shifts, out, nullptr, nullptr,
-                                                             nullptr, nullptr, reach, s);
+                                                             nullptr, nullptr, s);
     if (ts.kp_gather == 2)
         return gather2_launch<CUBIC, 2, 0, false, false, VS>(g, ts, rec, nullptr, rot, shifts, out, nullptr, nullptr,
-                                                             nullptr, nullptr, reach, s);
+                                                             nullptr, nullptr, s);
     return gather2_launch<CUBIC, 1, 0, false, false, VS>(g, ts, rec, nullptr, rot, shifts, out, nullptr, nullptr,
-                                                         nullptr, nullptr, reach, s);
+                                                         nullptr, nullptr, s);
 }
 
 template <bool CUBIC>
 hipError_t gather2_modes(int mode, const Geom& g, const TileSpec2& ts, const void* rec, const void* gw,
                          const void* rot, const void* shifts, void* out, void* wout, const void* gsrc, void* grot,
-                         void* gshift, const float* reach, hipStream_t s) {
-    if (mode == 0) return gather2_forw<CUBIC, float>(g, ts, rec, rot, shifts, out, reach, s);
+                         void* gshift, hipStream_t s) {
+    if (mode == 0) return gather2_forw<CUBIC, float>(g, ts, rec, rot, shifts, out, s);
     if (mode == 1)
-        return gather2_launch<CUBIC, 1, 1, true, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, reach, s);
+        return gather2_launch<CUBIC, 1, 1, true, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, s);
     const bool rs = grot || gshift;
     if (wout)
         return rs ? gather2_launch<CUBIC, 1, 2, true, true>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
-                                                            gshift, reach, s)
+                                                            gshift, s)
                   : gather2_launch<CUBIC, 1, 2, false, true>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
-                                                             gshift, reach, s);
-    return rs ? gather2_launch<CUBIC, 1, 2, true, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, reach, s)
+                                                             gshift, s);
+    return rs ? gather2_launch<CUBIC, 1, 2, true, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, s)
               : gather2_launch<CUBIC, 1, 2, false, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
-                                                          gshift, reach, s);
+                                                          gshift, s);
 }
 
 }  // namespace
 
 hipError_t launch_gather2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* rec,
                                 const void* gw, const void* rot, const void* shifts, void* out, void* wout,
-                                const void* gsrc, void* grot, void* gshift, const float* reach, hipStream_t s, bool rec_half) {
+                                const void* gsrc, void* grot, void* gshift, hipStream_t s, bool rec_half) {
     if (rec_half) {
         if (mode != 0) return hipErrorInvalidValue;
-        return cubic ? gather2_forw<true, __half>(g, ts, rec, rot, shifts, out, reach, s)
-                     : gather2_forw<false, __half>(g, ts, rec, rot, shifts, out, reach, s);
+        return cubic ? gather2_forw<true, __half>(g, ts, rec, rot, shifts, out, s)
+                     : gather2_forw<false, __half>(g, ts, rec, rot, shifts, out, s);
     }
     if (mode == 1 && !grot && !gshift) return hipSuccess;
-    return cubic ? gather2_modes<true>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, reach, s)
-                 : gather2_modes<false>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, reach, s);
+    return cubic ? gather2_modes<true>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, s)
+                 : gather2_modes<false>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, s);
 }
 
 hipError_t launch_scatter2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* src,
                                  const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
-                                 const float* reach, hipStream_t s) {
+                                 hipStream_t s) {
     if (mode == 0) {
         if (weights)
-            return cubic ? scatter2_kp<true, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s)
-                         : scatter2_kp<false, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
-        return cubic ? scatter2_kp<true, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s)
-                     : scatter2_kp<false, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s);
+            return cubic ? scatter2_all<true, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s)
+                         : scatter2_all<false, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+        return cubic ? scatter2_all<true, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
+                     : scatter2_all<false, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
     }
-    return cubic ? scatter2_kp<true, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s)
-                 : scatter2_kp<false, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s);
+    return cubic ? scatter2_all<true, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
+                 : scatter2_all<false, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
 }
 
 }  // namespace tp

@@ -32,11 +32,21 @@
 //                     the backprojection is applied afterwards by k_mirror_x0.
 //
 // Poses whose first two matrix columns a, b have singular values in
-// [kScaleMin, kScaleMax] take this path (pose_tiled3: rotations, and scaled or
-// sheared matrices); the per-pixel kernels handle the others and write the
-// masked pixels of the forward.  A sample x = sc a + sr b of such a pose has
-// sc = as . x and sr = bs . x with the dual basis (as, bs) of a, b, which
-// bounds the rows and the half plane sc >= 0 that can reach a box.
+// [kScaleMin, kScaleMax] take this path (pose_tiled3); the per-pixel kernels
+// handle the others and write the masked pixels of the forward.  Each kernel
+// comes in two instantiations:
+//   GEN = false  rotations (columns orthonormal to kRotationTol), one
+//                workgroup per work item over the grid their samples reach;
+//   GEN = true   the other tiled poses (scaled, anisotropically magnified or
+//                sheared matrices), launched after the first on a small
+//                persistent grid.  Its workgroups first find the call's
+//                largest singular value among such poses, and exit at once
+//                when there is none, so rotation-only calls pay one short
+//                launch.  A sample x = sc a + sr b of such a pose has
+//                sc = as . x and sr = bs . x with the dual basis (as, bs),
+//                which bounds the rows and the half plane sc >= 0 that can
+//                reach a box; the grid reaches samples up to kScaleMax times
+//                farther out.  Scatters add their tiles into the volume.
 #include <type_traits>
 
 #include "tp_device.hh"
@@ -71,23 +81,38 @@ __device__ __forceinline__ bool half_plane_hits(const float* as, const float* hi
     return uhi >= 0.f;
 }
 
-// Tiled pose whose plane and half plane reach the box; `general`: not a
-// rotation (its bounds need the dual basis, carried as a flag in the pose list).
-__device__ __forceinline__ bool pose_hits(const float* R, const float* lo, const float* hi, bool& general) {
+// Is the pose of this instantiation's class (rotation, or GEN: another tiled
+// matrix)?  `as` receives the half-plane vector (column 0, or its dual).
+template <bool GEN>
+__device__ __forceinline__ bool pose_of_class(const float* R, float* as) {
     const PoseGram gr = pose_gram3(R);
-    general = !gram_is_rotation(gr);
-    if ((general && !gram_tiled(gr)) || !plane_hits(R, lo, hi)) return false;
-    float as[3] = {R[0], R[3], R[6]}, bs[3];
-    if (general) pose_dual3(R, gr, as, bs);
-    return half_plane_hits(as, hi, lo);
+    if constexpr (GEN) {
+        if (gram_is_rotation(gr) || !gram_tiled(gr)) return false;
+        float bs[3];
+        pose_dual3(R, gr, as, bs);
+        return true;
+    } else {
+        as[0] = R[0];
+        as[1] = R[3];
+        as[2] = R[6];
+        return gram_is_rotation(gr);
+    }
 }
 
-// Rows r (sr = r*os = bs . x) whose samples can lie in the box.  A rotation's
-// bs is its column 1; other poses (`general`) compute their dual basis.
-__device__ __forceinline__ void box_rows(const float* R, bool general, const float* lo, const float* hi,
-                                         const TileSpec& ts, int& r0, int& r1) {
+// Pose of this class whose plane and half plane reach the box.
+template <bool GEN>
+__device__ __forceinline__ bool pose_hits(const float* R, const float* lo, const float* hi) {
+    float as[3];
+    return pose_of_class<GEN>(R, as) && plane_hits(R, lo, hi) && half_plane_hits(as, hi, lo);
+}
+
+// Rows r (sr = r*os = bs . x) whose samples can lie in the box: bs is a
+// rotation's column 1, or (GEN) the dual basis vector.
+template <bool GEN>
+__device__ __forceinline__ void box_rows(const float* R, const float* lo, const float* hi, const TileSpec& ts,
+                                         int& r0, int& r1) {
     float as[3], bs[3] = {R[1], R[4], R[7]};
-    if (general) pose_dual3(R, pose_gram3(R), as, bs);
+    if constexpr (GEN) pose_dual3(R, pose_gram3(R), as, bs);
     float vlo = 0.f, vhi = 0.f;
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
@@ -229,13 +254,12 @@ constexpr int kCullInFlight = 2;  // rotations loaded together per lane
 constexpr int kChunk = 1024;      // poses culled per phase
 
 // List entries: pose index relative to the phase, plus which boxes it crosses.
-// kGeneral: the pose is not a rotation (box_rows needs its dual basis).
-constexpr unsigned kHit1 = 1u << 14, kHit2 = 1u << 15, kGeneral = 1u << 13, kPoseMask = kGeneral - 1;
-static_assert(2 * kChunk <= int(kPoseMask) + 1, "pose index must fit below the flag bits");
+constexpr unsigned kHit1 = 1u << 14, kHit2 = 1u << 15, kPoseMask = kHit1 - 1;
+static_assert(kChunk <= int(kPoseMask) + 1, "pose index must fit below the flag bits");
 
 // Cull poses [pbase, pend) (at most kChunk) against up to two boxes with a
 // workgroup of NT lanes; returns the count.
-template <int NT, bool TWO, int CH = kChunk>
+template <int NT, bool TWO, int CH, bool GEN>
 __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pend, int pbase, const float* lo1,
                                           const float* hi1, const float* lo2, const float* hi2,
                                           unsigned short* plist, int* pcount) {
@@ -254,11 +278,8 @@ __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pe
         for (int q = 0; q < kCullInFlight; ++q) {
             const int p = pbase + int(threadIdx.x) + (q0 + q) * NT;
             if (p >= pend) continue;
-            bool gen = false;
-            const bool h1 = pose_hits(R[q], lo1, hi1, gen), h2 = TWO && pose_hits(R[q], lo2, hi2, gen);
-            if (h1 || h2)
-                plist[atomicAdd(pcount, 1)] =
-                    (unsigned short)((p - pbase) | (h1 ? kHit1 : 0) | (h2 ? kHit2 : 0) | (gen ? kGeneral : 0));
+            const bool h1 = pose_hits<GEN>(R[q], lo1, hi1), h2 = TWO && pose_hits<GEN>(R[q], lo2, hi2);
+            if (h1 || h2) plist[atomicAdd(pcount, 1)] = (unsigned short)((p - pbase) | (h1 ? kHit1 : 0) | (h2 ? kHit2 : 0));
         }
     }
     __syncthreads();
@@ -271,7 +292,7 @@ __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pe
 // survivors from the back (kChunk entries hold both lists), so each pass
 // batches only poses that cross its box.
 constexpr int kChunkSc = kChunk / 2;
-template <int NT>
+template <int NT, bool GEN>
 __device__ __forceinline__ void cull_chunk_boxes(const float* __restrict__ rotb, int pend, int pbase,
                                                  const float* lo1, const float* hi1, const float* lo2,
                                                  const float* hi2, unsigned short* plist, int* pcnt, int& n1,
@@ -293,14 +314,11 @@ __device__ __forceinline__ void cull_chunk_boxes(const float* __restrict__ rotb,
             const int p = pbase + int(threadIdx.x) + (q0 + q) * NT;
             // box 2 is box 1 negated (bit for bit), which a plane through the origin
             // crosses exactly when it crosses box 1: one plane test serves both
-            const PoseGram gr = pose_gram3(R[q]);
-            const bool general = !gram_is_rotation(gr);
-            if (p >= pend || (general && !gram_tiled(gr)) || !plane_hits(R[q], lo1, hi1)) continue;
-            float as[3] = {R[q][0], R[q][3], R[q][6]}, bs[3];
-            if (general) pose_dual3(R[q], gr, as, bs);
-            const unsigned short e = (unsigned short)((p - pbase) | (general ? kGeneral : 0u));
-            if (half_plane_hits(as, hi1, lo1)) plist[atomicAdd(&pcnt[0], 1)] = e;
-            if (half_plane_hits(as, hi2, lo2)) plist[kChunk - 1 - atomicAdd(&pcnt[1], 1)] = e;
+            float as[3];
+            if (p >= pend || !pose_of_class<GEN>(R[q], as) || !plane_hits(R[q], lo1, hi1)) continue;
+            if (half_plane_hits(as, hi1, lo1)) plist[atomicAdd(&pcnt[0], 1)] = (unsigned short)(p - pbase);
+            if (half_plane_hits(as, hi2, lo2))
+                plist[kChunk - 1 - atomicAdd(&pcnt[1], 1)] = (unsigned short)(p - pbase);
         }
     }
     __syncthreads();
@@ -371,7 +389,8 @@ __device__ __forceinline__ Interp<float> cubic3_grads(F&& fetch, float d, float 
     return o;
 }
 
-template <bool CUBIC, int KP, bool OSX, int GMODE = 0, bool RS = true, bool WG = false, typename VS = float>
+template <bool CUBIC, int KP, bool OSX, int GMODE = 0, bool RS = true, bool WG = false, typename VS = float,
+          bool GEN = false>
 __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec ts, const Cx<VS>* __restrict__ rec,
                                                         const float* __restrict__ rot,
                                                         const float* __restrict__ shifts,
@@ -380,8 +399,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                                                         float* __restrict__ grot = nullptr,
                                                         float* __restrict__ gshift = nullptr,
                                                         const float* __restrict__ gw = nullptr,
-                                                        float* __restrict__ wout = nullptr,
-                                                        const float* __restrict__ reach = nullptr) {
+                                                        float* __restrict__ wout = nullptr) {
     static_assert(GMODE == 0 || KP == 1, "the gradient modes sum one pose per wave batch");
     static_assert(GMODE == 0 || std::is_same<VS, float>::value, "complex-half volumes are read by the forward only");
     constexpr bool GRADS = GMODE == 1 || (GMODE == 2 && RS);
@@ -401,51 +419,33 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
     constexpr int QCAP = 256;
     __shared__ Slot slots[NW][KP];
     __shared__ unsigned queue[NW][QCAP];
+    __shared__ int part[NW];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slot = lane / RPS, jrow = lane % RPS;
-    const int nt = ts.nt;
-    // items: the core pieces and tiles of the grid that unit-scale poses reach (one launch slot
-    // each), then the tiles of the wider grid for enlarging poses, which the grid-stride loop
-    // visits after them and which are skipped when inside the first grid or beyond the reach
-    const int64_t items1 = g.B * (int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fd1 - ts.fd0) * ts.ksplit +
-                                  int64_t(nt) * nt * ts.ntfd);
-    const int64_t per_b2 = int64_t(ts.nt2) * ts.nt2 * ts.ntfd2;
+    // samples lie within |x| <= rho_k: rotations reach rho_unit + 1; GEN poses up to kScaleMax
+    // times farther (the call's own largest singular value), on a tile grid that far out
+    float rho_k = ts.rho_unit + 1.0f;
+    if constexpr (GEN) {
+        rho_k = fminf(ts.rho, general_reach<3, NT>(rot, g.B_rot * g.P, ts.rho_unit, part));
+        if (rho_k <= 0.f) return;  // no such pose in this call
+    }
+    const float rho2 = rho_k * rho_k;
+    const int nt = GEN ? ts.nt2 : ts.nt, ntd = GEN ? ts.ntfd2 : ts.ntfd;
+    const int org = GEN ? ts.org2 : ts.org, orgd = GEN ? ts.orgd2 : ts.orgd;
+    const int fc0 = GEN ? ts.fc0_2 : ts.fc0, fc1 = GEN ? ts.fc1_2 : ts.fc1;
+    const int fd0 = GEN ? ts.fd0_2 : ts.fd0, fd1 = GEN ? ts.fd1_2 : ts.fd1;
+    const int64_t items = g.B * (int64_t(fc1 - fc0) * (fc1 - fc0) * (fd1 - fd0) * ts.ksplit + int64_t(nt) * nt * ntd);
     const float cut2 = float(g.cut2);
-    // tiles beyond the call's reach (launch_pose_reach) hold no sample; the wider grid's slots
-    // follow the first grid's and are visited only when the reach leaves the first grid
-    const float rho_k = fminf(ts.rho, *reach), rho2 = rho_k * rho_k;
     const int N = g.N, H = g.H;
-    const int64_t nslot1 = kXcds * xcd_per<kRunForw>(items1);
-    const int64_t nslot = nslot1 + kXcds * xcd_per<kRunForw>(g.B * per_b2);
-    for (int64_t slot_i = blockIdx.x; slot_i < nslot; slot_i += gridDim.x) {
-        if (slot_i >= nslot1 && rho_k + 2.0f <= float(-ts.org) && rho_k + 2.0f <= float(-ts.orgd)) break;
-        const int64_t w = slot_i < nslot1 ? xcd_item<kRunForw>(slot_i) : items1 + xcd_item<kRunForw>(slot_i - nslot1);
-        if (w >= items1 + g.B * per_b2 || (slot_i < nslot1 && w >= items1)) continue;
-        int64_t b;
-        int tc, tr, td, p0, p1;
-        if (w < items1) {
-            const Item it = item_of(w, g.B, int(g.P), ts.ntfd, nt, nt, ts.fd0, ts.fd1, ts.fc0, ts.fc1, ts.fc0, ts.fc1,
-                                    ts.ksplit, ts.prange);
-            if (it.skip) continue;
-            b = it.b;
-            tc = ts.org + it.kc * L;
-            tr = ts.org + it.kr * L;
-            td = ts.orgd + it.kd * LD;
-            p0 = it.p0;
-            p1 = it.p1;
-        } else {
-            const int64_t q = w - items1;
-            b = q / per_b2;
-            const int t = int(q - b * per_b2);
-            tc = ts.org2 + (t % ts.nt2) * L;
-            tr = ts.org2 + ((t / ts.nt2) % ts.nt2) * L;
-            td = ts.orgd2 + (t / (ts.nt2 * ts.nt2)) * LD;
-            if (tc >= ts.org && tc < ts.org + nt * L && tr >= ts.org && tr < ts.org + nt * L && td >= ts.orgd &&
-                td < ts.orgd + ts.ntfd * LD)
-                continue;
-            p0 = 0;
-            p1 = int(g.P);
-        }
+    const int64_t per = xcd_per<kRunForw>(items);
+    for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
+        const int64_t w = xcd_item<kRunForw>(slot_i);
+        if (w >= items) continue;
+        const Item it = item_of(w, g.B, int(g.P), ntd, nt, nt, fd0, fd1, fc0, fc1, fc0, fc1, ts.ksplit, ts.prange);
+        if (it.skip) continue;
+        const int64_t b = it.b;
+        const int tc = org + it.kc * L, tr = org + it.kr * L, td = orgd + it.kd * LD;
+        const int p0 = it.p0, p1 = it.p1;
         // samples owned by this tile: floor(x) in [t, t + edge) on every axis (+ slack)
         const float lo[3] = {float(tc) - ts.eps, float(tr) - ts.eps, float(td) - ts.eps};
         const float hi[3] = {float(tc + L) + ts.eps, float(tr + L) + ts.eps, float(td + LD) + ts.eps};
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
         const Cx<VS>* recb = rec + b * g.vol;
         bool loaded = false;
         for (int pbase = p0; pbase < p1; pbase += CH) {
-            const int np = cull_chunk<NT, false, CH>(rotb, p1, pbase, lo, hi, lo, hi, plist, &pcount);
+            const int np = cull_chunk<NT, false, CH, GEN>(rotb, p1, pbase, lo, hi, lo, hi, plist, &pcount);
             if (np == 0) continue;
             if (!loaded) {
                 // stage the tile and its halo.  When the staged box lies on one side of c = 0 and
@@ -544,7 +544,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
 #pragma unroll
                 for (int k = 0; k < 11; ++k) acc[k] = 0.f;
                 int r0, r1;
-                box_rows(R, (pe & kGeneral) != 0, lo, hi, ts, r0, r1);
+                box_rows<GEN>(R, lo, hi, ts, r0, r1);
                 const int nr = sv ? max(0, r1 - r0 + 1) : 0;
                 const int maxnr = wave_max(nr);
                 for (int rbase = 0; rbase < maxnr; rbase += RPS) {
@@ -780,13 +780,12 @@ __device__ __forceinline__ void scatter_sample(const Geom& g, const Slot& sd, in
 
 // MODE 0: backprojection, v = proj * conj(phase(r, c)), optional weights.
 // MODE 1: reconstruction gradient of the projection, v = g * phase(-r, -c).
-template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool OSX>
+template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool OSX, bool GEN>
 __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_scatter3_tiled(Geom g, TileSpec ts, const Cx<float>* __restrict__ src,
                                                            const float* __restrict__ weights,
                                                            const float* __restrict__ rot,
                                                            const float* __restrict__ shifts,
-                                                           Cx<float>* __restrict__ dst, float* __restrict__ wdst,
-                                                           const float* __restrict__ reach) {
+                                                           Cx<float>* __restrict__ dst, float* __restrict__ wdst) {
     constexpr int SL = CUBIC ? 2 : 1, SH = CUBIC ? 1 : 0;  // stencil reach below / above floor(x)
     constexpr int SLOW = CUBIC ? 1 : 0;                    // first tap at floor(x) - SLOW
     constexpr int RPS = 64 / KP;
@@ -797,13 +796,20 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
     __shared__ int pcnt[2];
     __shared__ Slot slots[NW][KP];
     __shared__ int marks[NW][64];
+    __shared__ int part[NW];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slot = lane / RPS, jrow = lane % RPS;
     const int N = g.N, H = g.H, half = N / 2;
     const int64_t items = g.B * (int64_t(ts.sd1 - ts.sd0) * (ts.sr1 - ts.sr0) * ts.sc1 * ts.ksplit +
                                  int64_t(ts.ntd) * ts.ntr * ts.ntc);
     const float cut2 = float(g.cut2);
-    const float rho_k = fminf(ts.rho, *reach);  // tiles beyond the call's reach hold no sample
+    // samples lie within |x| <= rho_k: rotations reach rho_unit + 1, GEN poses up to kScaleMax
+    // times farther (the call's own largest singular value)
+    float rho_k = ts.rho_unit + 1.0f;
+    if constexpr (GEN) {
+        rho_k = fminf(ts.rho, general_reach<3, NT>(rot, g.B_rot * g.P, ts.rho_unit, part));
+        if (rho_k <= 0.f) return;  // no such pose in this call
+    }
     const int64_t per = xcd_per<kRunScatter>(items);
     for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
         const int64_t w = xcd_item<kRunScatter>(slot_i);
@@ -842,15 +848,16 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
         const int pend = dist2 > rho_k * rho_k ? it.p0 : it.p1;
 
         const float* shb = shifts ? shifts + sb * g.P * 2 : nullptr;
+        bool touched = false;  // GEN: some pose reaches the tile (else it is left as the rotations wrote it)
         for (int pbase = it.p0; pbase < pend; pbase += kChunkSc) {
             int n1, n2;
-            cull_chunk_boxes<NT>(rotb, pend, pbase, lo1, hi1, lo2, hi2, plist, pcnt, n1, n2);
+            cull_chunk_boxes<NT, GEN>(rotb, pend, pbase, lo1, hi1, lo2, hi2, plist, pcnt, n1, n2);
+            touched |= n1 + n2 > 0;
 #pragma unroll 1
             for (int pass = 0; pass < 2; ++pass) {
                 const int np = pass == 0 ? n1 : n2;
                 // pose of list entry k of this pass (box-2 entries are stored from the back)
-                auto entry_at = [&](int k) { return unsigned(plist[pass == 0 ? k : kChunk - 1 - k]); };
-                auto pose_at = [&](int k) { return pbase + int(entry_at(k) & kPoseMask); };
+                auto pose_at = [&](int k) { return pbase + int(plist[pass == 0 ? k : kChunk - 1 - k]); };
                 float lo[3], hi[3];
 #pragma unroll
                 for (int k = 0; k < 3; ++k) {
@@ -871,8 +878,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                 if (base < np) load_pose(rotb, shb, pose_at(min(base + slot, np - 1)), Rn, Sn);
                 for (; base < np; base += NW * KP) {
                     const bool sv = base + slot < np;
-                    const unsigned pe = entry_at(min(base + slot, np - 1));
-                    const int pp = pbase + int(pe & kPoseMask);
+                    const int pp = pose_at(min(base + slot, np - 1));
                     float R[9], Sh[2];
 #pragma unroll
                     for (int e = 0; e < 9; ++e) R[e] = Rn[e];
@@ -890,7 +896,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                     __builtin_amdgcn_wave_barrier();
                     {
                     int r0, r1;
-                    box_rows(R, (pe & kGeneral) != 0, lo, hi, ts, r0, r1);
+                    box_rows<GEN>(R, lo, hi, ts, r0, r1);
                     const int nr = sv ? max(0, r1 - r0 + 1) : 0;
                     const int maxnr = wave_max(nr);
                     for (int rbase = 0; rbase < maxnr; rbase += RPS) {
@@ -956,7 +962,10 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
             __syncthreads();
         }
 
-        // write every stored cell of the tile once (core pieces add into a zeroed region)
+        // write every stored cell of the tile once (core pieces add into a zeroed region).  GEN
+        // adds onto what the rotation launch wrote: its core pieces with atomics, its other
+        // tiles (one workgroup each) by a plain read and write
+        if (GEN && !touched) continue;
         __syncthreads();
         for (int e = tid; e < S3; e += NT) {
             const int lc = e % SC, lr = (e / SC) % SR, ld = e / (SC * SR);
@@ -969,6 +978,10 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                 atomic_add(&dst[idx].re, float(acc_re[a]));
                 atomic_add(&dst[idx].im, float(acc_im[a]));
                 if (WEIGHTS) atomic_add(&wdst[idx], float(acc_w[a]));
+            } else if (GEN) {
+                const Cx<float> o = dst[idx];
+                dst[idx] = Cx<float>{o.re + float(acc_re[a]), o.im + float(acc_im[a])};
+                if (WEIGHTS) wdst[idx] += float(acc_w[a]);
             } else {
                 dst[idx] = Cx<float>{float(acc_re[a]), float(acc_im[a])};
                 if (WEIGHTS) wdst[idx] = float(acc_w[a]);
@@ -1029,20 +1042,37 @@ __global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<fl
     }
 }
 
+// Work items of the forward tile grid (GEN: the grid that general poses reach).
+template <bool GEN>
+int64_t forw_items(const Geom& g, const TileSpec& ts) {
+    const int nt = GEN ? ts.nt2 : ts.nt, ntd = GEN ? ts.ntfd2 : ts.ntfd;
+    const int fc = GEN ? ts.fc1_2 - ts.fc0_2 : ts.fc1 - ts.fc0, fd = GEN ? ts.fd1_2 - ts.fd0_2 : ts.fd1 - ts.fd0;
+    return g.B * (int64_t(fc) * fc * fd * ts.ksplit + int64_t(nt) * nt * ntd);
+}
+// Workgroups of a launch over `items`: one per item (rotations), or the persistent GEN grid.
+template <bool GEN, int RUN>
+unsigned grid_of(int64_t items) {
+    const int64_t slots = kXcds * xcd_per<RUN>(items);
+    return grid_for(GEN && slots > kGenGrid ? kGenGrid : slots);
+}
+
 template <bool CUBIC, int KP, bool OSX, typename VS>
 hipError_t forw_launch(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts,
-                       void* out, const float* reach, hipStream_t s) {
-    const int64_t fcore = int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fd1 - ts.fd0) * ts.ksplit;
-    const int64_t work = g.B * (fcore + int64_t(ts.nt) * ts.nt * ts.ntfd);
-    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP, OSX, 0, true, false, VS>),
-                       dim3(grid_for(kXcds * xcd_per<kRunForw>(work))), dim3(kForwThreads), 0, s, g, ts,
-                       (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out, nullptr, nullptr, nullptr, nullptr, nullptr, reach);
+                       void* out, hipStream_t s) {
+    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP, OSX, 0, true, false, VS, false>),
+                       dim3(grid_of<false, kRunForw>(forw_items<false>(g, ts))), dim3(kForwThreads), 0, s, g, ts,
+                       (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP, OSX, 0, true, false, VS, true>),
+                       dim3(grid_of<true, kRunForw>(forw_items<true>(g, ts))), dim3(kForwThreads), 0, s, g, ts,
+                       (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
     return hipGetLastError();
 }
 
 template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool OSX>
 hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
-                          const void* shifts, void* dst, void* wdst, const float* reach, hipStream_t s) {
+                          const void* shifts, void* dst, void* wdst, hipStream_t s) {
     const int64_t score = int64_t(ts.sd1 - ts.sd0) * (ts.sr1 - ts.sr0) * ts.sc1 * ts.ksplit;
     if (score > 0) {
         const int64_t cells = g.B * int64_t((ts.sd1 - ts.sd0) * SD) * ((ts.sr1 - ts.sr0) * SR) * (ts.sc1 * SC);
@@ -1053,12 +1083,19 @@ hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, co
         const hipError_t ez = hipGetLastError();
         if (ez != hipSuccess) return ez;
     }
+    // rotations write every tile; the general poses add onto them
     const int64_t work = g.B * (score + int64_t(ts.ntd) * ts.ntr * ts.ntc);
-    hipLaunchKernelGGL((k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP, OSX>), dim3(grid_for(kXcds * xcd_per<kRunScatter>(work))),
-                       dim3(kScatterThreads), 0, s, g,
-                       ts, (const Cx<float>*)src, (const float*)weights, (const float*)rot, (const float*)shifts,
-                       (Cx<float>*)dst, (float*)wdst, reach);
+    hipLaunchKernelGGL((k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP, OSX, false>),
+                       dim3(grid_of<false, kRunScatter>(work)), dim3(kScatterThreads), 0, s, g, ts,
+                       (const Cx<float>*)src, (const float*)weights, (const float*)rot, (const float*)shifts,
+                       (Cx<float>*)dst, (float*)wdst);
     hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP, OSX, true>),
+                       dim3(grid_of<true, kRunScatter>(work)), dim3(kScatterThreads), 0, s, g, ts,
+                       (const Cx<float>*)src, (const float*)weights, (const float*)rot, (const float*)shifts,
+                       (Cx<float>*)dst, (float*)wdst);
+    e = hipGetLastError();
     if (e != hipSuccess || MODE != 0) return e;
     const int64_t pairs = g.B * int64_t(g.N) * g.N;
     int64_t blocks = (pairs + kBlock - 1) / kBlock;
@@ -1070,120 +1107,134 @@ hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, co
 
 template <bool CUBIC, int MODE, bool WEIGHTS, bool OSX>
 hipError_t scatter_kp_osx(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
-                          const void* shifts, void* dst, void* wdst, const float* reach, hipStream_t s) {
+                          const void* shifts, void* dst, void* wdst, hipStream_t s) {
     if (ts.kp_scatter >= 4)
-        return scatter_launch<CUBIC, MODE, WEIGHTS, 4, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
+        return scatter_launch<CUBIC, MODE, WEIGHTS, 4, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, s);
     if (ts.kp_scatter == 2)
-        return scatter_launch<CUBIC, MODE, WEIGHTS, 2, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
-    return scatter_launch<CUBIC, MODE, WEIGHTS, 1, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
+        return scatter_launch<CUBIC, MODE, WEIGHTS, 2, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    return scatter_launch<CUBIC, MODE, WEIGHTS, 1, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, s);
 }
 
 template <bool CUBIC, int MODE, bool WEIGHTS>
 hipError_t scatter_kp(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
-                      const void* shifts, void* dst, void* wdst, const float* reach, hipStream_t s) {
-    if (ts.os_exact) return scatter_kp_osx<CUBIC, MODE, WEIGHTS, true>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
-    return scatter_kp_osx<CUBIC, MODE, WEIGHTS, false>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
+                      const void* shifts, void* dst, void* wdst, hipStream_t s) {
+    if (ts.os_exact) return scatter_kp_osx<CUBIC, MODE, WEIGHTS, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    return scatter_kp_osx<CUBIC, MODE, WEIGHTS, false>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+}
+
+template <bool CUBIC, bool OSX, bool GEN>
+hipError_t grads_one(const Geom& g, const TileSpec& ts, const void* gproj, const void* rec, const void* rot,
+                     const void* shifts, void* grot, void* gshift, hipStream_t s) {
+    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, 1, OSX, 1, true, false, float, GEN>),
+                       dim3(grid_of<GEN, kRunForw>(forw_items<GEN>(g, ts))), dim3(kForwThreads), 0, s, g, ts,
+                       (const Cx<float>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)nullptr,
+                       (const Cx<float>*)gproj, (float*)grot, (float*)gshift, nullptr, nullptr);
+    return hipGetLastError();
 }
 
 template <bool CUBIC, bool OSX>
 hipError_t grads_launch(const Geom& g, const TileSpec& ts, const void* gproj, const void* rec, const void* rot,
-                        const void* shifts, void* grot, void* gshift, const float* reach, hipStream_t s) {
-    const int64_t fcore = int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fd1 - ts.fd0) * ts.ksplit;
-    const int64_t work = g.B * (fcore + int64_t(ts.nt) * ts.nt * ts.ntfd);
-    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, 1, OSX, 1>), dim3(grid_for(kXcds * xcd_per<kRunForw>(work))),
-                       dim3(kForwThreads), 0, s, g, ts, (const Cx<float>*)rec, (const float*)rot,
-                       (const float*)shifts, (Cx<float>*)nullptr, (const Cx<float>*)gproj, (float*)grot,
-                       (float*)gshift, nullptr, nullptr, reach);
+                        const void* shifts, void* grot, void* gshift, hipStream_t s) {
+    const hipError_t e = grads_one<CUBIC, OSX, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, s);
+    if (e != hipSuccess) return e;
+    return grads_one<CUBIC, OSX, true>(g, ts, gproj, rec, rot, shifts, grot, gshift, s);
+}
+
+template <bool CUBIC, bool OSX, bool RS, bool WG, bool GEN>
+hipError_t bpback_one(const Geom& g, const TileSpec& ts, const void* gdata, const void* gw, const void* proj,
+                      const void* rot, const void* shifts, void* gproj, void* gweights, void* grot, void* gshift,
+                      hipStream_t s) {
+    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, 1, OSX, 2, RS, WG, float, GEN>),
+                       dim3(grid_of<GEN, kRunForw>(forw_items<GEN>(g, ts))), dim3(kForwThreads), 0, s, g, ts,
+                       (const Cx<float>*)gdata, (const float*)rot, (const float*)shifts, (Cx<float>*)gproj,
+                       (const Cx<float>*)proj, (float*)grot, (float*)gshift, (const float*)gw, (float*)gweights);
     return hipGetLastError();
 }
 
 template <bool CUBIC, bool OSX, bool RS, bool WG>
 hipError_t bpback_launch(const Geom& g, const TileSpec& ts, const void* gdata, const void* gw, const void* proj,
                          const void* rot, const void* shifts, void* gproj, void* gweights, void* grot, void* gshift,
-                         const float* reach, hipStream_t s) {
-    const int64_t fcore = int64_t(ts.fc1 - ts.fc0) * (ts.fc1 - ts.fc0) * (ts.fd1 - ts.fd0) * ts.ksplit;
-    const int64_t work = g.B * (fcore + int64_t(ts.nt) * ts.nt * ts.ntfd);
-    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, 1, OSX, 2, RS, WG>), dim3(grid_for(kXcds * xcd_per<kRunForw>(work))),
-                       dim3(kForwThreads), 0, s, g, ts, (const Cx<float>*)gdata, (const float*)rot,
-                       (const float*)shifts, (Cx<float>*)gproj, (const Cx<float>*)proj, (float*)grot, (float*)gshift,
-                       (const float*)gw, (float*)gweights, reach);
-    return hipGetLastError();
+                         hipStream_t s) {
+    const hipError_t e = bpback_one<CUBIC, OSX, RS, WG, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights,
+                                                               grot, gshift, s);
+    if (e != hipSuccess) return e;
+    return bpback_one<CUBIC, OSX, RS, WG, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
 }
 
 template <bool CUBIC, bool OSX>
 hipError_t bpback_flags(const Geom& g, const TileSpec& ts, const void* gdata, const void* gw, const void* proj,
                         const void* rot, const void* shifts, void* gproj, void* gweights, void* grot, void* gshift,
-                        const float* reach, hipStream_t s) {
+                        hipStream_t s) {
     const bool rs = grot || gshift, wg = gw && gweights;
     if (rs)
         return wg ? bpback_launch<CUBIC, OSX, true, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
-                                                          gshift, reach, s)
+                                                          gshift, s)
                   : bpback_launch<CUBIC, OSX, true, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, nullptr, grot,
-                                                           gshift, reach, s);
+                                                           gshift, s);
     return wg ? bpback_launch<CUBIC, OSX, false, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
-                                                       gshift, reach, s)
+                                                       gshift, s)
               : bpback_launch<CUBIC, OSX, false, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, nullptr, grot,
-                                                        gshift, reach, s);
+                                                        gshift, s);
 }
 
 template <bool CUBIC, bool OSX, typename VS>
 hipError_t forw_kp(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts, void* out,
-                   const float* reach, hipStream_t s) {
-    if (ts.kp_forw >= 4) return forw_launch<CUBIC, 4, OSX, VS>(g, ts, rec, rot, shifts, out, reach, s);
-    if (ts.kp_forw == 2) return forw_launch<CUBIC, 2, OSX, VS>(g, ts, rec, rot, shifts, out, reach, s);
-    return forw_launch<CUBIC, 1, OSX, VS>(g, ts, rec, rot, shifts, out, reach, s);
+                   hipStream_t s) {
+    if (ts.kp_forw >= 4) return forw_launch<CUBIC, 4, OSX, VS>(g, ts, rec, rot, shifts, out, s);
+    if (ts.kp_forw == 2) return forw_launch<CUBIC, 2, OSX, VS>(g, ts, rec, rot, shifts, out, s);
+    return forw_launch<CUBIC, 1, OSX, VS>(g, ts, rec, rot, shifts, out, s);
 }
 
 template <typename VS>
 hipError_t forw_store(bool cubic, const Geom& g, const TileSpec& ts, const void* rec, const void* rot,
-                      const void* shifts, void* out, const float* reach, hipStream_t s) {
+                      const void* shifts, void* out, hipStream_t s) {
     if (cubic)
-        return ts.os_exact ? forw_kp<true, true, VS>(g, ts, rec, rot, shifts, out, reach, s)
-                           : forw_kp<true, false, VS>(g, ts, rec, rot, shifts, out, reach, s);
-    return ts.os_exact ? forw_kp<false, true, VS>(g, ts, rec, rot, shifts, out, reach, s)
-                       : forw_kp<false, false, VS>(g, ts, rec, rot, shifts, out, reach, s);
+        return ts.os_exact ? forw_kp<true, true, VS>(g, ts, rec, rot, shifts, out, s)
+                           : forw_kp<true, false, VS>(g, ts, rec, rot, shifts, out, s);
+    return ts.os_exact ? forw_kp<false, true, VS>(g, ts, rec, rot, shifts, out, s)
+                       : forw_kp<false, false, VS>(g, ts, rec, rot, shifts, out, s);
 }
 
 }  // namespace
 
 hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* rec,
-                                      const void* rot, const void* shifts, void* out, const float* reach, hipStream_t s, bool rec_half) {
-    if (rec_half) return forw_store<__half>(cubic, g, ts, rec, rot, shifts, out, reach, s);
-    return forw_store<float>(cubic, g, ts, rec, rot, shifts, out, reach, s);
+                                      const void* rot, const void* shifts, void* out, hipStream_t s, bool rec_half) {
+    if (rec_half) return forw_store<__half>(cubic, g, ts, rec, rot, shifts, out, s);
+    return forw_store<float>(cubic, g, ts, rec, rot, shifts, out, s);
 }
 
 hipError_t launch_grads3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gproj, const void* rec,
-                               const void* rot, const void* shifts, void* grot, void* gshift, const float* reach, hipStream_t s) {
+                               const void* rot, const void* shifts, void* grot, void* gshift, hipStream_t s) {
     if (!grot && !gshift) return hipSuccess;
     if (cubic)
-        return ts.os_exact ? grads_launch<true, true>(g, ts, gproj, rec, rot, shifts, grot, gshift, reach, s)
-                           : grads_launch<true, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, reach, s);
-    return ts.os_exact ? grads_launch<false, true>(g, ts, gproj, rec, rot, shifts, grot, gshift, reach, s)
-                       : grads_launch<false, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, reach, s);
+        return ts.os_exact ? grads_launch<true, true>(g, ts, gproj, rec, rot, shifts, grot, gshift, s)
+                           : grads_launch<true, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, s);
+    return ts.os_exact ? grads_launch<false, true>(g, ts, gproj, rec, rot, shifts, grot, gshift, s)
+                       : grads_launch<false, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, s);
 }
 
 hipError_t launch_bpback3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gdata, const void* gw,
                                 const void* proj, const void* rot, const void* shifts, void* gproj, void* gweights,
-                                void* grot, void* gshift, const float* reach, hipStream_t s) {
+                                void* grot, void* gshift, hipStream_t s) {
     if (cubic)
-        return ts.os_exact ? bpback_flags<true, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, reach, s)
-                           : bpback_flags<true, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, reach, s);
-    return ts.os_exact ? bpback_flags<false, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, reach, s)
-                       : bpback_flags<false, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, reach, s);
+        return ts.os_exact ? bpback_flags<true, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s)
+                           : bpback_flags<true, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+    return ts.os_exact ? bpback_flags<false, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s)
+                       : bpback_flags<false, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
 }
 
 hipError_t launch_scatter3_tiled(bool cubic, int mode, const Geom& g, const TileSpec& ts, const void* src,
                                  const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
-                                 const float* reach, hipStream_t s) {
+                                 hipStream_t s) {
     if (mode == 0) {
         if (weights)
-            return cubic ? scatter_kp<true, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s)
-                         : scatter_kp<false, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, reach, s);
-        return cubic ? scatter_kp<true, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s)
-                     : scatter_kp<false, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s);
+            return cubic ? scatter_kp<true, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s)
+                         : scatter_kp<false, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+        return cubic ? scatter_kp<true, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
+                     : scatter_kp<false, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
     }
-    return cubic ? scatter_kp<true, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s)
-                 : scatter_kp<false, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, reach, s);
+    return cubic ? scatter_kp<true, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
+                 : scatter_kp<false, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
 }
 
 }  // namespace tp

@@ -1,10 +1,13 @@
 // Wave-level building blocks shared by the tile-owner kernels (tp_tiled3d.hip,
 // tp_tiled2d.hip): DPP scans, the window-owner lookup of compacted sample
-// lists, and the XCD-aware hand-out of work items.
+// lists, the XCD-aware hand-out of work items, and the reach of a call's
+// general poses.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "tp_device.hh"
 
 namespace tp {
 namespace {
@@ -99,5 +102,41 @@ __device__ __forceinline__ int64_t xcd_item(int64_t slot) {
     const int64_t x = slot % kXcds, j = slot / kXcds;
     return ((j / RUN) * kXcds + x) * RUN + j % RUN;
 }
+// Opening scan of the GEN (non-rotation) tiled kernels: the radius their
+// samples reach, rho_unit * (largest singular value over the call's tiled
+// poses that are not rotations) + 1, or 0 when there is no such pose.  Every
+// lane of the NT-lane workgroup takes part; `part` holds NT / 64 ints.
+template <int DIM, int NT>
+__device__ float general_reach(const float* __restrict__ rot, int64_t poses, float rho_unit, int* part) {
+    constexpr int RS = DIM == 2 ? 4 : 9, U = 4;  // U poses per lane in flight
+    float m = 0.f;
+    for (int64_t p0 = threadIdx.x; p0 < poses; p0 += U * NT) {
+        float R[U][RS];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t p = min(p0 + u * NT, poses - 1);
+#pragma unroll
+            for (int e = 0; e < RS; ++e) R[u][e] = rot[p * RS + e];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const PoseGram gr = DIM == 2 ? pose_gram2(R[u]) : pose_gram3(R[u]);
+            if (p0 + u * NT < poses && !gram_is_rotation(gr) && gram_tiled(gr)) m = fmaxf(m, gram_smax(gr));
+        }
+    }
+    // non-negative floats order like their bit patterns as ints
+    const int wm = wave_max(__float_as_int(m));
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = wm;
+    __syncthreads();
+    int b = 0;
+    for (int w = 0; w < NT / 64; ++w) b = max(b, part[w]);
+    __syncthreads();
+    const float s = __int_as_float(b);
+    return s > 0.f ? rho_unit * s + 1.0f : 0.f;
+}
+
+// Workgroups of a GEN kernel's persistent grid (a multiple of kXcds).
+constexpr int64_t kGenGrid = 1024;
+
 }  // namespace
 }  // namespace tp
