@@ -4,10 +4,17 @@
 // reference (validate_projection_inputs, projection_utils.h:23-48, and the
 // per-op TORCH_CHECKs), derives the launch geometry, zero-fills the outputs
 // that are accumulated, and enqueues the kernels on the caller's stream.
-// Nothing is synchronised and nothing is allocated.
+// Nothing is synchronised.  The only memory besides the caller's is a small
+// scratch area per (device, stream) that the calls of the tiled kernels use
+// (tp::CallPoses: a summary of their poses and work counters), allocated by
+// the first such call on that stream and kept for the life of the process.
 #include <algorithm>
 #include <cmath>
+#include <map>
+#include <memory>
+#include <mutex>
 #include <string>
+#include <utility>
 
 #include "../../../include/torch_projectors_hip.h"
 #include "tp_launch.hh"
@@ -268,6 +275,49 @@ int need(const void* p, const char* name) {
 
 int launched(hipError_t e, const char* what) { return e == hipSuccess ? TP_OK : hip_fail(e, what); }
 
+// Scratch of the calls on one (device, stream).  Calls on one stream run in
+// order on the GPU, so they share it; `busy` is held while one call enqueues
+// its kernels, so that calls from several host threads on one stream do not
+// interleave their kernels.
+struct StreamScratch {
+    tp::CallPoses* p = nullptr;
+    std::mutex busy;
+};
+std::mutex g_scratch_mu;
+std::map<std::pair<int, hipStream_t>, std::unique_ptr<StreamScratch>> g_scratch;
+
+// The scratch of one call: taken (and its stream's `busy` held) until the call returns.
+struct CallScratch {
+    tp::CallPoses* p = nullptr;
+    std::unique_lock<std::mutex> hold;
+    int get(hipStream_t st) {
+        if (p) return TP_OK;
+        int dev = 0;
+        TP_TRY(launched(hipGetDevice(&dev), "hipGetDevice"));
+        StreamScratch* e;
+        {
+            std::lock_guard<std::mutex> lk(g_scratch_mu);
+            std::unique_ptr<StreamScratch>& slot = g_scratch[{dev, st}];
+            if (!slot) {
+                std::unique_ptr<StreamScratch> fresh(new StreamScratch);
+                TP_TRY(launched(hipMalloc(reinterpret_cast<void**>(&fresh->p), tp::kCallScratchBytes),
+                                "scratch allocation"));
+                slot = std::move(fresh);
+            }
+            e = slot.get();
+        }
+        hold = std::unique_lock<std::mutex>(e->busy);
+        p = e->p;
+        return TP_OK;
+    }
+};
+
+// Summary of the call's poses for its tiled kernels (tp::launch_call_poses).
+int call_poses(int dim, const tp::Geom& g, const void* rot, float rho_unit, CallScratch& sc, hipStream_t s) {
+    TP_TRY(sc.get(s));
+    return launched(tp::launch_call_poses(dim, g.B_rot * g.P, rot, rho_unit, sc.p, s), "pose summary launch");
+}
+
 // TP_F16S: the volume is stored as complex half; it is widened exactly to
 // fp32 on load and everything else (poses, arithmetic, projections) is the
 // TP_F32 path.
@@ -292,9 +342,11 @@ int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int6
     TP_TRY(need(out, "projections"));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool cubic = interp == TP_CUBIC;
+    CallScratch sc;
     if (use_tiles(dim, dt, os, n)) {
-        TP_TRY(launched(tp::launch_project3_forw_tiled(cubic, g, tile_spec(g, cubic), rec, rot, shifts, out, s,
-                                                       rec_half),
+        const tp::TileSpec ts = tile_spec(g, cubic);
+        TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_project3_forw_tiled(cubic, g, ts, rec, rot, shifts, out, sc.p, 0, s, rec_half),
                         "tiled projection launch"));
         return launched(tp::launch_project_forw(dim, kdt, cubic, g, rec, rot, shifts, out, s, true),
                         "projection launch");
@@ -303,8 +355,10 @@ int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int6
         // zero-fill first: the tiled gather writes the active pixels of tiled poses, the
         // rest kernel the other poses
         TP_TRY(zero(out, cx_words(dt, g.B * g.P * int64_t(g.npix)), s));
-        TP_TRY(launched(tp::launch_gather2_tiled(cubic, 0, g, tile_spec2(g, cubic), rec, nullptr, rot, shifts, out,
-                                                 nullptr, nullptr, nullptr, nullptr, s, rec_half),
+        const tp::TileSpec2 ts = tile_spec2(g, cubic);
+        TP_TRY(call_poses(2, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_gather2_tiled(cubic, 0, g, ts, rec, nullptr, rot, shifts, out, nullptr, nullptr,
+                                                 nullptr, nullptr, sc.p, 0, s, rec_half),
                         "tiled projection launch"));
         return launched(tp::launch_project_forw(dim, kdt, cubic, g, rec, rot, shifts, out, s, true),
                         "projection launch");
@@ -337,19 +391,24 @@ int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, in
     TP_TRY(need(gproj, "grad_projections"));
     TP_TRY(need(rec, "reconstruction"));
     TP_TRY(need(rot, "rotations"));
+    CallScratch sc;
     if (tiles) {
         const tp::TileSpec ts = tile_spec(g, cubic);
-        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, s),
+        TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, sc.p, 0,
+                                                  s),
                         "tiled reconstruction-gradient launch"));
-        TP_TRY(launched(tp::launch_grads3_tiled(cubic, g, ts, gproj, rec, rot, shifts, grot, gshift, s),
+        TP_TRY(launched(tp::launch_grads3_tiled(cubic, g, ts, gproj, rec, rot, shifts, grot, gshift, sc.p, 1, s),
                         "tiled rotation/shift-gradient launch"));
     }
     if (tiles2) {
         const tp::TileSpec2 ts = tile_spec2(g, cubic);
-        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, s),
+        TP_TRY(call_poses(2, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, sc.p, 0,
+                                                  s),
                         "tiled reconstruction-gradient launch"));
         TP_TRY(launched(tp::launch_gather2_tiled(cubic, 1, g, ts, rec, nullptr, rot, shifts, nullptr, nullptr, gproj,
-                                                 grot, gshift, s),
+                                                 grot, gshift, sc.p, 1, s),
                         "tiled rotation/shift-gradient launch"));
     }
     return launched(tp::launch_project_back(dim, dtype, cubic, g, gproj, rec, rot, shifts, grec, grot, gshift, s,
@@ -383,14 +442,19 @@ int backproject_forw(int dim, int dtype, const void* proj, int64_t B, int64_t P,
     if (g.work == 0) return TP_OK;
     TP_TRY(need(proj, "projections"));
     TP_TRY(need(rot, "rotations"));
-    if (tiles)
-        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 0, g, tile_spec(g, cubic), proj, weights, rot, shifts, data, wrec,
-                                                  s),
+    CallScratch sc;
+    if (tiles) {
+        const tp::TileSpec ts = tile_spec(g, cubic);
+        TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 0, g, ts, proj, weights, rot, shifts, data, wrec, sc.p, 0, s),
                         "tiled backprojection launch"));
-    if (tiles2)
-        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 0, g, tile_spec2(g, cubic), proj, weights, rot, shifts, data,
-                                                  wrec, s),
+    }
+    if (tiles2) {
+        const tp::TileSpec2 ts = tile_spec2(g, cubic);
+        TP_TRY(call_poses(2, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_scatter2_tiled(cubic, 0, g, ts, proj, weights, rot, shifts, data, wrec, sc.p, 0, s),
                         "tiled backprojection launch"));
+    }
     return launched(
         tp::launch_backproject_forw(dim, dtype, cubic, g, proj, weights, rot, shifts, data, wrec, s, tiles || tiles2),
         "backprojection launch");
@@ -425,14 +489,21 @@ int backproject_back(int dim, int dtype, const void* gdata, const void* gw, int6
         TP_TRY(zero(gproj, cx_words(dtype, g.B * g.P * int64_t(g.npix)), s));
         TP_TRY(zero(gweights, re_words(dtype, g.B * g.P * int64_t(g.npix)), s));
     }
-    if (tiles)
-        TP_TRY(launched(tp::launch_bpback3_tiled(cubic, g, tile_spec(g, cubic), gdata, gw, proj, rot, shifts, gproj,
-                                                 gweights, grot, gshift, s),
+    CallScratch sc;
+    if (tiles) {
+        const tp::TileSpec ts = tile_spec(g, cubic);
+        TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_bpback3_tiled(cubic, g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
+                                                 gshift, sc.p, 0, s),
                         "tiled backprojection backward launch"));
-    if (tiles2)
-        TP_TRY(launched(tp::launch_gather2_tiled(cubic, 2, g, tile_spec2(g, cubic), gdata, gw, rot, shifts, gproj,
-                                                 (gw && gweights) ? gweights : nullptr, proj, grot, gshift, s),
+    }
+    if (tiles2) {
+        const tp::TileSpec2 ts = tile_spec2(g, cubic);
+        TP_TRY(call_poses(2, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(launched(tp::launch_gather2_tiled(cubic, 2, g, ts, gdata, gw, rot, shifts, gproj,
+                                                 (gw && gweights) ? gweights : nullptr, proj, grot, gshift, sc.p, 0, s),
                         "tiled backprojection backward launch"));
+    }
     return launched(tp::launch_backproject_back(dim, dtype, cubic, g, gdata, gw, proj, rot, shifts, gproj, gweights,
                                                 grot, gshift, s, tiles2 || tiles),
                     "backprojection backward launch");

@@ -77,6 +77,28 @@ struct TileSpec2 {
     int kp_gather;          // gather (forward): poses per wavefront batch
 };
 
+// Per-call summary of the poses, written into a device scratch area by
+// launch_call_poses before the tiled kernels of the call (stream order) and
+// read by them: the rotation kernels do nothing when no pose is a rotation,
+// the kernels of the other tiled poses (GEN) exit at once when there is no
+// such pose, and the persistent kernels take their work from per-XCD
+// counters.  A call runs at most kTiledPairs (rotation, GEN) kernel pairs;
+// pair `gl` uses counter sets 2 gl (rotations) and 2 gl + 1 (GEN).
+constexpr int kXcdCount = 8;    // XCDs of an MI355X (workgroups are dealt to them round-robin)
+constexpr int kTiledPairs = 2;
+struct CallPoses {
+    int any_rot;      // some pose of the call is a rotation
+    float gen_reach;  // rho_unit * (largest singular value of the other tiled poses) + 1; 0: none
+    int pad[14];
+    unsigned next[2 * kTiledPairs][kXcdCount];  // batches of slots taken so far (zeroed by the pre-pass)
+};
+constexpr int kCallScratchBytes = 256;
+static_assert(sizeof(CallPoses) <= kCallScratchBytes, "call scratch");
+
+// Fill *cp for the B_rot * P poses at rot (dim 2 or 3), rho_unit = the
+// TileSpec/TileSpec2 field of the call.
+hipError_t launch_call_poses(int dim, int64_t poses, const void* rot, float rho_unit, CallPoses* cp, hipStream_t s);
+
 constexpr int kBlock = 256;
 constexpr int64_t kMaxGrid = int64_t(1) << 22;
 
@@ -106,33 +128,36 @@ hipError_t launch_backproject_forw(int dim, int dt, bool cubic, const Geom& g, c
                                    bool rest_only = false);
 // fp32 3D tile-owner paths (tiled poses only; the per-pixel kernels with
 // `rest_only` complete the other poses and the masked pixels).  Each launches
-// the rotation kernel and then the kernel of the other tiled poses.
+// the rotation kernel and then the kernel of the other tiled poses, after
+// launch_call_poses has filled *cp; `gl` (< kTiledPairs) picks their
+// counters, distinct for the kernel pairs of one call.
 // `rec_half`: the volume is stored as complex half and widened to fp32 on load.
 hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* rec,
-                                      const void* rot, const void* shifts, void* out, hipStream_t s,
-                                      bool rec_half = false);
+                                      const void* rot, const void* shifts, void* out, CallPoses* cp, int gl,
+                                      hipStream_t s, bool rec_half = false);
 // Rotation/shift gradients of project_3d_to_2d_back for tiled poses, added
 // into zero-filled grot / gshift (either may be null).
 hipError_t launch_grads3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gproj, const void* rec,
-                               const void* rot, const void* shifts, void* grot, void* gshift, hipStream_t s);
+                               const void* rot, const void* shifts, void* grot, void* gshift, CallPoses* cp, int gl,
+                               hipStream_t s);
 // backproject_2d_to_3d_back for tiled poses into zero-filled outputs:
 // grad_projections from grad_data_rec, grad_weights from grad_weight_rec (when
 // both gw and gweights are given), rotation/shift gradients (either may be null).
 hipError_t launch_bpback3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gdata, const void* gw,
                                 const void* proj, const void* rot, const void* shifts, void* gproj, void* gweights,
-                                void* grot, void* gshift, hipStream_t s);
+                                void* grot, void* gshift, CallPoses* cp, int gl, hipStream_t s);
 // mode 0: backprojection into data (+ weights), with the x = 0 Hermitian completion;
 // mode 1: reconstruction gradient of the projection.
 hipError_t launch_scatter3_tiled(bool cubic, int mode, const Geom& g, const TileSpec& ts, const void* src,
                                  const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
-                                 hipStream_t s);
+                                 CallPoses* cp, int gl, hipStream_t s);
 
 // fp32 2D tile-owner scatter (tiled poses only), into zero-filled dst / wdst.
 // mode 0: backprojection with the x = 0 Hermitian completion; mode 1:
 // reconstruction gradient of the projection.
 hipError_t launch_scatter2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* src,
                                  const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
-                                 hipStream_t s);
+                                 CallPoses* cp, int gl, hipStream_t s);
 // fp32 2D tile-owner gathers (tiled poses only; the per-pixel kernels with
 // `rest` complete the other poses and the masked pixels).  mode 0: forward
 // (rec -> out); mode 1: rotation/shift gradients of project_2d_back (gsrc =
@@ -142,7 +167,8 @@ hipError_t launch_scatter2_tiled(bool cubic, int mode, const Geom& g, const Tile
 // `rec_half` (mode 0): the volume is stored as complex half and widened to fp32 on load.
 hipError_t launch_gather2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* rec,
                                 const void* gw, const void* rot, const void* shifts, void* out, void* wout,
-                                const void* gsrc, void* grot, void* gshift, hipStream_t s, bool rec_half = false);
+                                const void* gsrc, void* grot, void* gshift, CallPoses* cp, int gl, hipStream_t s,
+                                bool rec_half = false);
 
 // Reference preparation (tp_fourier.hip).  Elements are opaque words of
 // elem_bytes (2, 4, 8 or 16); `dim` spatial axes (2 or 3) after the batch.

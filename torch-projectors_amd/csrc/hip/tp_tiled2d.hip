@@ -310,7 +310,8 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
                                                              const float* __restrict__ weights,
                                                              const float* __restrict__ rot,
                                                              const float* __restrict__ shifts,
-                                                             Cx<float>* __restrict__ dst, float* __restrict__ wdst) {
+                                                             Cx<float>* __restrict__ dst, float* __restrict__ wdst,
+                                                             CallPoses* __restrict__ cp, int gl) {
     constexpr int SL = CUBIC ? 2 : 1, SH = CUBIC ? 1 : 0;  // stencil reach below / above floor(x)
     constexpr int SLOW = CUBIC ? 1 : 0;                    // first tap at floor(x) - SLOW
     constexpr int RPS = 64 / KP;
@@ -325,22 +326,29 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
     __shared__ int pcnt[2];
     __shared__ Slot2 slots[NW][KP];
     __shared__ int marks[NW][64];
-    __shared__ int part[NW];
+    __shared__ int gen_sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slot = lane / RPS, jrow = lane % RPS;
     const int N = g.N, H = g.H, half = N / 2;
-    // samples lie within |x| <= rho_k: rotations reach rho_unit + 1, GEN poses up to kScaleMax
-    // times farther (the call's own largest singular value), over a wider range of tiles
+    // samples lie within |x| <= rho_k: rotations reach rho_unit + 1 (and have nothing to do when
+    // the call has none); GEN poses the call's own reach, up to kScaleMax times farther, over
+    // the tiles within it (the same rule as the host's for the rotations' and the widest range)
+    const int any_rot = GEN ? 1 : call_flag(&cp->any_rot);
     float rho_k = ts.rho_unit + 1.0f;
+    int tkr0 = ts.kr0, tnr = ts.nr, tnc = ts.nc;
     if constexpr (GEN) {
-        rho_k = fminf(ts.rho, general_reach<2, kThreads>(rot, g.B_rot * g.P, ts.rho_unit, part));
-        if (rho_k <= 0.f) return;  // no such pose in this call
+        rho_k = fminf(ts.rho, cp->gen_reach);
+        if (!(rho_k > 0.f)) return;  // no such pose in this call
+        const float reach = fminf(rho_k + 3.0f, float(N));
+        tkr0 = max(ts.kr0_2, int(floorf((-reach + float(half - 1)) / float(TR))));
+        const int kr1 = min(ts.kr0_2 + ts.nr_2, int(floorf((reach + float(half - 1)) / float(TR))) + 1);
+        tnr = max(0, kr1 - tkr0);
+        tnc = min(ts.nc_2, int(floorf(reach / float(TC))) + 1);
     }
-    const int tkr0 = GEN ? ts.kr0_2 : ts.kr0, tnr = GEN ? ts.nr_2 : ts.nr, tnc = GEN ? ts.nc_2 : ts.nc;
     const int64_t items = g.B * ts.ksplit * int64_t(tnr) * tnc;
     const float cut2 = float(g.cut2);
-    const int64_t per = xcd_per<kRun>(items);
-    for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
+    for (Slots<GEN> sl(xcd_per<kRun>(items), slot_counters<GEN>(cp, gl), &gen_sh); sl.ok(); sl.next(&gen_sh)) {
+        const int64_t slot_i = sl.s;
         const int64_t w = xcd_item<kRun>(slot_i);
         if (w >= items) continue;
         // items: tile column fastest, then tile row, pose range, batch
@@ -351,6 +359,7 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
         const int jr = int(q % ts.ksplit);
         const int64_t b = q / ts.ksplit;
         const int p0 = jr * ts.prange, p1 = min(int(g.P), p0 + ts.prange);
+        if (!any_rot) return;  // rotation kernel, no rotation in the call
         // stored cells of this tile, signed coordinates: r in [-N/2+1, N/2], c in [0, N/2]
         const int tc = kc * TC, tr = -half + 1 + kr * TR;
         const int fc0 = -tc - TC + 1, fr0 = -tr - TR + 1;
@@ -564,12 +573,12 @@ unsigned grid2_of(int64_t items) {
 
 template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool PRIV, bool GEN>
 hipError_t scatter2_one(const Geom& g, const TileSpec2& ts, const void* src, const void* weights, const void* rot,
-                        const void* shifts, void* dst, void* wdst, hipStream_t s) {
+                        const void* shifts, void* dst, void* wdst, CallPoses* cp, int gl, hipStream_t s) {
     const int64_t work = g.B * ts.ksplit * (GEN ? int64_t(ts.nr_2) * ts.nc_2 : int64_t(ts.nr) * ts.nc);
     if (work == 0) return hipSuccess;
     hipLaunchKernelGGL((k_scatter2_tiled<CUBIC, MODE, WEIGHTS, KP, PRIV, GEN>), dim3(grid2_of<GEN>(work)),
                        dim3(kThreads), 0, s, g, ts, (const Cx<float>*)src, (const float*)weights, (const float*)rot,
-                       (const float*)shifts, (Cx<float>*)dst, (float*)wdst);
+                       (const float*)shifts, (Cx<float>*)dst, (float*)wdst, cp, gl);
     return hipGetLastError();
 }
 
@@ -578,22 +587,22 @@ hipError_t scatter2_one(const Geom& g, const TileSpec2& ts, const void* src, con
 // of a cell) when that is 1.5 or more.
 template <bool CUBIC, int MODE, bool WEIGHTS, bool GEN>
 hipError_t scatter2_kp(const Geom& g, const TileSpec2& ts, const void* src, const void* weights, const void* rot,
-                       const void* shifts, void* dst, void* wdst, hipStream_t s) {
+                       const void* shifts, void* dst, void* wdst, CallPoses* cp, int gl, hipStream_t s) {
     if (g.os * (GEN ? kScaleMin : 1.0) >= kPrivOs)
-        return scatter2_one<CUBIC, MODE, WEIGHTS, 1, true, GEN>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-    if (ts.kp >= 4) return scatter2_one<CUBIC, MODE, WEIGHTS, 4, false, GEN>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-    if (ts.kp == 2) return scatter2_one<CUBIC, MODE, WEIGHTS, 2, false, GEN>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-    return scatter2_one<CUBIC, MODE, WEIGHTS, 1, false, GEN>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+        return scatter2_one<CUBIC, MODE, WEIGHTS, 1, true, GEN>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
+    if (ts.kp >= 4) return scatter2_one<CUBIC, MODE, WEIGHTS, 4, false, GEN>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
+    if (ts.kp == 2) return scatter2_one<CUBIC, MODE, WEIGHTS, 2, false, GEN>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
+    return scatter2_one<CUBIC, MODE, WEIGHTS, 1, false, GEN>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
 }
 
 // Rotations, then the other tiled poses (both add into the zero-filled image), then the
 // x = 0 completion of the backprojection.
 template <bool CUBIC, int MODE, bool WEIGHTS>
 hipError_t scatter2_all(const Geom& g, const TileSpec2& ts, const void* src, const void* weights, const void* rot,
-                        const void* shifts, void* dst, void* wdst, hipStream_t s) {
-    hipError_t e = scatter2_kp<CUBIC, MODE, WEIGHTS, false>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+                        const void* shifts, void* dst, void* wdst, CallPoses* cp, int gl, hipStream_t s) {
+    hipError_t e = scatter2_kp<CUBIC, MODE, WEIGHTS, false>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
     if (e != hipSuccess) return e;
-    e = scatter2_kp<CUBIC, MODE, WEIGHTS, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+    e = scatter2_kp<CUBIC, MODE, WEIGHTS, true>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
     if (e != hipSuccess || MODE != 0) return e;
     int64_t blocks = (g.B * g.N + kBlock - 1) / kBlock;
     if (blocks > 65536) blocks = 65536;
@@ -665,7 +674,8 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
                                                             const float* __restrict__ shifts,
                                                             Cx<float>* __restrict__ out, float* __restrict__ wout,
                                                             const Cx<float>* __restrict__ gsrc,
-                                                            float* __restrict__ grot, float* __restrict__ gshift) {
+                                                            float* __restrict__ grot, float* __restrict__ gshift,
+                                                            CallPoses* __restrict__ cp, int gl) {
     static_assert(GMODE == 0 || KP == 1, "the gradient modes sum one pose per wave batch");
     static_assert(GMODE == 0 || std::is_same<VS, float>::value, "complex-half volumes are read by the forward only");
     constexpr int LO = CUBIC ? 1 : 0, HI = CUBIC ? 2 : 1, WC = GC + LO + HI, WR = GR + LO + HI, W2 = WC * WR;
@@ -678,22 +688,27 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
     __shared__ int pcnt[2];
     __shared__ Slot2 slots[NW][KP];
     __shared__ int marks[NW][64];
-    __shared__ int part[NW];
+    __shared__ int gen_sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slot = lane / RPS, jrow = lane % RPS;
     const int N = g.N, H = g.H;
-    // samples lie within |x| <= rho_k: rotations reach rho_unit + 1, GEN poses up to kScaleMax
-    // times farther (the call's own largest singular value), on a wider grid of tiles
+    // samples lie within |x| <= rho_k: rotations reach rho_unit + 1 (and have nothing to do when
+    // the call has none); GEN poses the call's own reach, up to kScaleMax times farther, on the
+    // part of the wide grid that this reach needs
+    const int any_rot = GEN ? 1 : call_flag(&cp->any_rot);
     float rho_k = ts.rho_unit + 1.0f;
+    int gnt = ts.gnt, gorg = ts.gorg;
     if constexpr (GEN) {
-        rho_k = fminf(ts.rho, general_reach<2, kThreads>(rot, g.B_rot * g.P, ts.rho_unit, part));
-        if (rho_k <= 0.f) return;  // no such pose in this call
+        rho_k = fminf(ts.rho, cp->gen_reach);
+        if (!(rho_k > 0.f)) return;  // no such pose in this call
+        const int h = half_tiles_for(rho_k, GC, ts.gnt2 / 2);
+        gnt = 2 * h;
+        gorg = ts.gorg2 + (ts.gnt2 / 2 - h) * GC;
     }
-    const int gnt = GEN ? ts.gnt2 : ts.gnt, gorg = GEN ? ts.gorg2 : ts.gorg;
     const int64_t items = g.B * ts.gksplit * int64_t(gnt) * gnt;
     const float cut2 = float(g.cut2);
-    const int64_t per = xcd_per<kRun>(items);
-    for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
+    for (Slots<GEN> sl(xcd_per<kRun>(items), slot_counters<GEN>(cp, gl), &gen_sh); sl.ok(); sl.next(&gen_sh)) {
+        const int64_t slot_i = sl.s;
         const int64_t w = xcd_item<kRun>(slot_i);
         if (w >= items) continue;
         const int kc = int(w % gnt);
@@ -703,6 +718,7 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
         const int jr = int(q % ts.gksplit);
         const int64_t b = q / ts.gksplit;
         const int p0 = jr * ts.gprange, p1 = min(int(g.P), p0 + ts.gprange);
+        if (!any_rot) return;  // rotation kernel, no rotation in the call
         const int tc = gorg + kc * GC, tr = gorg + kr * GR;
         // samples owned by this tile: floor(x) in [t, t + edge) on both axes (+ slack)
         const float lo[2] = {float(tc) - ts.eps, float(tr) - ts.eps};
@@ -880,14 +896,14 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
 template <bool CUBIC, int KP, int GMODE, bool RS, bool WG, typename VS = float>
 hipError_t gather2_launch(const Geom& g, const TileSpec2& ts, const void* rec, const void* gw, const void* rot,
                           const void* shifts, void* out, void* wout, const void* gsrc, void* grot, void* gshift,
-                          hipStream_t s) {
+                          CallPoses* cp, int gl, hipStream_t s) {
     // rotations, then the other tiled poses (their samples and gradient terms are their own)
     const int64_t work = g.B * ts.gksplit * int64_t(ts.gnt) * ts.gnt;
     if (work > 0) {
         hipLaunchKernelGGL((k_gather2_tiled<CUBIC, KP, GMODE, RS, WG, VS, false>), dim3(grid2_of<false>(work)),
                            dim3(kThreads), 0, s, g, ts, (const Cx<VS>*)rec, (const float*)gw, (const float*)rot,
                            (const float*)shifts, (Cx<float>*)out, (float*)wout, (const Cx<float>*)gsrc,
-                           (float*)grot, (float*)gshift);
+                           (float*)grot, (float*)gshift, cp, gl);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -896,68 +912,68 @@ hipError_t gather2_launch(const Geom& g, const TileSpec2& ts, const void* rec, c
     hipLaunchKernelGGL((k_gather2_tiled<CUBIC, KP, GMODE, RS, WG, VS, true>), dim3(grid2_of<true>(work2)),
                        dim3(kThreads), 0, s, g, ts, (const Cx<VS>*)rec, (const float*)gw, (const float*)rot,
                        (const float*)shifts, (Cx<float>*)out, (float*)wout, (const Cx<float>*)gsrc, (float*)grot,
-                       (float*)gshift);
+                       (float*)gshift, cp, gl);
     return hipGetLastError();
 }
 
 template <bool CUBIC, typename VS>
 hipError_t gather2_forw(const Geom& g, const TileSpec2& ts, const void* rec, const void* rot, const void* shifts,
-                        void* out, hipStream_t s) {
+                        void* out, CallPoses* cp, int gl, hipStream_t s) {
     if (ts.kp_gather >= 4)
         return gather2_launch<CUBIC, 4, 0, false, false, VS>(g, ts, rec, nullptr, rot, shifts, out, nullptr, nullptr,
-                                                             nullptr, nullptr, s);
+                                                             nullptr, nullptr, cp, gl, s);
     if (ts.kp_gather == 2)
         return gather2_launch<CUBIC, 2, 0, false, false, VS>(g, ts, rec, nullptr, rot, shifts, out, nullptr, nullptr,
-                                                             nullptr, nullptr, s);
+                                                             nullptr, nullptr, cp, gl, s);
     return gather2_launch<CUBIC, 1, 0, false, false, VS>(g, ts, rec, nullptr, rot, shifts, out, nullptr, nullptr,
-                                                         nullptr, nullptr, s);
+                                                         nullptr, nullptr, cp, gl, s);
 }
 
 template <bool CUBIC>
 hipError_t gather2_modes(int mode, const Geom& g, const TileSpec2& ts, const void* rec, const void* gw,
                          const void* rot, const void* shifts, void* out, void* wout, const void* gsrc, void* grot,
-                         void* gshift, hipStream_t s) {
-    if (mode == 0) return gather2_forw<CUBIC, float>(g, ts, rec, rot, shifts, out, s);
+                         void* gshift, CallPoses* cp, int gl, hipStream_t s) {
+    if (mode == 0) return gather2_forw<CUBIC, float>(g, ts, rec, rot, shifts, out, cp, gl, s);
     if (mode == 1)
-        return gather2_launch<CUBIC, 1, 1, true, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, s);
+        return gather2_launch<CUBIC, 1, 1, true, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, cp, gl, s);
     const bool rs = grot || gshift;
     if (wout)
         return rs ? gather2_launch<CUBIC, 1, 2, true, true>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
-                                                            gshift, s)
+                                                            gshift, cp, gl, s)
                   : gather2_launch<CUBIC, 1, 2, false, true>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
-                                                             gshift, s);
-    return rs ? gather2_launch<CUBIC, 1, 2, true, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, s)
+                                                             gshift, cp, gl, s);
+    return rs ? gather2_launch<CUBIC, 1, 2, true, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, cp, gl, s)
               : gather2_launch<CUBIC, 1, 2, false, false>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
-                                                          gshift, s);
+                                                          gshift, cp, gl, s);
 }
 
 }  // namespace
 
 hipError_t launch_gather2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* rec,
                                 const void* gw, const void* rot, const void* shifts, void* out, void* wout,
-                                const void* gsrc, void* grot, void* gshift, hipStream_t s, bool rec_half) {
+                                const void* gsrc, void* grot, void* gshift, CallPoses* cp, int gl, hipStream_t s, bool rec_half) {
     if (rec_half) {
         if (mode != 0) return hipErrorInvalidValue;
-        return cubic ? gather2_forw<true, __half>(g, ts, rec, rot, shifts, out, s)
-                     : gather2_forw<false, __half>(g, ts, rec, rot, shifts, out, s);
+        return cubic ? gather2_forw<true, __half>(g, ts, rec, rot, shifts, out, cp, gl, s)
+                     : gather2_forw<false, __half>(g, ts, rec, rot, shifts, out, cp, gl, s);
     }
     if (mode == 1 && !grot && !gshift) return hipSuccess;
-    return cubic ? gather2_modes<true>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, s)
-                 : gather2_modes<false>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, s);
+    return cubic ? gather2_modes<true>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, cp, gl, s)
+                 : gather2_modes<false>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, cp, gl, s);
 }
 
 hipError_t launch_scatter2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* src,
                                  const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
-                                 hipStream_t s) {
+                                 CallPoses* cp, int gl, hipStream_t s) {
     if (mode == 0) {
         if (weights)
-            return cubic ? scatter2_all<true, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s)
-                         : scatter2_all<false, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-        return cubic ? scatter2_all<true, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
-                     : scatter2_all<false, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
+            return cubic ? scatter2_all<true, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s)
+                         : scatter2_all<false, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
+        return cubic ? scatter2_all<true, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, cp, gl, s)
+                     : scatter2_all<false, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, cp, gl, s);
     }
-    return cubic ? scatter2_all<true, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
-                 : scatter2_all<false, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
+    return cubic ? scatter2_all<true, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, cp, gl, s)
+                 : scatter2_all<false, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, cp, gl, s);
 }
 
 }  // namespace tp

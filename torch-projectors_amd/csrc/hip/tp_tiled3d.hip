@@ -193,9 +193,16 @@ struct Slot {
     int64_t base;
 };
 
+// The tiled kernels read columns 0 and 1 of a pose only (the slice plane and
+// its sample grid); column 2 is not loaded (zero), which cuts the bytes the
+// pose culls read per tile by a third.
 __device__ __forceinline__ void load_rot(const float* __restrict__ Rg, float* R) {
 #pragma unroll
-    for (int e = 0; e < 9; ++e) R[e] = Rg[e];
+    for (int k = 0; k < 3; ++k) {
+        R[3 * k] = Rg[3 * k];
+        R[3 * k + 1] = Rg[3 * k + 1];
+        R[3 * k + 2] = 0.f;
+    }
 }
 // Rotation and shift of pose p (shifts may be absent: zeros).
 __device__ __forceinline__ void load_pose(const float* __restrict__ rotb, const float* __restrict__ shb, int p,
@@ -250,7 +257,8 @@ __device__ __forceinline__ Item item_of(int64_t w, int64_t B, int P, int nd, int
 
 // Poses culled per phase: each lane tests kChunk / NT of them, the survivors'
 // indices (relative to the phase) go to an LDS list.
-constexpr int kCullInFlight = 2;  // rotations loaded together per lane
+constexpr int kCullInFlight = 2;  // rotations loaded together per lane (scatter)
+constexpr int kCullInFlightF = 2; // the same, forward
 constexpr int kChunk = 1024;      // poses culled per phase
 
 // List entries: pose index relative to the phase, plus which boxes it crosses.
@@ -267,15 +275,15 @@ __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pe
     if (threadIdx.x == 0) *pcount = 0;
     __syncthreads();
 #pragma unroll 1
-    for (int q0 = 0; q0 < CH / NT; q0 += kCullInFlight) {
-        float R[kCullInFlight][9];
+    for (int q0 = 0; q0 < CH / NT; q0 += kCullInFlightF) {
+        float R[kCullInFlightF][9];
 #pragma unroll
-        for (int q = 0; q < kCullInFlight; ++q) {
+        for (int q = 0; q < kCullInFlightF; ++q) {
             const int p = min(pbase + int(threadIdx.x) + (q0 + q) * NT, pend - 1);
             load_rot(rotb + int64_t(p) * 9, R[q]);
         }
 #pragma unroll
-        for (int q = 0; q < kCullInFlight; ++q) {
+        for (int q = 0; q < kCullInFlightF; ++q) {
             const int p = pbase + int(threadIdx.x) + (q0 + q) * NT;
             if (p >= pend) continue;
             const bool h1 = pose_hits<GEN>(R[q], lo1, hi1), h2 = TWO && pose_hits<GEN>(R[q], lo2, hi2);
@@ -394,8 +402,8 @@ template <bool CUBIC, int KP, bool OSX, int GMODE = 0, bool RS = true, bool WG =
 __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec ts, const Cx<VS>* __restrict__ rec,
                                                         const float* __restrict__ rot,
                                                         const float* __restrict__ shifts,
-                                                        Cx<float>* __restrict__ out,
-                                                        const Cx<float>* __restrict__ gsrc = nullptr,
+                                                        Cx<float>* __restrict__ out, CallPoses* __restrict__ cp,
+                                                        int gl, const Cx<float>* __restrict__ gsrc = nullptr,
                                                         float* __restrict__ grot = nullptr,
                                                         float* __restrict__ gshift = nullptr,
                                                         const float* __restrict__ gw = nullptr,
@@ -419,26 +427,36 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
     constexpr int QCAP = 256;
     __shared__ Slot slots[NW][KP];
     __shared__ unsigned queue[NW][QCAP];
-    __shared__ int part[NW];
+    __shared__ int gen_sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slot = lane / RPS, jrow = lane % RPS;
-    // samples lie within |x| <= rho_k: rotations reach rho_unit + 1; GEN poses up to kScaleMax
-    // times farther (the call's own largest singular value), on a tile grid that far out
+    // samples lie within |x| <= rho_k: rotations reach rho_unit + 1 (and have nothing to do when
+    // the call has none); GEN poses the call's own reach, up to kScaleMax times farther, over
+    // the part of the wide grid that this reach needs
+    const int any_rot = GEN ? 1 : call_flag(&cp->any_rot);
     float rho_k = ts.rho_unit + 1.0f;
+    int nt = ts.nt, ntd = ts.ntfd, org = ts.org, orgd = ts.orgd;
+    int fc0 = ts.fc0, fc1 = ts.fc1, fd0 = ts.fd0, fd1 = ts.fd1;
     if constexpr (GEN) {
-        rho_k = fminf(ts.rho, general_reach<3, NT>(rot, g.B_rot * g.P, ts.rho_unit, part));
-        if (rho_k <= 0.f) return;  // no such pose in this call
+        rho_k = fminf(ts.rho, cp->gen_reach);
+        if (!(rho_k > 0.f)) return;  // no such pose in this call
+        const int h = half_tiles_for(rho_k, L, ts.nt2 / 2), hd = half_tiles_for(rho_k, LD, ts.ntfd2 / 2);
+        const int off = ts.nt2 / 2 - h, offd = ts.ntfd2 / 2 - hd;
+        nt = 2 * h;
+        ntd = 2 * hd;
+        org = ts.org2 + off * L;
+        orgd = ts.orgd2 + offd * LD;
+        fc0 = min(nt, max(0, ts.fc0_2 - off));
+        fc1 = min(nt, max(fc0, ts.fc1_2 - off));
+        fd0 = min(ntd, max(0, ts.fd0_2 - offd));
+        fd1 = min(ntd, max(fd0, ts.fd1_2 - offd));
     }
     const float rho2 = rho_k * rho_k;
-    const int nt = GEN ? ts.nt2 : ts.nt, ntd = GEN ? ts.ntfd2 : ts.ntfd;
-    const int org = GEN ? ts.org2 : ts.org, orgd = GEN ? ts.orgd2 : ts.orgd;
-    const int fc0 = GEN ? ts.fc0_2 : ts.fc0, fc1 = GEN ? ts.fc1_2 : ts.fc1;
-    const int fd0 = GEN ? ts.fd0_2 : ts.fd0, fd1 = GEN ? ts.fd1_2 : ts.fd1;
     const int64_t items = g.B * (int64_t(fc1 - fc0) * (fc1 - fc0) * (fd1 - fd0) * ts.ksplit + int64_t(nt) * nt * ntd);
     const float cut2 = float(g.cut2);
     const int N = g.N, H = g.H;
-    const int64_t per = xcd_per<kRunForw>(items);
-    for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
+    for (Slots<GEN> sl(xcd_per<kRunForw>(items), slot_counters<GEN>(cp, gl), &gen_sh); sl.ok(); sl.next(&gen_sh)) {
+        const int64_t slot_i = sl.s;
         const int64_t w = xcd_item<kRunForw>(slot_i);
         if (w >= items) continue;
         const Item it = item_of(w, g.B, int(g.P), ntd, nt, nt, fd0, fd1, fc0, fc1, fc0, fc1, ts.ksplit, ts.prange);
@@ -456,6 +474,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
             dist2 += q * q;
         }
         if (dist2 > rho2) continue;
+        if (!any_rot) return;  // rotation kernel, no rotation in the call
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
         const float* rotb = rot + rb * g.P * 9;
         const Cx<VS>* recb = rec + b * g.vol;
@@ -785,7 +804,8 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                                                            const float* __restrict__ weights,
                                                            const float* __restrict__ rot,
                                                            const float* __restrict__ shifts,
-                                                           Cx<float>* __restrict__ dst, float* __restrict__ wdst) {
+                                                           Cx<float>* __restrict__ dst, float* __restrict__ wdst,
+                                                           CallPoses* __restrict__ cp, int gl) {
     constexpr int SL = CUBIC ? 2 : 1, SH = CUBIC ? 1 : 0;  // stencil reach below / above floor(x)
     constexpr int SLOW = CUBIC ? 1 : 0;                    // first tap at floor(x) - SLOW
     constexpr int RPS = 64 / KP;
@@ -796,27 +816,30 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
     __shared__ int pcnt[2];
     __shared__ Slot slots[NW][KP];
     __shared__ int marks[NW][64];
-    __shared__ int part[NW];
+    __shared__ int gen_sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slot = lane / RPS, jrow = lane % RPS;
     const int N = g.N, H = g.H, half = N / 2;
     const int64_t items = g.B * (int64_t(ts.sd1 - ts.sd0) * (ts.sr1 - ts.sr0) * ts.sc1 * ts.ksplit +
                                  int64_t(ts.ntd) * ts.ntr * ts.ntc);
     const float cut2 = float(g.cut2);
-    // samples lie within |x| <= rho_k: rotations reach rho_unit + 1, GEN poses up to kScaleMax
-    // times farther (the call's own largest singular value)
+    // samples lie within |x| <= rho_k: rotations reach rho_unit + 1, GEN poses the call's own
+    // reach (up to kScaleMax times farther).  Without rotations in the call the rotation kernel
+    // does nothing at all and GEN stores every tile it owns; with them GEN adds onto the tiles.
+    const int any_rot = call_flag(&cp->any_rot);
     float rho_k = ts.rho_unit + 1.0f;
     if constexpr (GEN) {
-        rho_k = fminf(ts.rho, general_reach<3, NT>(rot, g.B_rot * g.P, ts.rho_unit, part));
-        if (rho_k <= 0.f) return;  // no such pose in this call
+        rho_k = fminf(ts.rho, cp->gen_reach);
+        if (!(rho_k > 0.f)) return;  // no such pose in this call
     }
-    const int64_t per = xcd_per<kRunScatter>(items);
-    for (int64_t slot_i = blockIdx.x; slot_i < kXcds * per; slot_i += gridDim.x) {
+    for (Slots<GEN> sl(xcd_per<kRunScatter>(items), slot_counters<GEN>(cp, gl), &gen_sh); sl.ok(); sl.next(&gen_sh)) {
+        const int64_t slot_i = sl.s;
         const int64_t w = xcd_item<kRunScatter>(slot_i);
         if (w >= items) continue;
         const Item it = item_of(w, g.B, int(g.P), ts.ntd, ts.ntr, ts.ntc, ts.sd0, ts.sd1, ts.sr0, ts.sr1, 0, ts.sc1,
                                 ts.ksplit, ts.prange);
         if (it.skip) continue;
+        if (!GEN && !any_rot && call_reach(&cp->gen_reach) > 0.f) return;  // GEN stores every tile
         const int64_t b = it.b;
         // stored cells of this tile, signed coordinates: d, r in [-N/2+1, N/2], c in [0, N/2]
         const int tc = it.kc * SC, tr = -half + 1 + it.kr * SR, td = -half + 1 + it.kd * SD;
@@ -845,10 +868,11 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
             const float q = lo1[k] > 0.f ? lo1[k] : (hi1[k] < 0.f ? -hi1[k] : 0.f);
             dist2 += q * q;
         }
-        const int pend = dist2 > rho_k * rho_k ? it.p0 : it.p1;
+        // (a rotation kernel without rotations in the call only stores zeros)
+        const int pend = (dist2 > rho_k * rho_k || (!GEN && !any_rot)) ? it.p0 : it.p1;
 
         const float* shb = shifts ? shifts + sb * g.P * 2 : nullptr;
-        bool touched = false;  // GEN: some pose reaches the tile (else it is left as the rotations wrote it)
+        bool touched = false;  // GEN: some pose reaches the tile
         for (int pbase = it.p0; pbase < pend; pbase += kChunkSc) {
             int n1, n2;
             cull_chunk_boxes<NT, GEN>(rotb, pend, pbase, lo1, hi1, lo2, hi2, plist, pcnt, n1, n2);
@@ -963,9 +987,9 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
         }
 
         // write every stored cell of the tile once (core pieces add into a zeroed region).  GEN
-        // adds onto what the rotation launch wrote: its core pieces with atomics, its other
-        // tiles (one workgroup each) by a plain read and write
-        if (GEN && !touched) continue;
+        // adds onto what the rotation kernel wrote: core pieces with atomics, the other tiles (one
+        // workgroup each) by a plain read and write; without rotations in the call it stores them
+        if (GEN && !touched && (it.core || any_rot)) continue;
         __syncthreads();
         for (int e = tid; e < S3; e += NT) {
             const int lc = e % SC, lr = (e / SC) % SR, ld = e / (SC * SR);
@@ -978,7 +1002,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                 atomic_add(&dst[idx].re, float(acc_re[a]));
                 atomic_add(&dst[idx].im, float(acc_im[a]));
                 if (WEIGHTS) atomic_add(&wdst[idx], float(acc_w[a]));
-            } else if (GEN) {
+            } else if (GEN && any_rot) {
                 const Cx<float> o = dst[idx];
                 dst[idx] = Cx<float>{o.re + float(acc_re[a]), o.im + float(acc_im[a])};
                 if (WEIGHTS) wdst[idx] += float(acc_w[a]);
@@ -1042,7 +1066,8 @@ __global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<fl
     }
 }
 
-// Work items of the forward tile grid (GEN: the grid that general poses reach).
+// Work items of the forward tile grid: the unit grid (rotations), or for GEN the whole wide
+// grid, a bound on the part of it that a call's reach selects (the kernel's persistent grid).
 template <bool GEN>
 int64_t forw_items(const Geom& g, const TileSpec& ts) {
     const int nt = GEN ? ts.nt2 : ts.nt, ntd = GEN ? ts.ntfd2 : ts.ntfd;
@@ -1056,23 +1081,27 @@ unsigned grid_of(int64_t items) {
     return grid_for(GEN && slots > kGenGrid ? kGenGrid : slots);
 }
 
-template <bool CUBIC, int KP, bool OSX, typename VS>
-hipError_t forw_launch(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts,
-                       void* out, hipStream_t s) {
-    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP, OSX, 0, true, false, VS, false>),
+// One forward-family kernel (GMODE 0, 1, 2) for rotations, then for the other tiled poses.
+template <bool CUBIC, int KP, bool OSX, int GMODE, bool RS, bool WG, typename VS>
+hipError_t forw_both(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts,
+                     void* out, CallPoses* cp, int gl, const void* gsrc, void* grot, void* gshift, const void* gw,
+                     void* wout, hipStream_t s) {
+    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP, OSX, GMODE, RS, WG, VS, false>),
                        dim3(grid_of<false, kRunForw>(forw_items<false>(g, ts))), dim3(kForwThreads), 0, s, g, ts,
-                       (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
+                       (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out, cp, gl,
+                       (const Cx<float>*)gsrc, (float*)grot, (float*)gshift, (const float*)gw, (float*)wout);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP, OSX, 0, true, false, VS, true>),
+    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP, OSX, GMODE, RS, WG, VS, true>),
                        dim3(grid_of<true, kRunForw>(forw_items<true>(g, ts))), dim3(kForwThreads), 0, s, g, ts,
-                       (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out);
+                       (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out, cp, gl,
+                       (const Cx<float>*)gsrc, (float*)grot, (float*)gshift, (const float*)gw, (float*)wout);
     return hipGetLastError();
 }
 
 template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool OSX>
 hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
-                          const void* shifts, void* dst, void* wdst, hipStream_t s) {
+                          const void* shifts, void* dst, void* wdst, CallPoses* cp, int gl, hipStream_t s) {
     const int64_t score = int64_t(ts.sd1 - ts.sd0) * (ts.sr1 - ts.sr0) * ts.sc1 * ts.ksplit;
     if (score > 0) {
         const int64_t cells = g.B * int64_t((ts.sd1 - ts.sd0) * SD) * ((ts.sr1 - ts.sr0) * SR) * (ts.sc1 * SC);
@@ -1083,18 +1112,19 @@ hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, co
         const hipError_t ez = hipGetLastError();
         if (ez != hipSuccess) return ez;
     }
-    // rotations write every tile; the general poses add onto them
+    // rotations write every tile (none: the other tiled poses store them); the other tiled
+    // poses add onto them
     const int64_t work = g.B * (score + int64_t(ts.ntd) * ts.ntr * ts.ntc);
     hipLaunchKernelGGL((k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP, OSX, false>),
                        dim3(grid_of<false, kRunScatter>(work)), dim3(kScatterThreads), 0, s, g, ts,
                        (const Cx<float>*)src, (const float*)weights, (const float*)rot, (const float*)shifts,
-                       (Cx<float>*)dst, (float*)wdst);
+                       (Cx<float>*)dst, (float*)wdst, cp, gl);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP, OSX, true>),
                        dim3(grid_of<true, kRunScatter>(work)), dim3(kScatterThreads), 0, s, g, ts,
                        (const Cx<float>*)src, (const float*)weights, (const float*)rot, (const float*)shifts,
-                       (Cx<float>*)dst, (float*)wdst);
+                       (Cx<float>*)dst, (float*)wdst, cp, gl);
     e = hipGetLastError();
     if (e != hipSuccess || MODE != 0) return e;
     const int64_t pairs = g.B * int64_t(g.N) * g.N;
@@ -1107,134 +1137,107 @@ hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, co
 
 template <bool CUBIC, int MODE, bool WEIGHTS, bool OSX>
 hipError_t scatter_kp_osx(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
-                          const void* shifts, void* dst, void* wdst, hipStream_t s) {
+                          const void* shifts, void* dst, void* wdst, CallPoses* cp, int gl, hipStream_t s) {
     if (ts.kp_scatter >= 4)
-        return scatter_launch<CUBIC, MODE, WEIGHTS, 4, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+        return scatter_launch<CUBIC, MODE, WEIGHTS, 4, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
     if (ts.kp_scatter == 2)
-        return scatter_launch<CUBIC, MODE, WEIGHTS, 2, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-    return scatter_launch<CUBIC, MODE, WEIGHTS, 1, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, s);
+        return scatter_launch<CUBIC, MODE, WEIGHTS, 2, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
+    return scatter_launch<CUBIC, MODE, WEIGHTS, 1, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
 }
 
 template <bool CUBIC, int MODE, bool WEIGHTS>
 hipError_t scatter_kp(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
-                      const void* shifts, void* dst, void* wdst, hipStream_t s) {
-    if (ts.os_exact) return scatter_kp_osx<CUBIC, MODE, WEIGHTS, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-    return scatter_kp_osx<CUBIC, MODE, WEIGHTS, false>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-}
-
-template <bool CUBIC, bool OSX, bool GEN>
-hipError_t grads_one(const Geom& g, const TileSpec& ts, const void* gproj, const void* rec, const void* rot,
-                     const void* shifts, void* grot, void* gshift, hipStream_t s) {
-    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, 1, OSX, 1, true, false, float, GEN>),
-                       dim3(grid_of<GEN, kRunForw>(forw_items<GEN>(g, ts))), dim3(kForwThreads), 0, s, g, ts,
-                       (const Cx<float>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)nullptr,
-                       (const Cx<float>*)gproj, (float*)grot, (float*)gshift, nullptr, nullptr);
-    return hipGetLastError();
-}
-
-template <bool CUBIC, bool OSX>
-hipError_t grads_launch(const Geom& g, const TileSpec& ts, const void* gproj, const void* rec, const void* rot,
-                        const void* shifts, void* grot, void* gshift, hipStream_t s) {
-    const hipError_t e = grads_one<CUBIC, OSX, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, s);
-    if (e != hipSuccess) return e;
-    return grads_one<CUBIC, OSX, true>(g, ts, gproj, rec, rot, shifts, grot, gshift, s);
-}
-
-template <bool CUBIC, bool OSX, bool RS, bool WG, bool GEN>
-hipError_t bpback_one(const Geom& g, const TileSpec& ts, const void* gdata, const void* gw, const void* proj,
-                      const void* rot, const void* shifts, void* gproj, void* gweights, void* grot, void* gshift,
-                      hipStream_t s) {
-    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, 1, OSX, 2, RS, WG, float, GEN>),
-                       dim3(grid_of<GEN, kRunForw>(forw_items<GEN>(g, ts))), dim3(kForwThreads), 0, s, g, ts,
-                       (const Cx<float>*)gdata, (const float*)rot, (const float*)shifts, (Cx<float>*)gproj,
-                       (const Cx<float>*)proj, (float*)grot, (float*)gshift, (const float*)gw, (float*)gweights);
-    return hipGetLastError();
-}
-
-template <bool CUBIC, bool OSX, bool RS, bool WG>
-hipError_t bpback_launch(const Geom& g, const TileSpec& ts, const void* gdata, const void* gw, const void* proj,
-                         const void* rot, const void* shifts, void* gproj, void* gweights, void* grot, void* gshift,
-                         hipStream_t s) {
-    const hipError_t e = bpback_one<CUBIC, OSX, RS, WG, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights,
-                                                               grot, gshift, s);
-    if (e != hipSuccess) return e;
-    return bpback_one<CUBIC, OSX, RS, WG, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+                      const void* shifts, void* dst, void* wdst, CallPoses* cp, int gl, hipStream_t s) {
+    if (ts.os_exact)
+        return scatter_kp_osx<CUBIC, MODE, WEIGHTS, true>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
+    return scatter_kp_osx<CUBIC, MODE, WEIGHTS, false>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
 }
 
 template <bool CUBIC, bool OSX>
 hipError_t bpback_flags(const Geom& g, const TileSpec& ts, const void* gdata, const void* gw, const void* proj,
                         const void* rot, const void* shifts, void* gproj, void* gweights, void* grot, void* gshift,
-                        hipStream_t s) {
+                        CallPoses* cp, int gl, hipStream_t s) {
     const bool rs = grot || gshift, wg = gw && gweights;
     if (rs)
-        return wg ? bpback_launch<CUBIC, OSX, true, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
-                                                          gshift, s)
-                  : bpback_launch<CUBIC, OSX, true, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, nullptr, grot,
-                                                           gshift, s);
-    return wg ? bpback_launch<CUBIC, OSX, false, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
-                                                       gshift, s)
-              : bpback_launch<CUBIC, OSX, false, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, nullptr, grot,
-                                                        gshift, s);
+        return wg ? forw_both<CUBIC, 1, OSX, 2, true, true, float>(g, ts, gdata, rot, shifts, gproj, cp, gl, proj, grot,
+                                                                   gshift, gw, gweights, s)
+                  : forw_both<CUBIC, 1, OSX, 2, true, false, float>(g, ts, gdata, rot, shifts, gproj, cp, gl, proj,
+                                                                    grot, gshift, gw, nullptr, s);
+    return wg ? forw_both<CUBIC, 1, OSX, 2, false, true, float>(g, ts, gdata, rot, shifts, gproj, cp, gl, proj, grot,
+                                                                gshift, gw, gweights, s)
+              : forw_both<CUBIC, 1, OSX, 2, false, false, float>(g, ts, gdata, rot, shifts, gproj, cp, gl, proj, grot,
+                                                                 gshift, gw, nullptr, s);
 }
 
 template <bool CUBIC, bool OSX, typename VS>
 hipError_t forw_kp(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts, void* out,
-                   hipStream_t s) {
-    if (ts.kp_forw >= 4) return forw_launch<CUBIC, 4, OSX, VS>(g, ts, rec, rot, shifts, out, s);
-    if (ts.kp_forw == 2) return forw_launch<CUBIC, 2, OSX, VS>(g, ts, rec, rot, shifts, out, s);
-    return forw_launch<CUBIC, 1, OSX, VS>(g, ts, rec, rot, shifts, out, s);
+                   CallPoses* cp, int gl, hipStream_t s) {
+#define TP_FORW(KPV) \
+    forw_both<CUBIC, KPV, OSX, 0, true, false, VS>(g, ts, rec, rot, shifts, out, cp, gl, nullptr, nullptr, nullptr, \
+                                                   nullptr, nullptr, s)
+    if (ts.kp_forw >= 4) return TP_FORW(4);
+    if (ts.kp_forw == 2) return TP_FORW(2);
+    return TP_FORW(1);
+#undef TP_FORW
 }
 
 template <typename VS>
 hipError_t forw_store(bool cubic, const Geom& g, const TileSpec& ts, const void* rec, const void* rot,
-                      const void* shifts, void* out, hipStream_t s) {
+                      const void* shifts, void* out, CallPoses* cp, int gl, hipStream_t s) {
     if (cubic)
-        return ts.os_exact ? forw_kp<true, true, VS>(g, ts, rec, rot, shifts, out, s)
-                           : forw_kp<true, false, VS>(g, ts, rec, rot, shifts, out, s);
-    return ts.os_exact ? forw_kp<false, true, VS>(g, ts, rec, rot, shifts, out, s)
-                       : forw_kp<false, false, VS>(g, ts, rec, rot, shifts, out, s);
+        return ts.os_exact ? forw_kp<true, true, VS>(g, ts, rec, rot, shifts, out, cp, gl, s)
+                           : forw_kp<true, false, VS>(g, ts, rec, rot, shifts, out, cp, gl, s);
+    return ts.os_exact ? forw_kp<false, true, VS>(g, ts, rec, rot, shifts, out, cp, gl, s)
+                       : forw_kp<false, false, VS>(g, ts, rec, rot, shifts, out, cp, gl, s);
 }
 
 }  // namespace
 
 hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* rec,
-                                      const void* rot, const void* shifts, void* out, hipStream_t s, bool rec_half) {
-    if (rec_half) return forw_store<__half>(cubic, g, ts, rec, rot, shifts, out, s);
-    return forw_store<float>(cubic, g, ts, rec, rot, shifts, out, s);
+                                      const void* rot, const void* shifts, void* out, CallPoses* cp, int gl,
+                                      hipStream_t s, bool rec_half) {
+    if (rec_half) return forw_store<__half>(cubic, g, ts, rec, rot, shifts, out, cp, gl, s);
+    return forw_store<float>(cubic, g, ts, rec, rot, shifts, out, cp, gl, s);
 }
 
 hipError_t launch_grads3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gproj, const void* rec,
-                               const void* rot, const void* shifts, void* grot, void* gshift, hipStream_t s) {
+                               const void* rot, const void* shifts, void* grot, void* gshift, CallPoses* cp, int gl,
+                               hipStream_t s) {
     if (!grot && !gshift) return hipSuccess;
-    if (cubic)
-        return ts.os_exact ? grads_launch<true, true>(g, ts, gproj, rec, rot, shifts, grot, gshift, s)
-                           : grads_launch<true, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, s);
-    return ts.os_exact ? grads_launch<false, true>(g, ts, gproj, rec, rot, shifts, grot, gshift, s)
-                       : grads_launch<false, false>(g, ts, gproj, rec, rot, shifts, grot, gshift, s);
+#define TP_GRADS(C, O) \
+    forw_both<C, 1, O, 1, true, false, float>(g, ts, rec, rot, shifts, nullptr, cp, gl, gproj, grot, gshift, nullptr, \
+                                              nullptr, s)
+    if (cubic) return ts.os_exact ? TP_GRADS(true, true) : TP_GRADS(true, false);
+    return ts.os_exact ? TP_GRADS(false, true) : TP_GRADS(false, false);
+#undef TP_GRADS
 }
 
 hipError_t launch_bpback3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gdata, const void* gw,
                                 const void* proj, const void* rot, const void* shifts, void* gproj, void* gweights,
-                                void* grot, void* gshift, hipStream_t s) {
+                                void* grot, void* gshift, CallPoses* cp, int gl, hipStream_t s) {
     if (cubic)
-        return ts.os_exact ? bpback_flags<true, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s)
-                           : bpback_flags<true, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
-    return ts.os_exact ? bpback_flags<false, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s)
-                       : bpback_flags<false, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift, s);
+        return ts.os_exact ? bpback_flags<true, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift,
+                                                      cp, gl, s)
+                           : bpback_flags<true, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
+                                                       gshift, cp, gl, s);
+    return ts.os_exact ? bpback_flags<false, true>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift,
+                                                   cp, gl, s)
+                       : bpback_flags<false, false>(g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot, gshift,
+                                                    cp, gl, s);
 }
 
 hipError_t launch_scatter3_tiled(bool cubic, int mode, const Geom& g, const TileSpec& ts, const void* src,
                                  const void* weights, const void* rot, const void* shifts, void* dst, void* wdst,
-                                 hipStream_t s) {
+                                 CallPoses* cp, int gl, hipStream_t s) {
     if (mode == 0) {
         if (weights)
-            return cubic ? scatter_kp<true, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s)
-                         : scatter_kp<false, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, s);
-        return cubic ? scatter_kp<true, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
-                     : scatter_kp<false, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
+            return cubic ? scatter_kp<true, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s)
+                         : scatter_kp<false, 0, true>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
+        return cubic ? scatter_kp<true, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, cp, gl, s)
+                     : scatter_kp<false, 0, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, cp, gl, s);
     }
-    return cubic ? scatter_kp<true, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s)
-                 : scatter_kp<false, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, s);
+    return cubic ? scatter_kp<true, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, cp, gl, s)
+                 : scatter_kp<false, 1, false>(g, ts, src, nullptr, rot, shifts, dst, nullptr, cp, gl, s);
 }
 
 }  // namespace tp

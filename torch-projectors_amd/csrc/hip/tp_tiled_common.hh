@@ -8,6 +8,7 @@
 #include <stdint.h>
 
 #include "tp_device.hh"
+#include "tp_launch.hh"
 
 namespace tp {
 namespace {
@@ -102,41 +103,78 @@ __device__ __forceinline__ int64_t xcd_item(int64_t slot) {
     const int64_t x = slot % kXcds, j = slot / kXcds;
     return ((j / RUN) * kXcds + x) * RUN + j % RUN;
 }
-// Opening scan of the GEN (non-rotation) tiled kernels: the radius their
-// samples reach, rho_unit * (largest singular value over the call's tiled
-// poses that are not rotations) + 1, or 0 when there is no such pose.  Every
-// lane of the NT-lane workgroup takes part; `part` holds NT / 64 ints.
-template <int DIM, int NT>
-__device__ float general_reach(const float* __restrict__ rot, int64_t poses, float rho_unit, int* part) {
-    constexpr int RS = DIM == 2 ? 4 : 9, U = 4;  // U poses per lane in flight
-    float m = 0.f;
-    for (int64_t p0 = threadIdx.x; p0 < poses; p0 += U * NT) {
-        float R[U][RS];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t p = min(p0 + u * NT, poses - 1);
-#pragma unroll
-            for (int e = 0; e < RS; ++e) R[u][e] = rot[p * RS + e];
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const PoseGram gr = DIM == 2 ? pose_gram2(R[u]) : pose_gram3(R[u]);
-            if (p0 + u * NT < poses && !gram_is_rotation(gr) && gram_tiled(gr)) m = fmaxf(m, gram_smax(gr));
+static_assert(kXcds == kXcdCount, "XCD count");
+
+// Slot sequence of a tiled kernel (slots map to work items through xcd_item).
+//   GEN = false: one slot per workgroup (the grid covers every slot).
+//   GEN = true:  a persistent grid; a workgroup takes batches of kGrab slots
+//                of its XCD (blockIdx.x mod kXcds) from that XCD's counter in
+//                the call scratch, the next batch in flight while it works on
+//                this one, until the XCD's `per` slots are taken.
+// Every member is called by all lanes of the workgroup (next() synchronises
+// them when a new batch is taken); `sh` is one int of LDS.
+constexpr int kGrab = 4;
+template <bool GEN>
+struct Slots {
+    int64_t s;       // current slot
+    int64_t j, jend;  // GEN: index within the XCD's slots, end of the batch
+    int64_t per;      // slots per XCD
+    unsigned* ctr;    // GEN: the XCD's counter (batches)
+    unsigned nxt;     // GEN, lane 0: the next batch, in flight
+    int x;            // GEN: XCD
+    __device__ __forceinline__ Slots(int64_t per_xcd, unsigned* counters, int* sh) : per(per_xcd) {
+        if constexpr (GEN) {
+            x = int(blockIdx.x % kXcds);
+            ctr = counters + x;
+            if (threadIdx.x == 0) *sh = int(atomicAdd(ctr, 1u));
+            __syncthreads();
+            j = int64_t(*sh) * kGrab;
+            __syncthreads();
+            jend = j + kGrab;
+            if (threadIdx.x == 0) nxt = atomicAdd(ctr, 1u);
+            s = j * kXcds + x;
+        } else {
+            s = blockIdx.x;
         }
     }
-    // non-negative floats order like their bit patterns as ints
-    const int wm = wave_max(__float_as_int(m));
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = wm;
-    __syncthreads();
-    int b = 0;
-    for (int w = 0; w < NT / 64; ++w) b = max(b, part[w]);
-    __syncthreads();
-    const float s = __int_as_float(b);
-    return s > 0.f ? rho_unit * s + 1.0f : 0.f;
-}
+    __device__ __forceinline__ bool ok() const { return GEN ? j < per : s < kXcds * per; }
+    __device__ __forceinline__ void next(int* sh) {
+        if constexpr (GEN) {
+            if (++j == jend) {
+                if (threadIdx.x == 0) *sh = int(nxt);
+                __syncthreads();
+                j = int64_t(*sh) * kGrab;
+                __syncthreads();
+                jend = j + kGrab;
+                if (threadIdx.x == 0 && j < per) nxt = atomicAdd(ctr, 1u);
+            }
+            s = j * kXcds + x;
+        } else {
+            s += gridDim.x;
+        }
+    }
+};
 
 // Workgroups of a GEN kernel's persistent grid (a multiple of kXcds).
-constexpr int64_t kGenGrid = 1024;
+constexpr int64_t kGenGrid = 2048;
+
+// Counter set of a kernel of tiled-kernel pair gl (tp_launch.hh: CallPoses).
+template <bool GEN>
+__device__ __forceinline__ unsigned* slot_counters(CallPoses* cp, int gl) { return cp->next[2 * gl + (GEN ? 1 : 0)]; }
+// Fields of the call summary read with a vector load where they are used (a
+// scalar load is hoisted to the kernel's start and waited for with the next).
+__device__ __forceinline__ int call_flag(const int* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float call_reach(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Tiles per half axis of a tile grid with edge `edge` centred on the origin
+// that holds floor(x) of every sample with |x| <= reach (+ slack below 2).
+__device__ __forceinline__ int half_tiles_for(float reach, int edge, int most) {
+    return min(most, int(ceilf((reach + 2.0f) / float(edge))));
+}
 
 }  // namespace
 }  // namespace tp
