@@ -133,6 +133,33 @@ int tp_project_3d_to_2d_forw(int dtype,
                              void* projections,
                              void* stream);
 
+/* Bytes of the static device scratch array of tp_project_3d_to_2d_forw_noalloc
+ * (one copy per GPU, held until the process ends). */
+#define TP_NOALLOC_SCRATCH_BYTES 256
+
+/* No counterpart in the reference.  tp_project_3d_to_2d_forw for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): same arguments, same results, but
+ * the tiled kernels' per-call pose summary and work counters live in a static
+ * device array of TP_NOALLOC_SCRATCH_BYTES per GPU instead of a scratch area
+ * that the first call on each stream allocates; the call itself allocates
+ * nothing.  The scratch it needs does not depend on the input sizes (a call
+ * needing more than the array would be rejected with TP_ERR_INVALID); the
+ * ordinary size limits of tp_project_3d_to_2d_forw apply.  Every call on one
+ * GPU shares that GPU's array, and each call's first kernel rewrites what the
+ * later ones read, so calls ordered on one stream are safe, while calls that
+ * overlap on one GPU (different streams with no order between them) race. */
+int tp_project_3d_to_2d_forw_noalloc(int dtype,
+                                     const void* reconstruction, int64_t B, int64_t rec_depth, int64_t rec_boxsize,
+                                     int64_t rec_boxsize_half,
+                                     const void* rotations, int64_t B_rot, int64_t P,
+                                     const void* shifts, int64_t B_shift,
+                                     int64_t proj_boxsize,
+                                     int interpolation, double oversampling, int has_cutoff,
+                                     double fourier_radius_cutoff,
+                                     void* projections,
+                                     void* stream);
+
 /* Replaces project_3d_to_2d_back_cuda (cuda/3d/projection_3d_to_2d_kernels.cu:1018-1179). */
 int tp_project_3d_to_2d_back(int dtype,
                              const void* grad_projections, int64_t B, int64_t P, int64_t proj_boxsize, int64_t proj_boxsize_half,

@@ -107,3 +107,15 @@ def test_half_volume_storage_is_forward_only():
     rc = lib.tp_backproject_2d_forw(capi.TP_F16S, _P(8), 1, 1, 8, 5, _P(None), _P(8), 1, _P(None), 1, 0, 2.0, 0,
                                     0.0, _P(8), _P(None), _P(None))
     assert rc == capi.TP_ERR_INVALID and "dtype" in lib.tp_last_error().decode()
+
+
+def test_noalloc_forward_checks_arguments_first():
+    """The no-allocation forward rejects invalid arguments with the same messages, before it
+    touches a device (nothing here has one)."""
+    lib = capi.lib()
+    a = dict(dtype=0, rec=_P(8), B=1, D=8, N=16, H=9, rot=_P(8), B_rot=1, P=2, shifts=_P(None), B_shift=1, n=8,
+             interp=0, os=1.0, has_cut=0, cut=0.0, out=_P(8), stream=_P(None))
+    assert lib.tp_project_3d_to_2d_forw_noalloc(*a.values()) == capi.TP_ERR_INVALID
+    assert "depth" in lib.tp_last_error().decode()
+    a.update(D=16, P=0)  # valid, nothing to do
+    assert lib.tp_project_3d_to_2d_forw_noalloc(*a.values()) == capi.TP_OK

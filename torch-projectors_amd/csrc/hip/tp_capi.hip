@@ -7,7 +7,8 @@
 // Nothing is synchronised.  The only memory besides the caller's is a small
 // scratch area per (device, stream) that the calls of the tiled kernels use
 // (tp::CallPoses: a summary of their poses and work counters), allocated by
-// the first such call on that stream and kept for the life of the process.
+// the first such call on that stream and kept for the life of the process;
+// tp_project_3d_to_2d_forw_noalloc uses a static device array instead.
 #include <algorithm>
 #include <cmath>
 #include <map>
@@ -286,12 +287,69 @@ struct StreamScratch {
 std::mutex g_scratch_mu;
 std::map<std::pair<int, hipStream_t>, std::unique_ptr<StreamScratch>> g_scratch;
 
-// The scratch of one call: taken (and its stream's `busy` held) until the call returns.
+// Scratch of tp_project_3d_to_2d_forw_noalloc: the static array `scratch`
+// below, one copy per GPU.  Its device address is looked up once per device
+// (hipGetSymbolAddress, with that device current) and kept in g_noalloc; the
+// array's name itself is a host-side stand-in and is never passed to a kernel.
+// The calls on one GPU share it: the pose pre-pass of each call rewrites
+// every field the kernels read (the flags and the work counters), and calls
+// that overlap on the GPU (different streams, no order between them) race.
+constexpr int kNoAllocMaxDevices = 64;
+constexpr size_t kCallScratchNeed = sizeof(tp::CallPoses);  // the same for every call and input size
+struct NoAllocDevice {
+    tp::CallPoses* p = nullptr;  // device address of this GPU's `scratch`
+    std::mutex busy;             // held while a call enqueues its kernels
+};
+NoAllocDevice g_noalloc[kNoAllocMaxDevices];
+std::mutex g_noalloc_init;
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[TP_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+// The current device's entry of g_noalloc, resolving its address on the first call on that device.
+int noalloc_device(NoAllocDevice*& out) {
+    if (kCallScratchNeed > TP_NOALLOC_SCRATCH_BYTES)
+        return fail("the call needs " + std::to_string(kCallScratchNeed) + " bytes of scratch, more than the " +
+                    std::to_string(TP_NOALLOC_SCRATCH_BYTES) + " of the static array");
+    int dev = 0;
+    TP_TRY(launched(hipGetDevice(&dev), "hipGetDevice"));
+    if (dev < 0 || dev >= kNoAllocMaxDevices)
+        return fail("the no-allocation entry point supports device indices below " +
+                    std::to_string(kNoAllocMaxDevices));
+    NoAllocDevice& d = g_noalloc[dev];
+    {
+        std::lock_guard<std::mutex> lk(g_noalloc_init);
+        if (!d.p) {
+            void* ptr = nullptr;
+            TP_TRY(launched(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"));
+            if (!ptr) return fail("hipGetSymbolAddress(scratch) returned NULL");
+            d.p = static_cast<tp::CallPoses*>(ptr);
+        }
+    }
+    out = &d;
+    return TP_OK;
+}
+
+// The scratch of one call, taken on first use (after the argument checks) and
+// held until the call returns, with the `busy` lock of its area.  `static_area`:
+// the current GPU's static array (no allocation); otherwise the area of the
+// (device, stream), allocated by the first call on that stream.
 struct CallScratch {
     tp::CallPoses* p = nullptr;
     std::unique_lock<std::mutex> hold;
+    bool static_area = false;
     int get(hipStream_t st) {
         if (p) return TP_OK;
+        if (static_area) {
+            NoAllocDevice* d = nullptr;
+            TP_TRY(noalloc_device(d));
+            hold = std::unique_lock<std::mutex>(d->busy);
+            p = d->p;
+            return TP_OK;
+        }
         int dev = 0;
         TP_TRY(launched(hipGetDevice(&dev), "hipGetDevice"));
         StreamScratch* e;
@@ -323,7 +381,7 @@ int call_poses(int dim, const tp::Geom& g, const void* rot, float rho_unit, Call
 // TP_F32 path.
 int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int64_t N, int64_t H, const void* rot,
                  int64_t B_rot, int64_t P, const void* shifts, int64_t B_shift, int64_t n, int interp, double os,
-                 int has_cut, double cut, void* out, void* stream) {
+                 int has_cut, double cut, void* out, void* stream, CallScratch& sc) {
     const bool rec_half = dtype == TP_F16S;
     const int dt = rec_half ? TP_F32 : dtype;  // arithmetic and output type
     const int kdt = rec_half ? 2 : dt;         // per-pixel kernels' volume type
@@ -342,7 +400,6 @@ int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int6
     TP_TRY(need(out, "projections"));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool cubic = interp == TP_CUBIC;
-    CallScratch sc;
     if (use_tiles(dim, dt, os, n)) {
         const tp::TileSpec ts = tile_spec(g, cubic);
         TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s));
@@ -526,9 +583,10 @@ int tp_project_2d_forw(int dtype, const void* reconstruction, int64_t B, int64_t
                        int64_t B_shift, int64_t proj_boxsize, int interpolation, double oversampling, int has_cutoff,
                        double fourier_radius_cutoff, void* projections, void* stream) {
     g_err.clear();
+    CallScratch sc;
     return project_forw(2, dtype, reconstruction, B, rec_boxsize, rec_boxsize, rec_boxsize_half, rotations, B_rot, P,
                         shifts, B_shift, proj_boxsize, interpolation, oversampling, has_cutoff,
-                        fourier_radius_cutoff, projections, stream);
+                        fourier_radius_cutoff, projections, stream, sc);
 }
 
 int tp_project_3d_to_2d_forw(int dtype, const void* reconstruction, int64_t B, int64_t rec_depth,
@@ -537,9 +595,23 @@ int tp_project_3d_to_2d_forw(int dtype, const void* reconstruction, int64_t B, i
                              double oversampling, int has_cutoff, double fourier_radius_cutoff, void* projections,
                              void* stream) {
     g_err.clear();
+    CallScratch sc;
     return project_forw(3, dtype, reconstruction, B, rec_depth, rec_boxsize, rec_boxsize_half, rotations, B_rot, P,
                         shifts, B_shift, proj_boxsize, interpolation, oversampling, has_cutoff,
-                        fourier_radius_cutoff, projections, stream);
+                        fourier_radius_cutoff, projections, stream, sc);
+}
+
+int tp_project_3d_to_2d_forw_noalloc(int dtype, const void* reconstruction, int64_t B, int64_t rec_depth,
+                                     int64_t rec_boxsize, int64_t rec_boxsize_half, const void* rotations,
+                                     int64_t B_rot, int64_t P, const void* shifts, int64_t B_shift,
+                                     int64_t proj_boxsize, int interpolation, double oversampling, int has_cutoff,
+                                     double fourier_radius_cutoff, void* projections, void* stream) {
+    g_err.clear();
+    CallScratch sc;
+    sc.static_area = true;
+    return project_forw(3, dtype, reconstruction, B, rec_depth, rec_boxsize, rec_boxsize_half, rotations, B_rot, P,
+                        shifts, B_shift, proj_boxsize, interpolation, oversampling, has_cutoff,
+                        fourier_radius_cutoff, projections, stream, sc);
 }
 
 int tp_project_2d_back(int dtype, const void* grad_projections, int64_t B, int64_t P, int64_t proj_boxsize,

@@ -26,6 +26,7 @@ SIGNATURES = {
     "tp_backproject_2d_back": [_I, _P, _P, _L, _L, _P, _L, _L, _L, _L, _P, _P, _L, _P, _L, _I, _D, _I, _D,
                                _P, _P, _P, _P, _P],
     "tp_project_3d_to_2d_forw": [_I, _P, _L, _L, _L, _L, _P, _L, _L, _P, _L, _L, _I, _D, _I, _D, _P, _P],
+    "tp_project_3d_to_2d_forw_noalloc": [_I, _P, _L, _L, _L, _L, _P, _L, _L, _P, _L, _L, _I, _D, _I, _D, _P, _P],
     "tp_project_3d_to_2d_back": [_I, _P, _L, _L, _L, _L, _P, _L, _L, _L, _P, _L, _P, _L, _I, _D, _I, _D,
                                  _P, _P, _P, _P],
     "tp_backproject_2d_to_3d_forw": [_I, _P, _L, _L, _L, _L, _P, _P, _L, _P, _L, _I, _D, _I, _D, _P, _P, _P],
