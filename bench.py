@@ -7,14 +7,26 @@ followed by the weighted backprojection `backproject_2d_to_3d_forw` of those
 2048 projections into a 512x512x257 data volume and its float32 weight volume.
 
 Prints ONE JSON line: whole-step Fourier samples/s (samples = B*P*n*(n/2+1)
-per op), per-op rates, the HBM roofline of the dominant op (algorithmic
-bytes per call / its mean duration, measured with HIP events on the stream
-the kernels run on), and the reference CPU path timed on a bounded sample of
-the same inputs on the host cores.
+per op) over the K timed steps, the median step beside the mean, per-op
+rates, the HBM roofline of the dominant op (algorithmic bytes per call / its
+mean duration, measured with HIP events on the stream the kernels run on),
+and the reference CPU path timed on a bounded sample of the same inputs on
+the host cores.
+
+Three fractions of the 8 TB/s peak are reported per op, and they mean
+different things:
+  alg_frac         algorithmic (per-tap, "effective") bytes / time: the
+                   reference's memory traffic if every tap went to memory;
+                   above 1 is possible for kernels that stage taps in LDS
+  compulsory_frac  each input read once and each output written once / time
+  traffic_frac     HBM bytes the rocprofv3 counters measured per call (the
+                   committed profiles/hbm_traffic_<config>.md, stamped with
+                   the commit it was measured at) / time
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--no-cpu]
-Configs: headline (default, the bench line), c2..c5 (the other BASELINE.json configurations:
-per-op rates and the CPU baseline on a bounded sample; no traffic figure for them).
+Configs: headline (default, the bench line), c2..c5 (the other BASELINE.json configurations),
+scaled (the headline with every pose matrix scaled by 1.02), published (the reference's
+published H100 rows: box 256, oversampling 1), prep, half.
 """
 import argparse
 import json
@@ -94,6 +106,23 @@ def ctf2_weights(B, P, n, gen):
     return torch.sin(k * rho2) ** 2
 
 
+# ----------------------------------------------------------------------------- Euler poses
+def euler_rotations(B, P, gen):
+    """Rz @ Ry @ Rx of three angles ~ U(0, 2 pi) per pose, float32 [B, P, 3, 3]: the poses of the
+    reference's benchmarks (paper/results/benchmarks/benchmark_base.py:190-227)."""
+    import torch
+    ax, ay, az = (torch.rand(B, P, generator=gen, dtype=torch.float64) * 2 * math.pi for _ in range(3))
+    z, o = torch.zeros_like(ax), torch.ones_like(ax)
+
+    def m(rows):
+        return torch.stack([torch.stack(r, -1) for r in rows], -2)
+
+    Rx = m([[o, z, z], [z, ax.cos(), -ax.sin()], [z, ax.sin(), ax.cos()]])
+    Ry = m([[ay.cos(), z, ay.sin()], [z, o, z], [-ay.sin(), z, ay.cos()]])
+    Rz = m([[az.cos(), -az.sin(), z], [az.sin(), az.cos(), z], [z, z, o]])
+    return (Rz @ Ry @ Rx).float()
+
+
 # ----------------------------------------------------------------------------- byte model
 def active_counts(n, cutoff=None):
     """(total, active forward, active scatter) pixels of one n x (n/2+1) projection
@@ -140,6 +169,28 @@ def bytes_backproject_back(npose, n, dim, interp, weights, cutoff=None):
     return npose * bwd * (taps(dim, interp) * 8 + 16 + ((4 * lin + 4) if weights else 0))
 
 
+# Compulsory traffic: every input read once, every output written once (complex 8 B, real 4 B
+# per element; poses are negligible).  `proj` = B*P*n*(n/2+1) projection elements, `vol` = the
+# reconstruction's elements.
+def compulsory_forward(proj, vol):
+    return vol * 8 + proj * 8
+
+
+def compulsory_backproject(proj, vol, weights):
+    per = 8 + (4 if weights else 0)
+    return proj * per + vol * per
+
+
+def compulsory_project_back(proj, vol):
+    # grad_projections and the volume read, the volume gradient written
+    return proj * 8 + vol * 8 + vol * 8
+
+
+def compulsory_backproject_back(proj, vol, weights):
+    # grad_data_rec (+ grad_weight_rec) and the projections read; grad_projections (+ grad_weights) written
+    return vol * (8 + (4 if weights else 0)) + proj * 8 + proj * (8 + (4 if weights else 0))
+
+
 # ----------------------------------------------------------------------------- workloads
 def timed_ops(calls, samples_per_op):
     """Run CPU calls in order, one run each; returns (seconds, samples, per-op seconds)."""
@@ -156,23 +207,32 @@ def timed_ops(calls, samples_per_op):
 
 
 class Workload:
-    """Inputs on the GPU, a step as a list of (op name, callable, bytes, samples)."""
+    """Inputs on the GPU, a step as a list of ops: (name, callable, algorithmic bytes, samples, poses,
+    compulsory bytes); `published` maps an op name to the reference's published rate for the same
+    configuration on other hardware (proj/s, hardware, source)."""
 
-    def __init__(self, name, desc, ops, cpu_sample=None, config=None, cpu_pmax=None, cpu_kind=None, cpu_cores=None):
+    def __init__(self, name, desc, ops, cpu_sample=None, config=None, cpu_pmax=None, cpu_kind=None, cpu_cores=None,
+                 published=None):
         self.name, self.desc, self.ops, self.cpu_sample, self.config = name, desc, ops, cpu_sample, config or {}
         self.cpu_pmax = cpu_pmax or ops[0][4]  # poses the CPU sample may take (one batch item's)
         # the CPU leg runs the reference build (or the oracle when absent) on `threads` cores,
         # unless the workload times its own port (numpy: one core)
         self.cpu_kind, self.cpu_cores = cpu_kind, cpu_cores
+        self.published = published or {}
 
 
-def make_headline(dev, k=0):
+def make_headline(dev, scale=None):
+    """The headline step; `scale` multiplies every pose matrix (the `scaled` workload: matrices that
+    are not rotations, such as magnification-corrected poses, through the same step)."""
     import torch
     import torch_projectors as tp
     gen = torch.Generator().manual_seed(20261201 + 6)
     P, n, os_ = 2048, 256, 2.0
     vol = blob_volume_rfft(256, 512, 32, 80.0, gen, dev)
-    rot = quat_rotations(P, gen)[None].to(dev)
+    rot = quat_rotations(P, gen)[None]
+    if scale is not None:
+        rot = (rot.double() * scale).float()
+    rot = rot.to(dev)
     sh = ((torch.rand(1, P, 2, generator=gen) * 16) - 8).to(dev)
     w = ctf2_weights(1, P, n, gen).float().to(dev)
     state = {}
@@ -187,8 +247,10 @@ def make_headline(dev, k=0):
 
     V = 512 * 512 * 257
     samples = P * n * (n // 2 + 1)
-    ops = [("project_3d_to_2d_forw", fwd, bytes_forward(P, n, 3, "linear"), samples, P),
-           ("backproject_2d_to_3d_forw", bp, bytes_backproject(P, n, 3, "linear", V, True), samples, P)]
+    ops = [("project_3d_to_2d_forw", fwd, bytes_forward(P, n, 3, "linear"), samples, P,
+            compulsory_forward(samples, V)),
+           ("backproject_2d_to_3d_forw", bp, bytes_backproject(P, n, 3, "linear", V, True), samples, P,
+            compulsory_backproject(samples, V, True))]
 
     def cpu_sample(p_cpu, threads, cpu_ops):
         """Run the same two ops on the first p_cpu poses on the CPU; returns seconds and samples."""
@@ -206,7 +268,16 @@ def make_headline(dev, k=0):
     cfg = {"workload": "headline: project_3d_to_2d_forw + backproject_2d_to_3d_forw (weights), linear",
            "volume": [1, 512, 512, 257], "poses": P, "proj": [n, n // 2 + 1], "oversampling": os_,
            "interpolation": "linear", "shifts": "U(-8,8)", "weights": "sin^2(k rho^2)"}
-    return Workload("headline", cfg["workload"], ops, cpu_sample, cfg)
+    name = "headline"
+    if scale is not None:
+        name = "scaled"
+        cfg["workload"] = f"scaled: the headline step with every pose matrix scaled by {scale}"
+        cfg["pose_scale"] = scale
+    return Workload(name, cfg["workload"], ops, cpu_sample, cfg)
+
+
+def make_scaled(dev):
+    return make_headline(dev, scale=1.02)
 
 
 def make_c2(dev):
@@ -231,7 +302,8 @@ def make_c2(dev):
     cfg = {"workload": "c2: project_3d_to_2d_forw, linear", "volume": [1, 256, 256, 129], "poses": P,
            "proj": [n, n // 2 + 1], "oversampling": os_}
     return Workload("c2", cfg["workload"], [("project_3d_to_2d_forw", fwd, bytes_forward(P, n, 3, "linear"),
-                                             samples, P)], cpu_sample, cfg)
+                                             samples, P, compulsory_forward(samples, 256 * 256 * 129))],
+                    cpu_sample, cfg)
 
 
 def make_c3(dev):
@@ -258,7 +330,7 @@ def make_c3(dev):
            "poses": P, "proj": [n, n // 2 + 1], "oversampling": os_}
     return Workload("c3", cfg["workload"],
                     [("backproject_2d_to_3d_forw", bp, bytes_backproject(P, n, 3, "linear", 256 * 256 * 129, True),
-                      samples, P)], cpu_sample, cfg)
+                      samples, P, compulsory_backproject(samples, 256 * 256 * 129, True))], cpu_sample, cfg)
 
 
 def make_c4(dev):
@@ -292,8 +364,10 @@ def make_c4(dev):
     cfg = {"workload": "c4: project_3d_to_2d_forw + project_3d_to_2d_back (rotation/shift grads), cubic",
            "volume": [1, 512, 512, 257], "poses": P, "proj": [n, n // 2 + 1], "oversampling": os_}
     return Workload("c4", cfg["workload"],
-                    [("project_3d_to_2d_forw", fwd, bytes_forward(P, n, 3, "cubic"), samples, P),
-                     ("project_3d_to_2d_back", back, bytes_project_back(P, n, 3, "cubic", V), samples, P)],
+                    [("project_3d_to_2d_forw", fwd, bytes_forward(P, n, 3, "cubic"), samples, P,
+                      compulsory_forward(samples, V)),
+                     ("project_3d_to_2d_back", back, bytes_project_back(P, n, 3, "cubic", V), samples, P,
+                      compulsory_project_back(samples, V))],
                     cpu_sample, cfg)
 
 
@@ -345,13 +419,14 @@ def make_c5(dev):
     cfg = {"workload": "c5: batched 2D cubic forward, backprojection (unit weights), both backward ops",
            "reconstruction": [B, 512, 257], "poses": P, "proj": [n, n // 2 + 1], "oversampling": os_, "cutoff": cut}
     return Workload("c5", cfg["workload"],
-                    [("project_2d_forw", fwd, bytes_forward(B * P, n, 2, "cubic", cut), samples, B * P),
+                    [("project_2d_forw", fwd, bytes_forward(B * P, n, 2, "cubic", cut), samples, B * P,
+                      compulsory_forward(samples, V)),
                      ("backproject_2d_forw", bp, bytes_backproject(B * P, n, 2, "cubic", V, True, cut), samples,
-                      B * P),
+                      B * P, compulsory_backproject(samples, V, True)),
                      ("backproject_2d_back", bp_back, bytes_backproject_back(B * P, n, 2, "cubic", True, cut),
-                      samples, B * P),
+                      samples, B * P, compulsory_backproject_back(samples, V, True)),
                      ("project_2d_back", p_back, bytes_project_back(B * P, n, 2, "cubic", V, cut), samples,
-                      B * P)], cpu_sample, cfg, cpu_pmax=P)
+                      B * P, compulsory_project_back(samples, V))], cpu_sample, cfg, cpu_pmax=P)
 
 
 def make_prep(dev):
@@ -400,8 +475,8 @@ def make_prep(dev):
            "spectrum": [N, N, N // 2 + 1], "oversampling": os_}
     # minimal bytes: read the input and write the output once
     return Workload("prep", cfg["workload"],
-                    [("to_fourier", fwd, n ** 3 * 4 + V * 8, V, 0),
-                     ("reconstruct", back, V * (8 + 4) + n ** 3 * 4, V, 0)],
+                    [("to_fourier", fwd, n ** 3 * 4 + V * 8, V, 0, n ** 3 * 4 + V * 8),
+                     ("reconstruct", back, V * (8 + 4) + n ** 3 * 4, V, 0, V * (8 + 4) + n ** 3 * 4)],
                     cpu_sample, cfg, cpu_pmax=1, cpu_kind="port", cpu_cores=1)
 
 
@@ -426,7 +501,8 @@ def make_half(dev):
     for interp in ("linear", "cubic"):
         for tag, v in (("complex32", vol16), ("complex64", vol)):
             ops.append((f"project_3d_to_2d_forw[{interp},{tag}]", fwd(v, interp),
-                        bytes_forward(P, n, 3, interp), samples, P))
+                        bytes_forward(P, n, 3, interp), samples, P,
+                        512 * 512 * 257 * (4 if tag == "complex32" else 8) + samples * 8))
 
     def cpu_sample(p_cpu, threads, cpu_ops):
         """The CPU reference on the widened volume (the storage's definition), linear."""
@@ -439,11 +515,83 @@ def make_half(dev):
     return Workload("half", cfg["workload"], ops, cpu_sample, cfg)
 
 
+def make_published(dev):
+    """published: the reference's published H100 rows at box 256 (volume 256^3, projections
+    256 x 129, oversampling 1, the default of its benchmark scripts), P = 2048 per batch item, batch
+    1 and 8, linear and cubic: forward projection, and backprojection with weights (forward op
+    only).  Inputs follow its benchmark scripts (paper/results/benchmarks/forward_3d_to_2d.py,
+    backward_2d_to_3d.py, benchmark_base.py:150-227): complex N(0,1) volumes and projections,
+    U(0,1) weights, Euler-angle rotations, shifts 5 N(0,1)."""
+    import torch
+    T = torch.ops.torch_projectors
+    gen = torch.Generator().manual_seed(20261201 + 8)
+    n, P = 256, 2048
+    V = n * n * (n // 2 + 1)
+    st = {}
+    for B in (1, 8):
+        st[B] = dict(vol=torch.randn(B, n, n, n // 2 + 1, generator=gen, dtype=torch.complex64).to(dev),
+                     rot=euler_rotations(B, P, gen).to(dev),
+                     sh=(5 * torch.randn(B, P, 2, generator=gen)).to(dev),
+                     proj=torch.randn(B, P, n, n // 2 + 1, generator=gen, dtype=torch.complex64).to(dev),
+                     w=torch.rand(B, P, n, n // 2 + 1, generator=gen).to(dev))
+
+    def fwd(B, interp):
+        d = st[B]
+        return lambda: T.project_3d_to_2d_forw(d["vol"], d["rot"], d["sh"], [n, n], interp, 1.0, None)
+
+    def bp(B, interp):
+        d = st[B]
+        return lambda: T.backproject_2d_to_3d_forw(d["proj"], d["w"], d["rot"], d["sh"], interp, 1.0, None)
+
+    # H100 proj/s (batch x poses per second), paper/results/tables/*.tex rows at box 256, 2048 poses
+    h100 = {("f", 1, "linear"): (929.5e3, "project-3d-to-2d-performance.tex:54"),
+            ("f", 1, "cubic"): (164.6e3, "project-3d-to-2d-performance.tex:55"),
+            ("f", 8, "linear"): (1838.2e3, "project-3d-to-2d-performance.tex:64"),
+            ("f", 8, "cubic"): (253.8e3, "project-3d-to-2d-performance.tex:65"),
+            ("b", 1, "linear"): (135.8e3, "backproject-2d-to-3d-performance.tex:54"),
+            ("b", 1, "cubic"): (18.5e3, "backproject-2d-to-3d-performance.tex:55"),
+            ("b", 8, "linear"): (134.0e3, "backproject-2d-to-3d-performance.tex:64"),
+            ("b", 8, "cubic"): (18.7e3, "backproject-2d-to-3d-performance.tex:65")}
+    ops, published = [], {}
+    for kind in ("f", "b"):
+        for B in (1, 8):
+            for interp in ("linear", "cubic"):
+                samples = B * P * n * (n // 2 + 1)
+                if kind == "f":
+                    name = f"project_3d_to_2d_forw[{interp},B{B}]"
+                    ops.append((name, fwd(B, interp), bytes_forward(B * P, n, 3, interp), samples, B * P,
+                                compulsory_forward(samples, B * V)))
+                else:
+                    name = f"backproject_2d_to_3d_forw[{interp},B{B}]"
+                    ops.append((name, bp(B, interp), bytes_backproject(B * P, n, 3, interp, B * V, True), samples,
+                                B * P, compulsory_backproject(samples, B * V, True)))
+                rate, src = h100[(kind, B, interp)]
+                published[name] = {"proj_per_s": rate, "hardware": "H100 (CUDA)", "source": src}
+
+    def cpu_sample(p, threads, cpu_ops):
+        """Batch item 0's first p poses through the linear forward and backprojection."""
+        d = st[1]
+        vc, rc, sc = d["vol"].cpu(), d["rot"][:, :p].cpu(), d["sh"][:, :p].cpu()
+        pc, wc = d["proj"][:, :p].cpu(), d["w"][:, :p].cpu()
+        return timed_ops([("project_3d_to_2d_forw[linear,B1]", lambda: cpu_ops.project_3d_to_2d_forw(
+                              vc, rc, sc, [n, n], "linear", 1.0, None)),
+                          ("backproject_2d_to_3d_forw[linear,B1]", lambda: cpu_ops.backproject_2d_to_3d_forw(
+                              pc, wc, rc, sc, "linear", 1.0, None))], p * n * (n // 2 + 1))
+
+    cfg = {"workload": "published: box 256 (volume 256^3, projections 256 x 129), oversampling 1, 2048 poses per "
+                       "item, batch 1 and 8, linear and cubic; forward and weighted backprojection",
+           "volume": ["B", 256, 256, 129], "poses": P, "proj": [n, n // 2 + 1], "oversampling": 1.0,
+           "shifts": "5 N(0,1)", "weights": "U(0,1)", "rotations": "Euler angles ~ U(0, 2 pi)"}
+    return Workload("published", cfg["workload"], ops, cpu_sample, cfg, cpu_pmax=P, published=published)
+
+
 # headline is the bench line; c2-c5 are the other BASELINE configurations,
-# prep the reference preparation around the headline volume and half the
-# headline forward from low-precision storage, run on request
+# prep the reference preparation around the headline volume, half the
+# headline forward from low-precision storage, scaled the headline with pose
+# matrices that are not rotations, published the reference's own published
+# rows (box 256, oversampling 1), run on request
 WORKLOADS = {"headline": make_headline, "c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5,
-             "prep": make_prep, "half": make_half}
+             "prep": make_prep, "half": make_half, "scaled": make_scaled, "published": make_published}
 
 
 # ----------------------------------------------------------------------------- CPU baseline
@@ -455,53 +603,91 @@ def cpu_ops_and_kind():
     return O, "port"
 
 
-def run_cpu_baseline(wl, target_s=12.0):
+def cpu_model():
+    """The host CPU's model name (lscpu's "Model name", else /proc/cpuinfo)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads():
+    """Threads for the CPU leg: every CPU of the process's affinity, capped by OMP_NUM_THREADS when
+    the environment sets it (the GPU boxes set it to the CPU share of one GPU, 16, while their
+    affinity lists every core of the host)."""
+    affinity = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    if share.isdigit() and int(share) > 0:
+        return min(affinity, int(share)), affinity, f"OMP_NUM_THREADS={share} (CPU share of one GPU)"
+    return affinity, affinity, "every CPU of the affinity mask"
+
+
+def run_cpu_baseline(wl, one_run_s=2.5, runs=5):
     """Time the workload's ops on the host cores on its first p poses.
 
-    p doubles (or scales by the measured rate) until one run takes about half
-    of target_s or covers every pose of the workload; short runs are repeated
-    up to about target_s and the fastest is reported.
+    p doubles (or scales by the measured rate) until one run takes about one_run_s or covers every
+    pose of the workload; then one warm-up run and `runs` timed runs, of which the median is
+    reported.
     """
+    import statistics
     import torch
-    threads = min(16, len(os.sched_getaffinity(0)))
+    threads, affinity, rule = cpu_threads()
     torch.set_num_threads(threads)
     ops, kind = cpu_ops_and_kind()
     p = min(8, wl.cpu_pmax)
-    t, s, parts = wl.cpu_sample(p, threads, ops)
-    while t < 0.5 * target_s and p < wl.cpu_pmax:
-        p = int(min(wl.cpu_pmax, max(2 * p, p * 0.6 * target_s / max(t, 1e-3))))
-        t, s, parts = wl.cpu_sample(p, threads, ops)
-    spent, runs = t, 1
-    while spent + t < target_s and runs < 5:
-        t2, s2, parts2 = wl.cpu_sample(p, threads, ops)
-        spent, runs = spent + t2, runs + 1
-        if t2 < t:
-            t, s, parts = t2, s2, parts2
+    t, _, _ = wl.cpu_sample(p, threads, ops)
+    while t < one_run_s and p < wl.cpu_pmax:
+        p = int(min(wl.cpu_pmax, max(2 * p, p * 1.2 * one_run_s / max(t, 1e-3))))
+        t, _, _ = wl.cpu_sample(p, threads, ops)
+    wl.cpu_sample(p, threads, ops)  # warm-up at the final size
+    res = [wl.cpu_sample(p, threads, ops) for _ in range(runs)]
+    times = [r[0] for r in res]
+    med = statistics.median(times)
+    t, s, parts = min(res, key=lambda r: abs(r[0] - med))
     split = ", ".join(f"{k} {v:.2f} s" for k, v in parts.items())
     kind, threads = wl.cpu_kind or kind, wl.cpu_cores or threads
-    return {"value": s / t, "unit": "Fourier samples/s", "cores": threads, "kind": kind,
-            "poses_per_s": p / t, "ops_s": {k: round(v, 4) for k, v in parts.items()},
-            "sample": f"first {p} poses of the workload (item 0), every op of the step, best of {runs} "
-                      f"run(s) ({t:.2f} s: {split}), {threads} threads"}
+    return {"value": s / med, "unit": "Fourier samples/s", "cores": threads, "kind": kind,
+            "poses_per_s": p / med, "ops_s": {k: round(v, 4) for k, v in parts.items()},
+            "runs_s": [round(x, 4) for x in times], "cpu_model": cpu_model(), "affinity_cpus": affinity,
+            "threads_rule": rule if not wl.cpu_cores else "the workload's own one-core port",
+            "sample": f"first {p} poses of the workload (item 0), every op of the step, median of {runs} runs "
+                      f"after 1 warm-up ({med:.2f} s; the median run: {split}), {threads} threads"}
 
 
 # ----------------------------------------------------------------------------- HBM traffic
-def measured_traffic(workload, op):
-    """HBM bytes per call of `op`, from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary.
+def measured_traffic(workload):
+    """HBM bytes per call of each op, and the commit they were measured at, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary.
 
-    The counters cannot be read from inside a run, so the figure comes from the
+    The counters cannot be read from inside a run, so the figures come from the
     summary profiles/hbm_traffic_<workload>.md (copy-kernel-scaled, read + write,
-    summed over the op's kernels); None when there is none for this workload.
+    summed over the op's kernels, its `traffic_bytes_per_call:` line) and the
+    commit from its `measured_at_commit:` line; ({}, None) when there is none.
     """
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"hbm_traffic_{workload}.md")
+    per_op, commit = {}, None
     try:
         with open(path) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_call:"):
-                    return json.loads(line.split(":", 1)[1]).get(op)
+                    per_op = json.loads(line.split(":", 1)[1])
+                elif line.startswith("measured_at_commit:"):
+                    commit = line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return None
+    return per_op, commit
 
 
 # ----------------------------------------------------------------------------- main
@@ -512,7 +698,7 @@ def log(msg):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="headline", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true")
@@ -566,20 +752,36 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     log(f"timed {a.steps} steps in {wall:.2f} s")
-    op_ms = [sum(ev[s][k].elapsed_time(ev[s][k + 1]) for s in range(a.steps)) / a.steps for k in range(nops)]
-    ms_step = sum(ev[s][0].elapsed_time(ev[s][nops]) for s in range(a.steps)) / a.steps
+    import statistics
+    op_runs = [[ev[s][k].elapsed_time(ev[s][k + 1]) for s in range(a.steps)] for k in range(nops)]
+    step_runs = [ev[s][0].elapsed_time(ev[s][nops]) for s in range(a.steps)]
+    op_ms = [sum(r) / a.steps for r in op_runs]
+    ms_step = sum(step_runs) / a.steps
 
+    traffic, traffic_commit = measured_traffic(a.config)
+    frac = lambda nbytes, sec: nbytes / sec / 1e9 / HBM_PEAK_GBS  # noqa: E731
     samples_step = sum(op[3] for op in wl.ops)
     per_op = {}
-    for k, (name, _, nbytes, samples, poses) in enumerate(wl.ops):
+    for k, (name, _, nbytes, samples, poses, comp) in enumerate(wl.ops):
         sec = op_ms[k] / 1e3
-        per_op[name] = {"ms": round(op_ms[k], 4), "samples_per_s": samples / sec, "poses_per_s": poses / sec,
-                        "alg_GB": nbytes / 1e9, "alg_GBps": nbytes / sec / 1e9,
-                        "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS}
+        o = {"ms": round(op_ms[k], 4), "ms_median": round(statistics.median(op_runs[k]), 4),
+             "samples_per_s": samples / sec, "poses_per_s": poses / sec,
+             "alg_GB": nbytes / 1e9, "alg_GBps": nbytes / sec / 1e9, "alg_frac": frac(nbytes, sec),
+             "compulsory_GB": comp / 1e9, "compulsory_frac": frac(comp, sec)}
+        if traffic.get(name) is not None:
+            o["traffic_GB"] = traffic[name] / 1e9
+            o["traffic_frac"] = frac(traffic[name], sec)
+        if name in wl.published:
+            pub = wl.published[name]
+            o["published"] = pub
+            o["vs_published"] = (poses / sec) / pub["proj_per_s"]
+        per_op[name] = o
     dom = max(range(nops), key=lambda k: op_ms[k])
-    dname, _, dbytes, _, _ = wl.ops[dom]
-    achieved = dbytes / (op_ms[dom] / 1e3) / 1e9
+    dname, _, dbytes, _, _, dcomp = wl.ops[dom]
+    dsec = op_ms[dom] / 1e3
+    achieved = dbytes / dsec / 1e9
     total_bytes = sum(op[2] for op in wl.ops)
+    total_comp = sum(op[5] for op in wl.ops)
 
     cpu = None
     if not a.no_cpu and wl.cpu_sample is not None:
@@ -587,22 +789,29 @@ def main():
         cpu = run_cpu_baseline(wl)
         log(f"cpu baseline: {cpu['sample']}")
 
+    dtraffic = traffic.get(dname)
     out = {
         "metric": METRIC,
         "value": samples_step / (ms_step / 1e3),
         "unit": "Fourier samples/s",
         "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(ms_step, 4),
+        "ms_per_step_median": round(statistics.median(step_runs), 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
         "config": wl.config,
         "poses_per_s": wl.ops[0][4] / (ms_step / 1e3),
         "step_alg_GBps": total_bytes / (ms_step / 1e3) / 1e9,
-        "step_hbm_frac": total_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS,
+        "step_alg_frac": frac(total_bytes, ms_step / 1e3),
+        "step_compulsory_frac": frac(total_comp, ms_step / 1e3),
         "wall_s": round(wall, 3),
         "ops": per_op,
         "roofline": {"bound": "hbm", "kernel": dname, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic(a.config, dname)},
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": dtraffic,
+                     "traffic_frac": frac(dtraffic, dsec) if dtraffic is not None else None,
+                     "traffic_commit": traffic_commit if dtraffic is not None else None,
+                     "compulsory": dcomp, "compulsory_frac": frac(dcomp, dsec),
+                     "achieved_is": "algorithmic (per-tap) bytes per call / mean call time"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

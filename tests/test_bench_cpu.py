@@ -53,3 +53,32 @@ def test_headline_bytes_per_launch():
         2048 * 25716 * 108 + 12 * 512 * 512 * 257
     assert abs(bench.bytes_forward(2048, 256, 3, "linear") / 1e9 - 3.928) < 5e-4
     assert abs(bench.bytes_backproject(2048, 256, 3, "linear", 512 * 512 * 257, True) / 1e9 - 6.496) < 5e-4
+
+
+def test_compulsory_bytes_of_the_headline():
+    """Each input read once and each output written once: the forward reads the 512 x 512 x 257
+    complex64 volume (0.539 GB) and writes 2048 projections of 256 x 129 (0.541 GB); the weighted
+    backprojection reads projections and weights and writes the data and weight volumes."""
+    V, S = 512 * 512 * 257, 2048 * 256 * 129
+    assert bench.compulsory_forward(S, V) == 8 * V + 8 * S
+    assert abs(bench.compulsory_forward(S, V) / 1e9 - (0.539 + 0.541)) < 2e-3
+    assert bench.compulsory_backproject(S, V, True) == 12 * S + 12 * V
+    assert bench.compulsory_backproject(S, V, False) == 8 * S + 8 * V
+
+
+def test_euler_rotations_are_rotations():
+    import torch
+    R = bench.euler_rotations(2, 7, torch.Generator().manual_seed(3)).double()
+    eye = torch.eye(3, dtype=torch.float64)
+    assert (R @ R.transpose(-1, -2) - eye).abs().max() < 1e-6
+    assert (torch.linalg.det(R) - 1).abs().max() < 1e-6
+
+
+def test_measured_traffic_reads_the_commit_stamp(tmp_path, monkeypatch):
+    prof = tmp_path / "profiles"
+    prof.mkdir()
+    (prof / "hbm_traffic_x.md").write_text('measured_at_commit: abc1234\n'
+                                           'traffic_bytes_per_call: {"op": 1000.0}\n')
+    monkeypatch.setattr(bench.os.path, "abspath", lambda p: str(tmp_path / "bench.py"))
+    per_op, commit = bench.measured_traffic("x")
+    assert per_op == {"op": 1000.0} and commit == "abc1234"
