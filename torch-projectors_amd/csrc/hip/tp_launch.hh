@@ -89,7 +89,8 @@ constexpr int kTiledPairs = 2;
 struct CallPoses {
     int any_rot;      // some pose of the call is a rotation
     float gen_reach;  // rho_unit * (largest singular value of the other tiled poses) + 1; 0: none
-    int pad[14];
+    int all_rot;      // every pose of the call is a rotation (the rotation kernels skip the class test)
+    int pad[13];
     unsigned next[2 * kTiledPairs][kXcdCount];  // batches of slots taken so far (zeroed by the pre-pass)
 };
 constexpr int kCallScratchBytes = 256;

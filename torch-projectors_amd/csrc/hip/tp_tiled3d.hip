@@ -83,10 +83,12 @@ __device__ __forceinline__ bool half_plane_hits(const float* as, const float* hi
 
 // Is the pose of this instantiation's class (rotation, or GEN: another tiled
 // matrix)?  `as` receives the half-plane vector (column 0, or its dual).
+// `all_rot`: every pose of the call is a rotation (CallPoses), so a rotation
+// kernel needs no test.
 template <bool GEN>
-__device__ __forceinline__ bool pose_of_class(const float* R, float* as) {
-    const PoseGram gr = pose_gram3(R);
+__device__ __forceinline__ bool pose_of_class(const float* R, float* as, bool all_rot) {
     if constexpr (GEN) {
+        const PoseGram gr = pose_gram3(R);
         if (gram_is_rotation(gr) || !gram_tiled(gr)) return false;
         float bs[3];
         pose_dual3(R, gr, as, bs);
@@ -95,15 +97,15 @@ __device__ __forceinline__ bool pose_of_class(const float* R, float* as) {
         as[0] = R[0];
         as[1] = R[3];
         as[2] = R[6];
-        return gram_is_rotation(gr);
+        return all_rot || gram_is_rotation(pose_gram3(R));
     }
 }
 
 // Pose of this class whose plane and half plane reach the box.
 template <bool GEN>
-__device__ __forceinline__ bool pose_hits(const float* R, const float* lo, const float* hi) {
+__device__ __forceinline__ bool pose_hits(const float* R, const float* lo, const float* hi, bool all_rot) {
     float as[3];
-    return pose_of_class<GEN>(R, as) && plane_hits(R, lo, hi) && half_plane_hits(as, hi, lo);
+    return pose_of_class<GEN>(R, as, all_rot) && plane_hits(R, lo, hi) && half_plane_hits(as, hi, lo);
 }
 
 // Rows r (sr = r*os = bs . x) whose samples can lie in the box: bs is a
@@ -270,7 +272,7 @@ static_assert(kChunk <= int(kPoseMask) + 1, "pose index must fit below the flag 
 template <int NT, bool TWO, int CH, bool GEN>
 __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pend, int pbase, const float* lo1,
                                           const float* hi1, const float* lo2, const float* hi2,
-                                          unsigned short* plist, int* pcount) {
+                                          unsigned short* plist, int* pcount, bool all_rot) {
     __syncthreads();  // every lane has read the previous count and list
     if (threadIdx.x == 0) *pcount = 0;
     __syncthreads();
@@ -286,7 +288,8 @@ __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pe
         for (int q = 0; q < kCullInFlightF; ++q) {
             const int p = pbase + int(threadIdx.x) + (q0 + q) * NT;
             if (p >= pend) continue;
-            const bool h1 = pose_hits<GEN>(R[q], lo1, hi1), h2 = TWO && pose_hits<GEN>(R[q], lo2, hi2);
+            const bool h1 = pose_hits<GEN>(R[q], lo1, hi1, all_rot),
+                       h2 = TWO && pose_hits<GEN>(R[q], lo2, hi2, all_rot);
             if (h1 || h2) plist[atomicAdd(pcount, 1)] = (unsigned short)((p - pbase) | (h1 ? kHit1 : 0) | (h2 ? kHit2 : 0));
         }
     }
@@ -304,7 +307,7 @@ template <int NT, bool GEN>
 __device__ __forceinline__ void cull_chunk_boxes(const float* __restrict__ rotb, int pend, int pbase,
                                                  const float* lo1, const float* hi1, const float* lo2,
                                                  const float* hi2, unsigned short* plist, int* pcnt, int& n1,
-                                                 int& n2) {
+                                                 int& n2, bool all_rot) {
     static_assert(kChunkSc % NT == 0 && (kChunkSc / NT) % kCullInFlight == 0, "cull shape");
     __syncthreads();  // every lane has read the previous counts and lists
     if (threadIdx.x == 0) pcnt[0] = pcnt[1] = 0;
@@ -323,7 +326,7 @@ __device__ __forceinline__ void cull_chunk_boxes(const float* __restrict__ rotb,
             // box 2 is box 1 negated (bit for bit), which a plane through the origin
             // crosses exactly when it crosses box 1: one plane test serves both
             float as[3];
-            if (p >= pend || !pose_of_class<GEN>(R[q], as) || !plane_hits(R[q], lo1, hi1)) continue;
+            if (p >= pend || !pose_of_class<GEN>(R[q], as, all_rot) || !plane_hits(R[q], lo1, hi1)) continue;
             if (half_plane_hits(as, hi1, lo1)) plist[atomicAdd(&pcnt[0], 1)] = (unsigned short)(p - pbase);
             if (half_plane_hits(as, hi2, lo2))
                 plist[kChunk - 1 - atomicAdd(&pcnt[1], 1)] = (unsigned short)(p - pbase);
@@ -434,6 +437,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
     // the call has none); GEN poses the call's own reach, up to kScaleMax times farther, over
     // the part of the wide grid that this reach needs
     const int any_rot = GEN ? 1 : call_flag(&cp->any_rot);
+    const bool all_rot = !GEN && call_flag(&cp->all_rot);
     float rho_k = ts.rho_unit + 1.0f;
     int nt = ts.nt, ntd = ts.ntfd, org = ts.org, orgd = ts.orgd;
     int fc0 = ts.fc0, fc1 = ts.fc1, fd0 = ts.fd0, fd1 = ts.fd1;
@@ -480,7 +484,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
         const Cx<VS>* recb = rec + b * g.vol;
         bool loaded = false;
         for (int pbase = p0; pbase < p1; pbase += CH) {
-            const int np = cull_chunk<NT, false, CH, GEN>(rotb, p1, pbase, lo, hi, lo, hi, plist, &pcount);
+            const int np = cull_chunk<NT, false, CH, GEN>(rotb, p1, pbase, lo, hi, lo, hi, plist, &pcount, all_rot);
             if (np == 0) continue;
             if (!loaded) {
                 // stage the tile and its halo.  When the staged box lies on one side of c = 0 and
@@ -739,14 +743,32 @@ struct TapMap {
     int lmin[3];
 };
 
+// Per-wave copy of a pose of the scatter's current batch: columns 0 and 1 of
+// the matrix (R6 = R[0], R[1], R[3], R[4], R[6], R[7]), the shifts, the pose's
+// first pixel in the projections and the first row of its samples in the box.
+struct ScSlot {
+    float R6[6];
+    float s0, s1;
+    int64_t base;
+    int r0;
+};
+// rotate_slice on the R6 layout (the same products in the same order).
+template <bool OSX>
+__device__ __forceinline__ void rotate_slice6(const float* __restrict__ R6, float r, float c, double os, float* x) {
+    const float sc = OSX ? c * float(os) : float(double(c) * os), sr = OSX ? r * float(os) : float(double(r) * os);
+    x[0] = R6[0] * sc + R6[1] * sr;
+    x[1] = R6[2] * sc + R6[3] * sr;
+    x[2] = R6[4] * sc + R6[5] * sr;
+}
+
 template <bool CUBIC, int MODE, bool WEIGHTS, bool OSX>
-__device__ __forceinline__ void scatter_sample(const Geom& g, const Slot& sd, int rr, int cc, Cx<float> v, float wpix,
-                                               bool shifted, bool flip, const TapMap& tm, double* acc_re,
-                                               double* acc_im, double* acc_w) {
+__device__ __forceinline__ void scatter_sample(const Geom& g, const ScSlot& sd, int rr, int cc, Cx<float> v,
+                                               float wpix, bool shifted, bool flip, const TapMap& tm,
+                                               double* acc_re, double* acc_im, double* acc_w) {
     constexpr int K = CUBIC ? 4 : 2, LOW = CUBIC ? 1 : 0;  // taps at floor(x) - LOW + j, j < K
     const float fr = float(rr), fc = float(cc);
     float x[3];
-    rotate_slice<OSX>(sd.R, fr, fc, g.os, x);
+    rotate_slice6<OSX>(sd.R6, fr, fc, g.os, x);
     if (shifted) {
         if (MODE == 0) v = cmul(v, cconj(phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k)));
         else v = cmul(v, phase_hw(-fr, -fc, sd.s0, sd.s1, g.phase_k));
@@ -814,7 +836,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
     __shared__ double acc_w[WEIGHTS ? S3 : 1];
     __shared__ unsigned short plist[kChunk];
     __shared__ int pcnt[2];
-    __shared__ Slot slots[NW][KP];
+    __shared__ ScSlot slots[NW][KP];
     __shared__ int marks[NW][64];
     __shared__ int gen_sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -827,6 +849,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
     // reach (up to kScaleMax times farther).  Without rotations in the call the rotation kernel
     // does nothing at all and GEN stores every tile it owns; with them GEN adds onto the tiles.
     const int any_rot = call_flag(&cp->any_rot);
+    const bool all_rot = !GEN && call_flag(&cp->all_rot);
     float rho_k = ts.rho_unit + 1.0f;
     if constexpr (GEN) {
         rho_k = fminf(ts.rho, cp->gen_reach);
@@ -875,7 +898,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
         bool touched = false;  // GEN: some pose reaches the tile
         for (int pbase = it.p0; pbase < pend; pbase += kChunkSc) {
             int n1, n2;
-            cull_chunk_boxes<NT, GEN>(rotb, pend, pbase, lo1, hi1, lo2, hi2, plist, pcnt, n1, n2);
+            cull_chunk_boxes<NT, GEN>(rotb, pend, pbase, lo1, hi1, lo2, hi2, plist, pcnt, n1, n2, all_rot);
             touched |= n1 + n2 > 0;
 #pragma unroll 1
             for (int pass = 0; pass < 2; ++pass) {
@@ -909,18 +932,23 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                     Sh[0] = Sn[0];
                     Sh[1] = Sn[1];
                     if (base + NW * KP < np) load_pose(rotb, shb, pose_at(min(base + NW * KP + slot, np - 1)), Rn, Sn);
+                    int r0, r1;
+                    box_rows<GEN>(R, lo, hi, ts, r0, r1);
                     if (jrow == 0 && sv) {
-                        Slot& sd = slots[wave][slot];
-#pragma unroll
-                        for (int e = 0; e < 9; ++e) sd.R[e] = R[e];
+                        ScSlot& sd = slots[wave][slot];
+                        sd.R6[0] = R[0];
+                        sd.R6[1] = R[1];
+                        sd.R6[2] = R[3];
+                        sd.R6[3] = R[4];
+                        sd.R6[4] = R[6];
+                        sd.R6[5] = R[7];
                         sd.s0 = Sh[0];
                         sd.s1 = Sh[1];
                         sd.base = (pose0 + pp) * int64_t(g.npix);
+                        sd.r0 = r0;
                     }
                     __builtin_amdgcn_wave_barrier();
                     {
-                    int r0, r1;
-                    box_rows<GEN>(R, lo, hi, ts, r0, r1);
                     const int nr = sv ? max(0, r1 - r0 + 1) : 0;
                     const int maxnr = wave_max(nr);
                     for (int rbase = 0; rbase < maxnr; rbase += RPS) {
@@ -935,19 +963,21 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                         const int incl = dpp_scan_add(cnt);
                         const int excl = incl - cnt;
                         const int total = __builtin_amdgcn_readlane(incl, 63);
+                        const int cx = c0 - excl;  // column of flattened sample e in this row: cx + e
                         int carry = 0;
                         // sample e0 + lane of this row block: owner lane, pixel, validity and the
                         // element to load (element 0 for lanes without a sample, so that every
                         // load is issued on every path: a load under a branch makes the compiler
-                        // wait for it before the previous window's taps)
+                        // wait for it before the previous window's taps).  The owner's row is
+                        // its slot's first row plus its row index within the block.
                         auto locate = [&](int e0, int& rr, int& cc, int& sl, bool& ok, int64_t& pidx) {
                             const int e = e0 + lane;
                             const int lw = window_owner(cnt, excl, e0, carry, marks[wave]);
-                            rr = __shfl(r, lw, 64);
-                            cc = __shfl(c0, lw, 64) + (e - __shfl(excl, lw, 64));
+                            cc = __shfl(cx, lw, 64) + e;
                             sl = lw / RPS;
                             ok = e < total;
-                            const Slot& sd = slots[wave][sl];
+                            const ScSlot& sd = slots[wave][sl];
+                            rr = sd.r0 + rbase + (lw - sl * RPS);
                             ok = ok && !filtered(float(rr), float(cc), cut2) &&
                                  !(cc == 0 && (rr == g.n / 2 || rr < 0));  // Friedel half of x = 0
                             const int pix = int(__umul24(unsigned(rr >= 0 ? rr : rr + g.n), unsigned(g.hp))) + cc;
