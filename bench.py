@@ -245,6 +245,7 @@ def make_headline(dev, scale=None):
         state["bp"] = tp.backproject_2d_to_3d_forw(state["proj"], rot, weights=w, shifts=sh,
                                                    interpolation="linear", oversampling=os_)
 
+    fwd()  # the backprojection's input, so that each op can also run alone (--ops)
     V = 512 * 512 * 257
     samples = P * n * (n // 2 + 1)
     ops = [("project_3d_to_2d_forw", fwd, bytes_forward(P, n, 3, "linear"), samples, P,
@@ -397,6 +398,8 @@ def make_c5(dev):
 
     def p_back():
         T.project_2d_back(st["gproj"], rec, rot_g, sh_g, "cubic", os_, cut)
+
+    bp_back()  # project_2d_back's input, so that each op can also run alone (--ops)
 
     def cpu_sample(p, threads, cpu_ops):
         """Item 0's first p poses through the four ops."""
@@ -702,6 +705,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="headline", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--ops", default=None,
+                    help="comma-separated op names: run only these ops of the workload's step (per-op counter "
+                         "runs); the JSON then describes that step")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run and time a plain 1 GiB copy kernel (calibrates HBM byte counters, measures the copy ceiling)")
     a = ap.parse_args()
@@ -732,6 +738,13 @@ def main():
                           "copy_frac_of_peak": moved / (ms / 1e3) / 1e9 / HBM_PEAK_GBS}))
         return
     wl = WORKLOADS[a.config](dev)
+    if a.ops:
+        keep = a.ops.split(",")
+        unknown = [k for k in keep if k not in [op[0] for op in wl.ops]]
+        if unknown:
+            print(f"bench.py: unknown op(s) {unknown} for --config {a.config}", file=sys.stderr)
+            sys.exit(2)
+        wl.ops = [op for op in wl.ops if op[0] in keep]
     torch.cuda.synchronize()
     log(f"inputs ready: {a.config}")
 
