@@ -564,11 +564,14 @@ __global__ __launch_bounds__(kBlock) void k_mirror2_x0(Geom g, Cx<float>* __rest
     }
 }
 
-// Workgroups of a launch over `items`: one per item (rotations), or the persistent GEN grid.
+// Workgroups of a launch of `kernel` over `items`: one per item (rotations), or the persistent
+// GEN grid.
 template <bool GEN>
-unsigned grid2_of(int64_t items) {
+unsigned grid2_of(int64_t items, const void* kernel) {
     const int64_t slots = kXcds * xcd_per<kRun>(items);
-    return grid_for(GEN && slots > kGenGrid ? kGenGrid : slots);
+    if (!GEN) return grid_for(slots);
+    const int64_t most = gen_grid(kernel, kThreads);
+    return grid_for(slots > most ? most : slots);
 }
 
 template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool PRIV, bool GEN>
@@ -576,8 +579,8 @@ hipError_t scatter2_one(const Geom& g, const TileSpec2& ts, const void* src, con
                         const void* shifts, void* dst, void* wdst, CallPoses* cp, int gl, hipStream_t s) {
     const int64_t work = g.B * ts.ksplit * (GEN ? int64_t(ts.nr_2) * ts.nc_2 : int64_t(ts.nr) * ts.nc);
     if (work == 0) return hipSuccess;
-    hipLaunchKernelGGL((k_scatter2_tiled<CUBIC, MODE, WEIGHTS, KP, PRIV, GEN>), dim3(grid2_of<GEN>(work)),
-                       dim3(kThreads), 0, s, g, ts, (const Cx<float>*)src, (const float*)weights, (const float*)rot,
+    const auto k = k_scatter2_tiled<CUBIC, MODE, WEIGHTS, KP, PRIV, GEN>;
+    hipLaunchKernelGGL(k, dim3(grid2_of<GEN>(work, (const void*)k)), dim3(kThreads), 0, s, g, ts, (const Cx<float>*)src, (const float*)weights, (const float*)rot,
                        (const float*)shifts, (Cx<float>*)dst, (float*)wdst, cp, gl);
     return hipGetLastError();
 }
@@ -900,8 +903,8 @@ hipError_t gather2_launch(const Geom& g, const TileSpec2& ts, const void* rec, c
     // rotations, then the other tiled poses (their samples and gradient terms are their own)
     const int64_t work = g.B * ts.gksplit * int64_t(ts.gnt) * ts.gnt;
     if (work > 0) {
-        hipLaunchKernelGGL((k_gather2_tiled<CUBIC, KP, GMODE, RS, WG, VS, false>), dim3(grid2_of<false>(work)),
-                           dim3(kThreads), 0, s, g, ts, (const Cx<VS>*)rec, (const float*)gw, (const float*)rot,
+        const auto kr = k_gather2_tiled<CUBIC, KP, GMODE, RS, WG, VS, false>;
+        hipLaunchKernelGGL(kr, dim3(grid2_of<false>(work, (const void*)kr)), dim3(kThreads), 0, s, g, ts, (const Cx<VS>*)rec, (const float*)gw, (const float*)rot,
                            (const float*)shifts, (Cx<float>*)out, (float*)wout, (const Cx<float>*)gsrc,
                            (float*)grot, (float*)gshift, cp, gl);
         const hipError_t e = hipGetLastError();
@@ -909,8 +912,8 @@ hipError_t gather2_launch(const Geom& g, const TileSpec2& ts, const void* rec, c
     }
     const int64_t work2 = g.B * ts.gksplit * int64_t(ts.gnt2) * ts.gnt2;
     if (work2 == 0) return hipSuccess;
-    hipLaunchKernelGGL((k_gather2_tiled<CUBIC, KP, GMODE, RS, WG, VS, true>), dim3(grid2_of<true>(work2)),
-                       dim3(kThreads), 0, s, g, ts, (const Cx<VS>*)rec, (const float*)gw, (const float*)rot,
+    const auto kg = k_gather2_tiled<CUBIC, KP, GMODE, RS, WG, VS, true>;
+    hipLaunchKernelGGL(kg, dim3(grid2_of<true>(work2, (const void*)kg)), dim3(kThreads), 0, s, g, ts, (const Cx<VS>*)rec, (const float*)gw, (const float*)rot,
                        (const float*)shifts, (Cx<float>*)out, (float*)wout, (const Cx<float>*)gsrc, (float*)grot,
                        (float*)gshift, cp, gl);
     return hipGetLastError();

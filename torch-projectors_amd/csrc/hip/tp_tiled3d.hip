@@ -1104,11 +1104,14 @@ int64_t forw_items(const Geom& g, const TileSpec& ts) {
     const int fc = GEN ? ts.fc1_2 - ts.fc0_2 : ts.fc1 - ts.fc0, fd = GEN ? ts.fd1_2 - ts.fd0_2 : ts.fd1 - ts.fd0;
     return g.B * (int64_t(fc) * fc * fd * ts.ksplit + int64_t(nt) * nt * ntd);
 }
-// Workgroups of a launch over `items`: one per item (rotations), or the persistent GEN grid.
+// Workgroups of a launch of `kernel` over `items`: one per item (rotations), or the persistent
+// GEN grid.
 template <bool GEN, int RUN>
-unsigned grid_of(int64_t items) {
+unsigned grid_of(int64_t items, const void* kernel, int threads) {
     const int64_t slots = kXcds * xcd_per<RUN>(items);
-    return grid_for(GEN && slots > kGenGrid ? kGenGrid : slots);
+    if (!GEN) return grid_for(slots);
+    const int64_t most = gen_grid(kernel, threads);
+    return grid_for(slots > most ? most : slots);
 }
 
 // One forward-family kernel (GMODE 0, 1, 2) for rotations, then for the other tiled poses.
@@ -1116,14 +1119,16 @@ template <bool CUBIC, int KP, bool OSX, int GMODE, bool RS, bool WG, typename VS
 hipError_t forw_both(const Geom& g, const TileSpec& ts, const void* rec, const void* rot, const void* shifts,
                      void* out, CallPoses* cp, int gl, const void* gsrc, void* grot, void* gshift, const void* gw,
                      void* wout, hipStream_t s) {
-    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP, OSX, GMODE, RS, WG, VS, false>),
-                       dim3(grid_of<false, kRunForw>(forw_items<false>(g, ts))), dim3(kForwThreads), 0, s, g, ts,
+    const auto kr = k_forw3_tiled<CUBIC, KP, OSX, GMODE, RS, WG, VS, false>;
+    const auto kg = k_forw3_tiled<CUBIC, KP, OSX, GMODE, RS, WG, VS, true>;
+    hipLaunchKernelGGL(kr, dim3(grid_of<false, kRunForw>(forw_items<false>(g, ts), (const void*)kr, kForwThreads)),
+                       dim3(kForwThreads), 0, s, g, ts,
                        (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out, cp, gl,
                        (const Cx<float>*)gsrc, (float*)grot, (float*)gshift, (const float*)gw, (float*)wout);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_forw3_tiled<CUBIC, KP, OSX, GMODE, RS, WG, VS, true>),
-                       dim3(grid_of<true, kRunForw>(forw_items<true>(g, ts))), dim3(kForwThreads), 0, s, g, ts,
+    hipLaunchKernelGGL(kg, dim3(grid_of<true, kRunForw>(forw_items<true>(g, ts), (const void*)kg, kForwThreads)),
+                       dim3(kForwThreads), 0, s, g, ts,
                        (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out, cp, gl,
                        (const Cx<float>*)gsrc, (float*)grot, (float*)gshift, (const float*)gw, (float*)wout);
     return hipGetLastError();
@@ -1145,14 +1150,16 @@ hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, co
     // rotations write every tile (none: the other tiled poses store them); the other tiled
     // poses add onto them
     const int64_t work = g.B * (score + int64_t(ts.ntd) * ts.ntr * ts.ntc);
-    hipLaunchKernelGGL((k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP, OSX, false>),
-                       dim3(grid_of<false, kRunScatter>(work)), dim3(kScatterThreads), 0, s, g, ts,
+    const auto kr = k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP, OSX, false>;
+    const auto kg = k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP, OSX, true>;
+    hipLaunchKernelGGL(kr, dim3(grid_of<false, kRunScatter>(work, (const void*)kr, kScatterThreads)),
+                       dim3(kScatterThreads), 0, s, g, ts,
                        (const Cx<float>*)src, (const float*)weights, (const float*)rot, (const float*)shifts,
                        (Cx<float>*)dst, (float*)wdst, cp, gl);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_scatter3_tiled<CUBIC, MODE, WEIGHTS, KP, OSX, true>),
-                       dim3(grid_of<true, kRunScatter>(work)), dim3(kScatterThreads), 0, s, g, ts,
+    hipLaunchKernelGGL(kg, dim3(grid_of<true, kRunScatter>(work, (const void*)kg, kScatterThreads)),
+                       dim3(kScatterThreads), 0, s, g, ts,
                        (const Cx<float>*)src, (const float*)weights, (const float*)rot, (const float*)shifts,
                        (Cx<float>*)dst, (float*)wdst, cp, gl);
     e = hipGetLastError();

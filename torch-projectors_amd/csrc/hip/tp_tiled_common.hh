@@ -107,13 +107,17 @@ static_assert(kXcds == kXcdCount, "XCD count");
 
 // Slot sequence of a tiled kernel (slots map to work items through xcd_item).
 //   GEN = false: one slot per workgroup (the grid covers every slot).
-//   GEN = true:  a persistent grid; a workgroup takes batches of kGrab slots
+//   GEN = true:  a persistent grid of the workgroups that fit on the device
+//                at once (gen_grid); a workgroup takes batches of kGrab slots
 //                of its XCD (blockIdx.x mod kXcds) from that XCD's counter in
 //                the call scratch, the next batch in flight while it works on
-//                this one, until the XCD's `per` slots are taken.
+//                this one, until the XCD's `per` slots are taken.  With one
+//                slot per batch an XCD's resident workgroups work on about as
+//                many consecutive slots as the rotation kernel's do, so its L2
+//                shares their halos and projection rows the same way.
 // Every member is called by all lanes of the workgroup (next() synchronises
 // them when a new batch is taken); `sh` is one int of LDS.
-constexpr int kGrab = 4;
+constexpr int kGrab = 1;
 template <bool GEN>
 struct Slots {
     int64_t s;       // current slot
@@ -155,8 +159,20 @@ struct Slots {
     }
 };
 
-// Workgroups of a GEN kernel's persistent grid (a multiple of kXcds).
-constexpr int64_t kGenGrid = 2048;
+// Workgroups of a GEN kernel's persistent grid: as many as are resident on the
+// current device at once (occupancy of `kernel` with `threads` lanes times the
+// CU count), a multiple of kXcds; kGenGrid when the runtime cannot say.
+constexpr int64_t kGenGrid = 1024;
+inline int64_t gen_grid(const void* kernel, int threads) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess || per_cu < 1 ||
+        cus < 1)
+        return kGenGrid;
+    const int64_t g = int64_t(per_cu) * cus / kXcds * kXcds;
+    return g >= kXcds ? g : kGenGrid;
+}
 
 // Counter set of a kernel of tiled-kernel pair gl (tp_launch.hh: CallPoses).
 template <bool GEN>
