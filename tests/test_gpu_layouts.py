@@ -79,3 +79,28 @@ def test_strided_inputs_backprojection(gpu, dim, interp):
     d4, w4 = f(p64, w.double(), rot.double(), sh.double(), interp, 2.0, None)
     assert w3.dtype == torch.float32 and w4.dtype == torch.float64
     assert rel_l2(d3, d4) <= 1e-12 and rel_l2(w3.double(), w4) <= 1e-6
+
+
+@pytest.mark.parametrize("interp", ["linear", "cubic"])
+@pytest.mark.parametrize("odd_box", [False, True])
+def test_volume_at_an_8_byte_boundary(gpu, oracle, interp, odd_box):
+    """A contiguous volume whose first element sits 8 bytes past a 16-byte boundary (a view one
+    element into a buffer), and one of odd box size (odd elements per batch item, so batch item 1
+    starts off a 16-byte boundary): the tiled forward reads complex64 values at 8-byte alignment
+    only, so such volumes give the projections of an aligned copy, bit for bit, and the oracle's."""
+    g = torch.Generator().manual_seed(41 + odd_box)
+    B, P, n = 2, 20, 32
+    N = 2 * n + (1 if odd_box else 0)
+    shape = (B, N, N, N // 2 + 1)
+    numel = B * N * N * (N // 2 + 1)
+    flat = torch.randn(numel + 1, generator=g, dtype=torch.complex64).to(gpu)
+    rec = flat[1:].view(shape)
+    assert rec.data_ptr() % 16 == 8 and rec.is_contiguous()
+    q = torch.linalg.qr(torch.randn(P, 3, 3, generator=g, dtype=torch.float64))[0]
+    rot = q.float()[None].expand(B, P, 3, 3).contiguous()
+    print(f"[layouts] 8-byte boundary volume {interp} odd_box={odd_box}", flush=True)
+    got = T.project_3d_to_2d_forw(rec, rot.to(gpu), None, [n, n], interp, 2.0, None)
+    aligned = T.project_3d_to_2d_forw(rec.clone(), rot.to(gpu), None, [n, n], interp, 2.0, None)
+    assert torch.equal(got, aligned)
+    ref = oracle.project_3d_to_2d_forw(rec.cpu(), rot, None, (n, n), interp, 2.0, None)
+    assert torch.equal(got.cpu(), ref)

@@ -569,8 +569,8 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                 int r0, r1;
                 box_rows<GEN>(R, lo, hi, ts, r0, r1);
                 const int nr = sv ? max(0, r1 - r0 + 1) : 0;
-                const int maxnr = wave_max(nr);
-                for (int rbase = 0; rbase < maxnr; rbase += RPS) {
+                // row blocks of RPS rows per pose while some pose has rows left
+                for (int rbase = 0; __ballot(nr > rbase) != 0; rbase += RPS) {
                     const int jr = rbase + jrow;
                     const int r = r0 + jr;
                     int c0 = 0, cnt = 0;
@@ -950,8 +950,8 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                     __builtin_amdgcn_wave_barrier();
                     {
                     const int nr = sv ? max(0, r1 - r0 + 1) : 0;
-                    const int maxnr = wave_max(nr);
-                    for (int rbase = 0; rbase < maxnr; rbase += RPS) {
+                    // row blocks of RPS rows per pose while some pose has rows left
+                    for (int rbase = 0; __ballot(nr > rbase) != 0; rbase += RPS) {
                         const int jr = rbase + jrow;
                         const int r = r0 + jr;
                         int c0 = 0, cnt = 0;
@@ -1021,24 +1021,31 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
         // workgroup each) by a plain read and write; without rotations in the call it stores them
         if (GEN && !touched && (it.core || any_rot)) continue;
         __syncthreads();
-        for (int e = tid; e < S3; e += NT) {
-            const int lc = e % SC, lr = (e / SC) % SR, ld = e / (SC * SR);
-            const int c = tc + lc, r = tr + lr, d = td + ld;
-            if (c >= H || r > half || d > half) continue;
-            const int re = r < 0 ? r + N : r, de = d < 0 ? d + N : d;
-            const int64_t idx = b * g.vol + (int64_t(de) * N + re) * H + c;
-            const int a = (e - lc) + ((lc + acc_swizzle(lr, ld)) & (SC - 1));
-            if (it.core) {
-                atomic_add(&dst[idx].re, float(acc_re[a]));
-                atomic_add(&dst[idx].im, float(acc_im[a]));
-                if (WEIGHTS) atomic_add(&wdst[idx], float(acc_w[a]));
-            } else if (GEN && any_rot) {
-                const Cx<float> o = dst[idx];
-                dst[idx] = Cx<float>{o.re + float(acc_re[a]), o.im + float(acc_im[a])};
-                if (WEIGHTS) wdst[idx] += float(acc_w[a]);
-            } else {
-                dst[idx] = Cx<float>{float(acc_re[a]), float(acc_im[a])};
-                if (WEIGHTS) wdst[idx] = float(acc_w[a]);
+        {
+            // each lane keeps one (c, r) of the tile and steps along d
+            static_assert(NT % (SC * SR) == 0, "write-out lanes keep their column and row");
+            const int lc = tid % SC, lr = (tid / SC) % SR;
+            const int c = tc + lc, r = tr + lr;
+            if (c < H && r <= half) {
+                const int64_t row = b * g.vol + int64_t(r < 0 ? r + N : r) * H + c, plane = int64_t(N) * H;
+                for (int ld = tid / (SC * SR); ld < SD; ld += NT / (SC * SR)) {
+                    const int d = td + ld;
+                    if (d > half) break;
+                    const int64_t idx = row + (d < 0 ? d + N : d) * plane;
+                    const int a = (ld * SR + lr) * SC + ((lc + acc_swizzle(lr, ld)) & (SC - 1));
+                    if (it.core) {
+                        atomic_add(&dst[idx].re, float(acc_re[a]));
+                        atomic_add(&dst[idx].im, float(acc_im[a]));
+                        if (WEIGHTS) atomic_add(&wdst[idx], float(acc_w[a]));
+                    } else if (GEN && any_rot) {
+                        const Cx<float> o = dst[idx];
+                        dst[idx] = Cx<float>{o.re + float(acc_re[a]), o.im + float(acc_im[a])};
+                        if (WEIGHTS) wdst[idx] += float(acc_w[a]);
+                    } else {
+                        dst[idx] = Cx<float>{float(acc_re[a]), float(acc_im[a])};
+                        if (WEIGHTS) wdst[idx] = float(acc_w[a]);
+                    }
+                }
             }
         }
         __syncthreads();
