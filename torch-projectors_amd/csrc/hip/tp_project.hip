@@ -74,11 +74,24 @@ __global__ __launch_bounds__(kBlock) void k_project_forw_rest(Geom g, const Cx<V
         const bool tiled = pose_tiled_d<DIM>(R);
         if (ZEROED && tiled) continue;  // block-uniform
         Cx<float>* outp = out + bp * g.npix;
-        // one row per wave, lanes along the row (no per-pixel division)
+        // one row per wave, lanes along the row (no per-pixel division).  For a tiled pose only
+        // the masked pixels are written.  The mask test r^2 + c^2 > cut2 (rounded as the
+        // reference rounds it) is monotone in c, so they are the row's tail: the scan starts at
+        // an estimate of its first column, sqrt(cut2 - r^2) - 2, once the exact test has passed
+        // the column before it (otherwise at 0).
         for (int i = threadIdx.x / 64; i < g.n; i += kBlock / 64) {
             const float r = freq_of<float>(i, g.n);
             Cx<float>* row = outp + int64_t(i) * g.hp;
-            for (int j = threadIdx.x % 64; j < g.hp; j += 64) {
+            int c_scan = 0;
+            if (tiled) {
+                const float rem = cut2 - r * r;
+                if (rem >= 4.f) {  // false for NaN: then every column is tested (none is masked)
+                    int cs = rem < 1.0e9f ? int(__builtin_amdgcn_sqrtf(rem)) - 2 : g.hp;
+                    cs = min(g.hp, max(0, cs));
+                    c_scan = (cs > 0 && filtered(r, float(cs - 1), cut2)) ? 0 : cs;
+                }
+            }
+            for (int j = c_scan + threadIdx.x % 64; j < g.hp; j += 64) {
                 const float c = float(j);
                 if (filtered(r, c, cut2)) row[j] = Cx<float>{0.f, 0.f};
                 else if (!tiled) row[j] = project_pixel<DIM, float, CUBIC>(g, rec + b * g.vol, R, S, r, c);
