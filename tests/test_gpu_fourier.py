@@ -171,3 +171,34 @@ def test_from_fourier_leaves_its_input(F, gpu):
     F.from_fourier(spec, 2.0)
     torch.cuda.synchronize()
     assert torch.equal(spec, keep)
+
+
+def test_plan_cache_eviction_keeps_results(F, gpu):
+    """More distinct transform shapes than the library caches plans for (32): the least recently
+    used plans are destroyed and made again when needed, and every transform stays correct."""
+    from torch_projectors import fourier as FM
+    xs = {b: _rand((b, 16, 16), torch.float32).to(gpu) for b in range(1, 41)}
+    for b in list(range(1, 41)) + [1, 2, 3]:
+        got = FM._rfftn(xs[b], 2).cpu()
+        exp = np.fft.rfftn(xs[b].cpu().double().numpy(), axes=(-2, -1), norm="forward")
+        assert rel_l2(got, torch.from_numpy(exp)) < 2e-6, b
+
+
+def test_same_shape_on_two_streams(F, gpu):
+    """Transforms of one shape queued on two streams at once have their own plans (and work
+    areas), so neither corrupts the other."""
+    from torch_projectors import fourier as FM
+    a = _rand((4, 64, 64, 64), torch.float32).to(gpu)
+    b = _rand((4, 64, 64, 64), torch.float32).to(gpu)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    outs = {}
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            outs["a"] = FM._rfftn(a, 3)
+        with torch.cuda.stream(s2):
+            outs["b"] = FM._rfftn(b, 3)
+    torch.cuda.synchronize()
+    for k, x in (("a", a), ("b", b)):
+        exp = np.fft.rfftn(x.cpu().double().numpy(), axes=(-3, -2, -1), norm="forward")
+        assert rel_l2(outs[k].cpu(), torch.from_numpy(exp)) < 2e-6, k

@@ -200,24 +200,55 @@ hipError_t launch_ifftshift_crop(int elem_bytes, int dim, const void* src, int64
 }
 
 // ---------------------------------------------------------------- FFTs (rocFFT through hipFFT)
-// Plans are cached for the life of the process, one per (direction, dtype,
-// dim, edge, batch, device); hipFFT allocates each plan's work area once.
-// Execution on a shared plan sets its stream first, so calls are serialised
-// by the cache lock.
+// Plans are cached per (direction, dtype, dim, edge, batch, device, stream);
+// hipFFT allocates each plan's work area once.  Keying on the stream gives
+// calls on different streams their own work areas, so transforms that run at
+// once on the GPU never share one; calls on one stream run in order.  The
+// cache holds at most kMaxPlans plans: the least recently used one is
+// destroyed after its device has finished all queued work (its transforms may
+// still be running).  The cache lock serialises the enqueues.
 namespace {
 
-using PlanKey = std::tuple<int, int, int, int64_t, int64_t, int>;
+using PlanKey = std::tuple<int, int, int, int64_t, int64_t, int, hipStream_t>;
+struct PlanEntry {
+    hipfftHandle h;
+    uint64_t used;  // tick of the last call
+};
+constexpr size_t kMaxPlans = 32;
 std::mutex g_fft_mu;
-std::map<PlanKey, hipfftHandle> g_plans;
+std::map<PlanKey, PlanEntry> g_plans;
+uint64_t g_fft_tick = 0;
 
-hipfftResult plan_for(bool forward, int dt, int dim, int64_t N, int64_t batch, hipfftHandle& out) {
+hipfftResult evict_oldest_plan() {
+    auto old = g_plans.begin();
+    for (auto it = g_plans.begin(); it != g_plans.end(); ++it)
+        if (it->second.used < old->second.used) old = it;
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return HIPFFT_INTERNAL_ERROR;
+    const int dev = std::get<5>(old->first);
+    if (hipSetDevice(dev) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        hipSetDevice(cur);
+        return HIPFFT_INTERNAL_ERROR;
+    }
+    const hipfftResult r = hipfftDestroy(old->second.h);
+    g_plans.erase(old);
+    if (hipSetDevice(cur) != hipSuccess) return HIPFFT_INTERNAL_ERROR;
+    return r;
+}
+
+hipfftResult plan_for(bool forward, int dt, int dim, int64_t N, int64_t batch, hipStream_t s, hipfftHandle& out) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return HIPFFT_INTERNAL_ERROR;
-    const PlanKey key{forward ? 1 : 0, dt, dim, N, batch, dev};
+    const PlanKey key{forward ? 1 : 0, dt, dim, N, batch, dev, s};
     auto it = g_plans.find(key);
     if (it != g_plans.end()) {
-        out = it->second;
+        it->second.used = ++g_fft_tick;
+        out = it->second.h;
         return HIPFFT_SUCCESS;
+    }
+    if (g_plans.size() >= kMaxPlans) {
+        const hipfftResult e = evict_oldest_plan();
+        if (e != HIPFFT_SUCCESS) return e;
     }
     hipfftHandle h;
     hipfftResult r = hipfftCreate(&h);
@@ -232,11 +263,12 @@ hipfftResult plan_for(bool forward, int dt, int dim, int64_t N, int64_t batch, h
     size_t work = 0;
     if (r == HIPFFT_SUCCESS)
         r = hipfftMakePlanMany(h, dim, n, nullptr, 1, 0, nullptr, 1, 0, type, int(batch), &work);
+    if (r == HIPFFT_SUCCESS) r = hipfftSetStream(h, s);
     if (r != HIPFFT_SUCCESS) {
         hipfftDestroy(h);
         return r;
     }
-    g_plans.emplace(key, h);
+    g_plans.emplace(key, PlanEntry{h, ++g_fft_tick});
     out = h;
     return HIPFFT_SUCCESS;
 }
@@ -246,8 +278,7 @@ hipfftResult plan_for(bool forward, int dt, int dim, int64_t N, int64_t batch, h
 int fft_forward(int dt, int dim, int64_t batch, int64_t N, const void* real, void* spec, hipStream_t s) {
     std::lock_guard<std::mutex> lock(g_fft_mu);
     hipfftHandle h;
-    hipfftResult r = plan_for(true, dt, dim, N, batch, h);
-    if (r == HIPFFT_SUCCESS) r = hipfftSetStream(h, s);
+    const hipfftResult r = plan_for(true, dt, dim, N, batch, s, h);
     if (r != HIPFFT_SUCCESS) return int(r);
     // out-of-place real-to-complex transforms leave their input intact
     if (dt == 0) return int(hipfftExecR2C(h, (hipfftReal*)real, (hipfftComplex*)spec));
@@ -257,8 +288,7 @@ int fft_forward(int dt, int dim, int64_t batch, int64_t N, const void* real, voi
 int fft_inverse(int dt, int dim, int64_t batch, int64_t N, void* spec, void* real, hipStream_t s) {
     std::lock_guard<std::mutex> lock(g_fft_mu);
     hipfftHandle h;
-    hipfftResult r = plan_for(false, dt, dim, N, batch, h);
-    if (r == HIPFFT_SUCCESS) r = hipfftSetStream(h, s);
+    const hipfftResult r = plan_for(false, dt, dim, N, batch, s, h);
     if (r != HIPFFT_SUCCESS) return int(r);
     if (dt == 0) return int(hipfftExecC2R(h, (hipfftComplex*)spec, (hipfftReal*)real));
     return int(hipfftExecZ2D(h, (hipfftDoubleComplex*)spec, (hipfftDoubleReal*)real));
