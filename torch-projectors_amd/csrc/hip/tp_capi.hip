@@ -283,6 +283,8 @@ int launched(hipError_t e, const char* what) { return e == hipSuccess ? TP_OK : 
 struct StreamScratch {
     tp::CallPoses* p = nullptr;
     std::mutex busy;
+    void* bins = nullptr;  // pose-bin workspace of the tiled 3D kernels, grown on demand
+    size_t bins_cap = 0;
 };
 std::mutex g_scratch_mu;
 std::map<std::pair<int, hipStream_t>, std::unique_ptr<StreamScratch>> g_scratch;
@@ -341,6 +343,27 @@ struct CallScratch {
     tp::CallPoses* p = nullptr;
     std::unique_lock<std::mutex> hold;
     bool static_area = false;
+    StreamScratch* area = nullptr;  // the (device, stream) area, when not static_area
+    // A pose-bin workspace of `need` bytes on the call's stream, or nullptr: the static area has
+    // none, and a failed allocation leaves the call without bins (the kernels then cull every pose).
+    // Growing waits for the stream's queued work, which may still read the old workspace.
+    void* bins(size_t need, hipStream_t st) {
+        if (static_area || !area) return nullptr;
+        if (need > area->bins_cap) {
+            if (hipStreamSynchronize(st) != hipSuccess) return nullptr;
+            if (area->bins) hipFree(area->bins);
+            area->bins = nullptr;
+            area->bins_cap = 0;
+            const size_t cap = need + need / 4;
+            if (hipMalloc(&area->bins, cap) != hipSuccess) {
+                area->bins = nullptr;
+                hipGetLastError();  // clear the allocation error
+                return nullptr;
+            }
+            area->bins_cap = cap;
+        }
+        return area->bins;
+    }
     int get(hipStream_t st) {
         if (p) return TP_OK;
         if (static_area) {
@@ -366,6 +389,7 @@ struct CallScratch {
         }
         hold = std::unique_lock<std::mutex>(e->busy);
         p = e->p;
+        area = e;
         return TP_OK;
     }
 };
@@ -374,6 +398,40 @@ struct CallScratch {
 int call_poses(int dim, const tp::Geom& g, const void* rot, float rho_unit, CallScratch& sc, hipStream_t s) {
     TP_TRY(sc.get(s));
     return launched(tp::launch_call_poses(dim, g.B_rot * g.P, rot, rho_unit, sc.p, s), "pose summary launch");
+}
+
+// Pose bins of the tiled 3D scatter's tile grid for this call (tp::BinGrid), in 2 x 2 x 2 tiles,
+// filled by launch_pose_bins after the call's pose summary.  None below kBinsMinPoses poses,
+// from 65536 poses (list entries are 16-bit) or beyond kBinsMaxBytes, and none without a
+// workspace: the scatter then culls every pose of each tile.
+constexpr int64_t kBinsMinPoses = 16;
+constexpr size_t kBinsMaxBytes = size_t(1) << 30;
+int make_bins(bool cubic, const tp::Geom& g, tp::TileSpec& ts, const void* rot, CallScratch& sc, hipStream_t s) {
+    ts.sbins = tp::BinGrid{};
+    if (g.P < kBinsMinPoses || g.P >= 65536) return TP_OK;
+    tp::BinGrid sb{};
+    sb.nb[0] = (ts.ntc + 1) / 2;
+    sb.nb[1] = (ts.ntr + 1) / 2;
+    sb.nb[2] = (ts.ntd + 1) / 2;
+    sb.n = sb.nb[0] * sb.nb[1] * sb.nb[2];
+    auto align = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t cells = size_t(g.B_rot) * size_t(sb.n);
+    const size_t counts = align(cells * sizeof(int)), lists = align(cells * size_t(g.P) * sizeof(unsigned short));
+    if (counts + lists > kBinsMaxBytes) return TP_OK;
+    char* w = static_cast<char*>(sc.bins(counts + lists, s));
+    if (!w) return TP_OK;
+    sb.count = reinterpret_cast<int*>(w);
+    sb.list = reinterpret_cast<unsigned short*>(w + counts);
+    // a bin's box holds its tiles' box-1 boxes (the tile dilated by the stencil and the slack) with
+    // half a voxel to spare
+    const float half = float(g.N / 2), pad = 0.5f;
+    const float sl = cubic ? 2.f : 1.f, sh = cubic ? 1.f : 0.f;
+    const tp::BinBox bb{{0.f, -half + 1.f, -half + 1.f},
+                        {2.f * tp::kScTC, 2.f * tp::kScTR, 2.f * tp::kScTD},
+                        sl + ts.eps + pad, sh + ts.eps + pad, ts.rho_unit + 1.0f};
+    TP_TRY(launched(tp::launch_pose_bins(g, rot, sb, bb, s), "pose-bin launch"));
+    ts.sbins = sb;
+    return TP_OK;
 }
 
 // TP_F16S: the volume is stored as complex half; it is widened exactly to
@@ -401,7 +459,7 @@ int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int6
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool cubic = interp == TP_CUBIC;
     if (use_tiles(dim, dt, os, n)) {
-        const tp::TileSpec ts = tile_spec(g, cubic);
+        tp::TileSpec ts = tile_spec(g, cubic);
         TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s));
         TP_TRY(launched(tp::launch_project3_forw_tiled(cubic, g, ts, rec, rot, shifts, out, sc.p, 0, s, rec_half),
                         "tiled projection launch"));
@@ -450,8 +508,9 @@ int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, in
     TP_TRY(need(rot, "rotations"));
     CallScratch sc;
     if (tiles) {
-        const tp::TileSpec ts = tile_spec(g, cubic);
+        tp::TileSpec ts = tile_spec(g, cubic);
         TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(make_bins(cubic, g, ts, rot, sc, s));
         TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, sc.p, 0,
                                                   s),
                         "tiled reconstruction-gradient launch"));
@@ -501,8 +560,9 @@ int backproject_forw(int dim, int dtype, const void* proj, int64_t B, int64_t P,
     TP_TRY(need(rot, "rotations"));
     CallScratch sc;
     if (tiles) {
-        const tp::TileSpec ts = tile_spec(g, cubic);
+        tp::TileSpec ts = tile_spec(g, cubic);
         TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(make_bins(cubic, g, ts, rot, sc, s));
         TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 0, g, ts, proj, weights, rot, shifts, data, wrec, sc.p, 0, s),
                         "tiled backprojection launch"));
     }
@@ -548,7 +608,7 @@ int backproject_back(int dim, int dtype, const void* gdata, const void* gw, int6
     }
     CallScratch sc;
     if (tiles) {
-        const tp::TileSpec ts = tile_spec(g, cubic);
+        tp::TileSpec ts = tile_spec(g, cubic);
         TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s));
         TP_TRY(launched(tp::launch_bpback3_tiled(cubic, g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
                                                  gshift, sc.p, 0, s),

@@ -37,6 +37,24 @@ constexpr float kRotationTol = 1e-5f;
 // Tile-owner enumeration parameters of the fp32 3D kernels (tp_tiled3d.hip).
 constexpr int kTileEdge = 16, kTileEdgeD = 12;         // forward tiles: 16 x 16 (c, r) x 12 (d) voxels
 constexpr int kScTC = 16, kScTR = 8, kScTD = 12;        // scatter tiles (c, r, d): fp64 accumulators
+
+// Pose bins of the scatter tile grid, filled per call by launch_pose_bins: for each block of
+// 2 x 2 x 2 tiles (a bin) and rotation batch item, the poses whose slice plane crosses the bin's
+// box, in increasing order.  The rotation kernel's tiles outside the core then cull only their
+// bin's poses instead of all P, in fewer and fuller phases.  list == nullptr: no bins (every tile
+// culls all its poses).
+struct BinGrid {
+    unsigned short* list;  // [B_rot][n][P] pose indices (P < 65536); entries past the count unused
+    int* count;            // [B_rot][n]
+    int nb[3];             // bins along c, r, d
+    int n;                 // nb[0] * nb[1] * nb[2]
+};
+// Box of bin (i, j, k) on axis a: [org[a] + idx * edge[a] - lo_pad, org[a] + (idx + 1) * edge[a] + hi_pad];
+// bins whose box lies beyond `reach` of the origin hold no pose.
+struct BinBox {
+    float org[3], edge[3];
+    float lo_pad, hi_pad, reach;
+};
 struct TileSpec {
     int nt, org;              // forward: tiles along c and r, and the signed origin of the grid there,
                               // laid out for unit-scale poses (|x| <= rho_unit + 1)
@@ -55,6 +73,7 @@ struct TileSpec {
     int cmax, rmin, rmax;     // pixel-grid limits of c and r (grid and cutoff)
     int kp_forw, kp_scatter;  // poses per wavefront batch (1, 2 or 4)
     bool os_exact;            // float(os) == os: c * os can be formed in float exactly as in double
+    BinGrid sbins;            // pose bins of the scatter tile grid (list null: none)
 };
 
 // Tile-owner kernels of the fp32 2D operators (tp_tiled2d.hip).
@@ -99,6 +118,10 @@ static_assert(sizeof(CallPoses) <= kCallScratchBytes, "call scratch");
 // Fill *cp for the B_rot * P poses at rot (dim 2 or 3), rho_unit = the
 // TileSpec/TileSpec2 field of the call.
 hipError_t launch_call_poses(int dim, int64_t poses, const void* rot, float rho_unit, CallPoses* cp, hipStream_t s);
+
+// Fill the pose bins bg (list and count allocated by the caller) of the scatter tile grid whose
+// bin boxes bb describes, for the B_rot * P poses at rot.
+hipError_t launch_pose_bins(const Geom& g, const void* rot, const BinGrid& bg, const BinBox& bb, hipStream_t s);
 
 constexpr int kBlock = 256;
 constexpr int64_t kMaxGrid = int64_t(1) << 22;

@@ -267,7 +267,7 @@ constexpr int kChunk = 1024;      // poses culled per phase
 constexpr unsigned kHit1 = 1u << 14, kHit2 = 1u << 15, kPoseMask = kHit1 - 1;
 static_assert(kChunk <= int(kPoseMask) + 1, "pose index must fit below the flag bits");
 
-// Cull poses [pbase, pend) (at most kChunk) against up to two boxes with a
+// Cull poses [pbase, pend) (at most CH) against up to two boxes with a
 // workgroup of NT lanes; returns the count.
 template <int NT, bool TWO, int CH, bool GEN>
 __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pend, int pbase, const float* lo1,
@@ -298,16 +298,17 @@ __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pe
     return np;
 }
 
-// Scatter culling: poses [pbase, pend) (at most kChunkSc) against box 1 and
-// box 2 separately.  Box-1 survivors fill plist from the front, box-2
-// survivors from the back (kChunk entries hold both lists), so each pass
-// batches only poses that cross its box.
+// Scatter culling: candidates [pbase, pend) (at most kChunkSc; poses, or
+// positions in the bin list lst as for cull_chunk) against box 1 and box 2
+// separately.  Box-1 survivors fill plist from the front, box-2 survivors from
+// the back (kChunk entries hold both lists), so each pass batches only poses
+// that cross its box.
 constexpr int kChunkSc = kChunk / 2;
 template <int NT, bool GEN>
 __device__ __forceinline__ void cull_chunk_boxes(const float* __restrict__ rotb, int pend, int pbase,
                                                  const float* lo1, const float* hi1, const float* lo2,
                                                  const float* hi2, unsigned short* plist, int* pcnt, int& n1,
-                                                 int& n2, bool all_rot) {
+                                                 int& n2, bool all_rot, const unsigned short* __restrict__ lst) {
     static_assert(kChunkSc % NT == 0 && (kChunkSc / NT) % kCullInFlight == 0, "cull shape");
     __syncthreads();  // every lane has read the previous counts and lists
     if (threadIdx.x == 0) pcnt[0] = pcnt[1] = 0;
@@ -315,21 +316,23 @@ __device__ __forceinline__ void cull_chunk_boxes(const float* __restrict__ rotb,
 #pragma unroll 1
     for (int q0 = 0; q0 < kChunkSc / NT; q0 += kCullInFlight) {
         float R[kCullInFlight][9];
+        int pq[kCullInFlight];
 #pragma unroll
         for (int q = 0; q < kCullInFlight; ++q) {
-            const int p = min(pbase + int(threadIdx.x) + (q0 + q) * NT, pend - 1);
-            load_rot(rotb + int64_t(p) * 9, R[q]);
+            const int k = min(pbase + int(threadIdx.x) + (q0 + q) * NT, pend - 1);
+            pq[q] = lst ? int(lst[k]) : k;
+            load_rot(rotb + int64_t(pq[q]) * 9, R[q]);
         }
 #pragma unroll
         for (int q = 0; q < kCullInFlight; ++q) {
-            const int p = pbase + int(threadIdx.x) + (q0 + q) * NT;
+            const int k = pbase + int(threadIdx.x) + (q0 + q) * NT;
             // box 2 is box 1 negated (bit for bit), which a plane through the origin
             // crosses exactly when it crosses box 1: one plane test serves both
             float as[3];
-            if (p >= pend || !pose_of_class<GEN>(R[q], as, all_rot) || !plane_hits(R[q], lo1, hi1)) continue;
-            if (half_plane_hits(as, hi1, lo1)) plist[atomicAdd(&pcnt[0], 1)] = (unsigned short)(p - pbase);
-            if (half_plane_hits(as, hi2, lo2))
-                plist[kChunk - 1 - atomicAdd(&pcnt[1], 1)] = (unsigned short)(p - pbase);
+            if (k >= pend || !pose_of_class<GEN>(R[q], as, all_rot) || !plane_hits(R[q], lo1, hi1)) continue;
+            const unsigned short e = lst ? (unsigned short)pq[q] : (unsigned short)(k - pbase);
+            if (half_plane_hits(as, hi1, lo1)) plist[atomicAdd(&pcnt[0], 1)] = e;
+            if (half_plane_hits(as, hi2, lo2)) plist[kChunk - 1 - atomicAdd(&pcnt[1], 1)] = e;
         }
     }
     __syncthreads();
@@ -337,7 +340,21 @@ __device__ __forceinline__ void cull_chunk_boxes(const float* __restrict__ rotb,
     n2 = pcnt[1];
 }
 
+// Pose bin of scatter tile (kc, kr, kd) in the grid with bins bg (rotation kernel, tiles outside the
+// core): its list and count for rotation batch item rb, or lst = nullptr when there are no bins.
+__device__ __forceinline__ void tile_bin(const BinGrid& bg, int64_t rb, int64_t P, int kc, int kr, int kd,
+                                         const unsigned short*& lst, int& cnt) {
+    lst = nullptr;
+    cnt = 0;
+    if (!bg.list) return;
+    const int64_t bi = rb * bg.n + (int64_t(kd >> 1) * bg.nb[1] + (kr >> 1)) * bg.nb[0] + (kc >> 1);
+    lst = bg.list + bi * P;
+    cnt = bg.count[bi];
+}
+
 // ----------------------------------------------------------------------------- forward
+// (The forward culls all its poses per tile: its single 2048-pose cull phase measured no faster
+// from pose bins, which cost a pre-pass.)
 // GMODE 0: forward projection into `out`.
 // GMODE 1: rotation and shift gradients of project_3d_to_2d_back for rotation
 //          poses (KP = 1): each owned sample's value and spatial gradient
@@ -486,6 +503,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
         for (int pbase = p0; pbase < p1; pbase += CH) {
             const int np = cull_chunk<NT, false, CH, GEN>(rotb, p1, pbase, lo, hi, lo, hi, plist, &pcount, all_rot);
             if (np == 0) continue;
+            auto pose_of = [&](unsigned e) { return pbase + int(e & kPoseMask); };
             if (!loaded) {
                 // stage the tile and its halo.  When the staged box lies on one side of c = 0 and
                 // needs no clamping, a cell is a plain wrapped load (conjugated from the mirrored
@@ -540,12 +558,10 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
             // wave batches of KP poses; the next batch's rotation and shift load during this one
             int base = wave * KP;
             float Rn[9], Sn[2];
-            load_pose(rotb, shifts ? shifts + sb * g.P * 2 : nullptr, pbase + (plist[min(base + slot, np - 1)] & kPoseMask),
-                      Rn, Sn);
+            load_pose(rotb, shifts ? shifts + sb * g.P * 2 : nullptr, pose_of(plist[min(base + slot, np - 1)]), Rn, Sn);
             for (; base < np; base += NW * KP) {
                 const bool sv = base + slot < np;
-                const unsigned pe = plist[min(base + slot, np - 1)];
-                const int pp = pbase + int(pe & kPoseMask);
+                const int pp = pose_of(plist[min(base + slot, np - 1)]);
                 float R[9], Sh[2];
 #pragma unroll
                 for (int e = 0; e < 9; ++e) R[e] = Rn[e];
@@ -553,7 +569,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                 Sh[1] = Sn[1];
                 if (base + NW * KP < np)
                     load_pose(rotb, shifts ? shifts + sb * g.P * 2 : nullptr,
-                              pbase + (plist[min(base + NW * KP + slot, np - 1)] & kPoseMask), Rn, Sn);
+                              pose_of(plist[min(base + NW * KP + slot, np - 1)]), Rn, Sn);
                 if (jrow == 0 && sv) {
                     Slot& sd = slots[wave][slot];
 #pragma unroll
@@ -896,15 +912,23 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
 
         const float* shb = shifts ? shifts + sb * g.P * 2 : nullptr;
         bool touched = false;  // GEN: some pose reaches the tile
-        for (int pbase = it.p0; pbase < pend; pbase += kChunkSc) {
+        // candidates: the tile's pose range, or (rotations, outside the core) its bin's poses
+        const unsigned short* lst = nullptr;
+        int lcnt = 0;
+        if (!GEN && !it.core && pend > it.p0) tile_bin(ts.sbins, rb, g.P, it.kc, it.kr, it.kd, lst, lcnt);
+        const int c_begin = lst ? 0 : it.p0, c_end = lst ? lcnt : pend;
+        for (int pbase = c_begin; pbase < c_end; pbase += kChunkSc) {
             int n1, n2;
-            cull_chunk_boxes<NT, GEN>(rotb, pend, pbase, lo1, hi1, lo2, hi2, plist, pcnt, n1, n2, all_rot);
+            cull_chunk_boxes<NT, GEN>(rotb, c_end, pbase, lo1, hi1, lo2, hi2, plist, pcnt, n1, n2, all_rot, lst);
             touched |= n1 + n2 > 0;
 #pragma unroll 1
             for (int pass = 0; pass < 2; ++pass) {
                 const int np = pass == 0 ? n1 : n2;
                 // pose of list entry k of this pass (box-2 entries are stored from the back)
-                auto pose_at = [&](int k) { return pbase + int(plist[pass == 0 ? k : kChunk - 1 - k]); };
+                auto pose_at = [&](int k) {
+                    const int e = int(plist[pass == 0 ? k : kChunk - 1 - k]);
+                    return lst ? e : pbase + e;
+                };
                 float lo[3], hi[3];
 #pragma unroll
                 for (int k = 0; k < 3; ++k) {
@@ -1103,6 +1127,58 @@ __global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<fl
     }
 }
 
+// Pose bins (launch_pose_bins): one workgroup per (rotation batch item, bin).  Lanes test 256
+// poses at a time against the bin's box with the tiles' plane test; a ballot and the waves'
+// counts place the hits in increasing pose order.  The bin box holds every tile box of its 2 x 2 x 2
+// tiles with half a voxel to spare on each side, far beyond the rounding of either plane test, so
+// a pose that crosses a tile's box is in its bin.
+constexpr int kBinThreads = 256;
+__global__ __launch_bounds__(kBinThreads) void k_pose_bins(Geom g, const float* __restrict__ rot, BinGrid bg,
+                                                           BinBox bb) {
+    __shared__ int wcnt[kBinThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t w = blockIdx.x;
+    const int64_t rb = w / bg.n;
+    const int bin = int(w - rb * bg.n);
+    const int idx[3] = {bin % bg.nb[0], (bin / bg.nb[0]) % bg.nb[1], bin / (bg.nb[0] * bg.nb[1])};
+    float lo[3], hi[3], dist2 = 0.f;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        lo[a] = bb.org[a] + float(idx[a]) * bb.edge[a] - bb.lo_pad;
+        hi[a] = bb.org[a] + float(idx[a] + 1) * bb.edge[a] + bb.hi_pad;
+        const float q = lo[a] > 0.f ? lo[a] : (hi[a] < 0.f ? -hi[a] : 0.f);
+        dist2 += q * q;
+    }
+    const int P = int(g.P);
+    const float* rotb = rot + rb * g.P * 9;
+    unsigned short* out = bg.list + w * g.P;
+    int total = 0;
+    const bool reached = dist2 <= bb.reach * bb.reach;  // tiles beyond the reach take no pose
+    for (int p0 = 0; reached && p0 < P; p0 += kBinThreads) {
+        const int p = p0 + tid;
+        bool hit = false;
+        if (p < P) {
+            float R[9];
+            load_rot(rotb + int64_t(p) * 9, R);
+            hit = plane_hits(R, lo, hi);
+        }
+        const uint64_t m = __ballot(hit);
+        const int rank = int(__builtin_amdgcn_mbcnt_hi(unsigned(m >> 32), __builtin_amdgcn_mbcnt_lo(unsigned(m), 0u)));
+        if (lane == 0) wcnt[wave] = __popcll(m);
+        __syncthreads();
+        int before = 0, sum = 0;
+#pragma unroll
+        for (int k = 0; k < kBinThreads / 64; ++k) {
+            before += k < wave ? wcnt[k] : 0;
+            sum += wcnt[k];
+        }
+        if (hit) out[total + before + rank] = (unsigned short)p;
+        total += sum;
+        __syncthreads();
+    }
+    if (tid == 0) bg.count[w] = total;
+}
+
 // Work items of the forward tile grid: the unit grid (rotations), or for GEN the whole wide
 // grid, a bound on the part of it that a call's reach selects (the kernel's persistent grid).
 template <bool GEN>
@@ -1236,6 +1312,13 @@ hipError_t forw_store(bool cubic, const Geom& g, const TileSpec& ts, const void*
 }
 
 }  // namespace
+
+hipError_t launch_pose_bins(const Geom& g, const void* rot, const BinGrid& bg, const BinBox& bb, hipStream_t s) {
+    const int64_t blocks = g.B_rot * int64_t(bg.n);
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_pose_bins, dim3(unsigned(blocks)), dim3(kBinThreads), 0, s, g, (const float*)rot, bg, bb);
+    return hipGetLastError();
+}
 
 hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* rec,
                                       const void* rot, const void* shifts, void* out, CallPoses* cp, int gl,
