@@ -429,7 +429,7 @@ int make_bins(bool cubic, const tp::Geom& g, tp::TileSpec& ts, const void* rot, 
     const tp::BinBox bb{{0.f, -half + 1.f, -half + 1.f},
                         {2.f * tp::kScTC, 2.f * tp::kScTR, 2.f * tp::kScTD},
                         sl + ts.eps + pad, sh + ts.eps + pad, ts.rho_unit + 1.0f};
-    TP_TRY(launched(tp::launch_pose_bins(g, rot, sb, bb, s), "pose-bin launch"));
+    TP_TRY(launched(tp::launch_pose_bins(g, rot, sb, bb, sc.p, s), "pose-bin launch"));
     ts.sbins = sb;
     return TP_OK;
 }

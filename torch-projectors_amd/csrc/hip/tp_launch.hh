@@ -120,8 +120,10 @@ static_assert(sizeof(CallPoses) <= kCallScratchBytes, "call scratch");
 hipError_t launch_call_poses(int dim, int64_t poses, const void* rot, float rho_unit, CallPoses* cp, hipStream_t s);
 
 // Fill the pose bins bg (list and count allocated by the caller) of the scatter tile grid whose
-// bin boxes bb describes, for the B_rot * P poses at rot.
-hipError_t launch_pose_bins(const Geom& g, const void* rot, const BinGrid& bg, const BinBox& bb, hipStream_t s);
+// bin boxes bb describes, for the B_rot * P poses at rot; after launch_call_poses has filled *cp
+// (all bins stay empty when the call has no rotation).
+hipError_t launch_pose_bins(const Geom& g, const void* rot, const BinGrid& bg, const BinBox& bb, const CallPoses* cp,
+                            hipStream_t s);
 
 constexpr int kBlock = 256;
 constexpr int64_t kMaxGrid = int64_t(1) << 22;

@@ -1134,7 +1134,7 @@ __global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<fl
 // a pose that crosses a tile's box is in its bin.
 constexpr int kBinThreads = 256;
 __global__ __launch_bounds__(kBinThreads) void k_pose_bins(Geom g, const float* __restrict__ rot, BinGrid bg,
-                                                           BinBox bb) {
+                                                           BinBox bb, const CallPoses* __restrict__ cp) {
     __shared__ int wcnt[kBinThreads / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t w = blockIdx.x;
@@ -1153,7 +1153,8 @@ __global__ __launch_bounds__(kBinThreads) void k_pose_bins(Geom g, const float* 
     const float* rotb = rot + rb * g.P * 9;
     unsigned short* out = bg.list + w * g.P;
     int total = 0;
-    const bool reached = dist2 <= bb.reach * bb.reach;  // tiles beyond the reach take no pose
+    // tiles beyond the reach take no pose, and only the rotation kernel reads the bins
+    const bool reached = dist2 <= bb.reach * bb.reach && call_flag(&cp->any_rot);
     for (int p0 = 0; reached && p0 < P; p0 += kBinThreads) {
         const int p = p0 + tid;
         bool hit = false;
@@ -1313,10 +1314,11 @@ hipError_t forw_store(bool cubic, const Geom& g, const TileSpec& ts, const void*
 
 }  // namespace
 
-hipError_t launch_pose_bins(const Geom& g, const void* rot, const BinGrid& bg, const BinBox& bb, hipStream_t s) {
+hipError_t launch_pose_bins(const Geom& g, const void* rot, const BinGrid& bg, const BinBox& bb, const CallPoses* cp,
+                            hipStream_t s) {
     const int64_t blocks = g.B_rot * int64_t(bg.n);
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_pose_bins, dim3(unsigned(blocks)), dim3(kBinThreads), 0, s, g, (const float*)rot, bg, bb);
+    hipLaunchKernelGGL(k_pose_bins, dim3(unsigned(blocks)), dim3(kBinThreads), 0, s, g, (const float*)rot, bg, bb, cp);
     return hipGetLastError();
 }
 
