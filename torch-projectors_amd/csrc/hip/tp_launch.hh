@@ -40,9 +40,9 @@ constexpr int kScTC = 16, kScTR = 8, kScTD = 12;        // scatter tiles (c, r, 
 
 // Pose bins of the scatter tile grid, filled per call by launch_pose_bins: for each block of
 // 2 x 2 x 2 tiles (a bin) and rotation batch item, the poses whose slice plane crosses the bin's
-// box, in increasing order.  The rotation kernel's tiles outside the core then cull only their
-// bin's poses instead of all P, in fewer and fuller phases.  list == nullptr: no bins (every tile
-// culls all its poses).
+// box, in increasing order (any matrix: the plane is spanned by its first two columns).  The
+// scatter's tiles outside the core then cull only their bin's poses instead of all P, in fewer and
+// fuller phases.  list == nullptr: no bins (every tile culls all its poses).
 struct BinGrid {
     unsigned short* list;  // [B_rot][n][P] pose indices (P < 65536); entries past the count unused
     int* count;            // [B_rot][n]
@@ -121,7 +121,7 @@ hipError_t launch_call_poses(int dim, int64_t poses, const void* rot, float rho_
 
 // Fill the pose bins bg (list and count allocated by the caller) of the scatter tile grid whose
 // bin boxes bb describes, for the B_rot * P poses at rot; after launch_call_poses has filled *cp
-// (all bins stay empty when the call has no rotation).
+// (bins beyond the reach of the call's tiled poses stay empty, bb.reach being the rotations').
 hipError_t launch_pose_bins(const Geom& g, const void* rot, const BinGrid& bg, const BinBox& bb, const CallPoses* cp,
                             hipStream_t s);
 

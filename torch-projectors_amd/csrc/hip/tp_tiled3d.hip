@@ -340,8 +340,8 @@ __device__ __forceinline__ void cull_chunk_boxes(const float* __restrict__ rotb,
     n2 = pcnt[1];
 }
 
-// Pose bin of scatter tile (kc, kr, kd) in the grid with bins bg (rotation kernel, tiles outside the
-// core): its list and count for rotation batch item rb, or lst = nullptr when there are no bins.
+// Pose bin of scatter tile (kc, kr, kd) in the grid with bins bg (tiles outside the core): its list
+// and count for rotation batch item rb, or lst = nullptr when there are no bins.
 __device__ __forceinline__ void tile_bin(const BinGrid& bg, int64_t rb, int64_t P, int kc, int kr, int kd,
                                          const unsigned short*& lst, int& cnt) {
     lst = nullptr;
@@ -912,10 +912,10 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
 
         const float* shb = shifts ? shifts + sb * g.P * 2 : nullptr;
         bool touched = false;  // GEN: some pose reaches the tile
-        // candidates: the tile's pose range, or (rotations, outside the core) its bin's poses
+        // candidates: the tile's pose range, or (outside the core) its bin's poses
         const unsigned short* lst = nullptr;
         int lcnt = 0;
-        if (!GEN && !it.core && pend > it.p0) tile_bin(ts.sbins, rb, g.P, it.kc, it.kr, it.kd, lst, lcnt);
+        if (!it.core && pend > it.p0) tile_bin(ts.sbins, rb, g.P, it.kc, it.kr, it.kd, lst, lcnt);
         const int c_begin = lst ? 0 : it.p0, c_end = lst ? lcnt : pend;
         for (int pbase = c_begin; pbase < c_end; pbase += kChunkSc) {
             int n1, n2;
@@ -1153,8 +1153,10 @@ __global__ __launch_bounds__(kBinThreads) void k_pose_bins(Geom g, const float* 
     const float* rotb = rot + rb * g.P * 9;
     unsigned short* out = bg.list + w * g.P;
     int total = 0;
-    // tiles beyond the reach take no pose, and only the rotation kernel reads the bins
-    const bool reached = dist2 <= bb.reach * bb.reach && call_flag(&cp->any_rot);
+    // tiles beyond the reach of the call's tiled poses (rotations, and the others up to their
+    // largest singular value) take no pose; a call without tiled poses needs no bins
+    const float gen = call_reach(&cp->gen_reach), reach = fmaxf(call_flag(&cp->any_rot) ? bb.reach : 0.f, gen);
+    const bool reached = reach > 0.f && dist2 <= reach * reach;
     for (int p0 = 0; reached && p0 < P; p0 += kBinThreads) {
         const int p = p0 + tid;
         bool hit = false;
