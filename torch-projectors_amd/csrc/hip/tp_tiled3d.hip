@@ -298,6 +298,57 @@ __device__ __forceinline__ int cull_chunk(const float* __restrict__ rotb, int pe
     return np;
 }
 
+// Forward culling of the other tiled poses (GEN) in two stages: a plane test of one pose per lane,
+// whose hits gather in the wave's row of `gst` (128 entries), and the class, dual-basis and
+// half-plane tests on 64 gathered hits at a time, so only the poses whose plane crosses the box
+// pay for the Gram matrix.  List entries as cull_chunk's (box 1 only).
+template <int NT, int CH>
+__device__ __forceinline__ int cull_chunk_gen(const float* __restrict__ rotb, int pend, int pbase, const float* lo,
+                                              const float* hi, unsigned short* plist, int* pcount,
+                                              unsigned short* gst) {
+    const int lane = threadIdx.x & 63;
+    __syncthreads();  // every lane has read the previous count and list
+    if (threadIdx.x == 0) *pcount = 0;
+    __syncthreads();
+    auto classify = [&](int nh) {  // lanes < nh test gathered hit `lane`
+        if (lane < nh) {
+            const int p = pbase + int(gst[lane]);
+            float R[9], as[3];
+            load_rot(rotb + int64_t(p) * 9, R);
+            if (pose_of_class<true>(R, as, false) && half_plane_hits(as, hi, lo))
+                plist[atomicAdd(pcount, 1)] = (unsigned short)((p - pbase) | kHit1);
+        }
+    };
+    int nh = 0;  // gathered hits of this wave
+#pragma unroll 1
+    for (int q0 = 0; q0 < CH / NT; ++q0) {
+        const int p = pbase + int(threadIdx.x) + q0 * NT;
+        bool hit = false;
+        if (p < pend) {
+            float R[9];
+            load_rot(rotb + int64_t(p) * 9, R);
+            hit = plane_hits(R, lo, hi);
+        }
+        const uint64_t m = __ballot(hit);
+        const int rank = int(__builtin_amdgcn_mbcnt_hi(unsigned(m >> 32), __builtin_amdgcn_mbcnt_lo(unsigned(m), 0u)));
+        if (hit) gst[nh + rank] = (unsigned short)(p - pbase);
+        nh += __popcll(m);
+        __builtin_amdgcn_wave_barrier();
+        if (nh >= 64) {
+            classify(64);
+            __builtin_amdgcn_wave_barrier();
+            const unsigned short rest = lane + 64 < nh ? gst[lane + 64] : 0;
+            __builtin_amdgcn_wave_barrier();
+            if (lane + 64 < nh) gst[lane] = rest;
+            nh -= 64;
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+    classify(nh);
+    __syncthreads();
+    return *pcount;
+}
+
 // Scatter culling: candidates [pbase, pend) (at most kChunkSc; poses, or
 // positions in the bin list lst as for cull_chunk) against box 1 and box 2
 // separately.  Box-1 survivors fill plist from the front, box-2 survivors from
@@ -444,6 +495,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
     static_assert(CH <= int(kPoseMask) + 1, "pose index must fit below the flag bits");
     __shared__ unsigned short plist[CH];
     __shared__ int pcount;
+    __shared__ unsigned short gst[GEN ? NW * 128 : 1];  // GEN culling: gathered plane hits per wave
     constexpr int QCAP = 256;
     __shared__ Slot slots[NW][KP];
     __shared__ unsigned queue[NW][QCAP];
@@ -501,7 +553,8 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
         const Cx<VS>* recb = rec + b * g.vol;
         bool loaded = false;
         for (int pbase = p0; pbase < p1; pbase += CH) {
-            const int np = cull_chunk<NT, false, CH, GEN>(rotb, p1, pbase, lo, hi, lo, hi, plist, &pcount, all_rot);
+            const int np = GEN ? cull_chunk_gen<NT, CH>(rotb, p1, pbase, lo, hi, plist, &pcount, gst + wave * 128)
+                               : cull_chunk<NT, false, CH, GEN>(rotb, p1, pbase, lo, hi, lo, hi, plist, &pcount, all_rot);
             if (np == 0) continue;
             auto pose_of = [&](unsigned e) { return pbase + int(e & kPoseMask); };
             if (!loaded) {
