@@ -40,7 +40,7 @@ constexpr int kScTC = 16, kScTR = 8, kScTD = 12;        // scatter tiles (c, r, 
 
 // Pose bins of the scatter tile grid, filled per call by launch_pose_bins: for each block of
 // 2 x 2 x 2 tiles (a bin) and rotation batch item, the poses whose slice plane crosses the bin's
-// box, in increasing order (any matrix: the plane is spanned by its first two columns).  The
+// box, in no particular order (any matrix: the plane is spanned by its first two columns).  The
 // scatter's tiles outside the core then cull only their bin's poses instead of all P, in fewer and
 // fuller phases.  list == nullptr: no bins (every tile culls all its poses).
 struct BinGrid {

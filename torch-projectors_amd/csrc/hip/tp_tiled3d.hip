@@ -1180,59 +1180,91 @@ __global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<fl
     }
 }
 
-// Pose bins (launch_pose_bins): one workgroup per (rotation batch item, bin).  Lanes test 256
-// poses at a time against the bin's box with the tiles' plane test; a ballot and the waves'
-// counts place the hits in increasing pose order.  The bin box holds every tile box of its 2 x 2 x 2
-// tiles with half a voxel to spare on each side, far beyond the rounding of either plane test, so
-// a pose that crosses a tile's box is in its bin.
-constexpr int kBinThreads = 256;
+// Pose bins (launch_pose_bins): one workgroup per rotation batch item, row of bins along c (bins
+// differ there only in their c extent) and block of kBinPoses poses, so each pose is loaded once per
+// row.  A lane tests its poses against every bin of the row with the tiles' plane test (a bit per
+// bin); per bin, a wave reserves room for its hits with one atomic on the bin's count and writes
+// them there.  A bin's list is thus in no particular order (the scatter's tiles cull it into
+// per-tile lists that are unordered anyway).  A bin box holds every tile box of its 2 x 2 x 2 tiles
+// with half a voxel to spare on each side, far beyond the rounding of either plane test, so a pose
+// that crosses a tile's box is in its bin.  The counts start at zero (launch_pose_bins clears them).
+constexpr int kBinThreads = 256, kBinPer = 4, kBinPoses = kBinThreads * kBinPer;
 __global__ __launch_bounds__(kBinThreads) void k_pose_bins(Geom g, const float* __restrict__ rot, BinGrid bg,
                                                            BinBox bb, const CallPoses* __restrict__ cp) {
-    __shared__ int wcnt[kBinThreads / 64];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t w = blockIdx.x;
-    const int64_t rb = w / bg.n;
-    const int bin = int(w - rb * bg.n);
-    const int idx[3] = {bin % bg.nb[0], (bin / bg.nb[0]) % bg.nb[1], bin / (bg.nb[0] * bg.nb[1])};
-    float lo[3], hi[3], dist2 = 0.f;
+    const int lane = threadIdx.x & 63;
+    const int nrow = bg.nb[1] * bg.nb[2];
+    const int64_t blocks = (g.P + kBinPoses - 1) / kBinPoses;
+    const int64_t w = blockIdx.x / blocks, pb = blockIdx.x - w * blocks;
+    const int64_t rb = w / nrow;
+    const int row = int(w - rb * nrow);
+    const int idx[3] = {0, row % bg.nb[1], row / bg.nb[1]};
+    float lo[3], hi[3];
 #pragma unroll
-    for (int a = 0; a < 3; ++a) {
+    for (int a = 1; a < 3; ++a) {
         lo[a] = bb.org[a] + float(idx[a]) * bb.edge[a] - bb.lo_pad;
         hi[a] = bb.org[a] + float(idx[a] + 1) * bb.edge[a] + bb.hi_pad;
-        const float q = lo[a] > 0.f ? lo[a] : (hi[a] < 0.f ? -hi[a] : 0.f);
-        dist2 += q * q;
     }
+    auto box_c = [&](int i) {
+        lo[0] = bb.org[0] + float(i) * bb.edge[0] - bb.lo_pad;
+        hi[0] = bb.org[0] + float(i + 1) * bb.edge[0] + bb.hi_pad;
+    };
+    // bins beyond the reach of the call's tiled poses (rotations, and the others up to their
+    // largest singular value) take no pose; a call without tiled poses needs no bins.  Along c
+    // (from 0 up) the distance grows, so the reached bins of a row come first.
+    const float gen = call_reach(&cp->gen_reach), reach = fmaxf(call_flag(&cp->any_rot) ? bb.reach : 0.f, gen);
+    int nreach = 0;
+    for (int i = 0; i < bg.nb[0]; ++i) {
+        box_c(i);
+        float dist2 = 0.f;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            const float q = lo[a] > 0.f ? lo[a] : (hi[a] < 0.f ? -hi[a] : 0.f);
+            dist2 += q * q;
+        }
+        if (reach > 0.f && dist2 <= reach * reach) nreach = i + 1;
+    }
+    if (nreach == 0) return;
     const int P = int(g.P);
     const float* rotb = rot + rb * g.P * 9;
-    unsigned short* out = bg.list + w * g.P;
-    int total = 0;
-    // tiles beyond the reach of the call's tiled poses (rotations, and the others up to their
-    // largest singular value) take no pose; a call without tiled poses needs no bins
-    const float gen = call_reach(&cp->gen_reach), reach = fmaxf(call_flag(&cp->any_rot) ? bb.reach : 0.f, gen);
-    const bool reached = reach > 0.f && dist2 <= reach * reach;
-    for (int p0 = 0; reached && p0 < P; p0 += kBinThreads) {
-        const int p = p0 + tid;
-        bool hit = false;
-        if (p < P) {
-            float R[9];
-            load_rot(rotb + int64_t(p) * 9, R);
-            hit = plane_hits(R, lo, hi);
-        }
-        const uint64_t m = __ballot(hit);
-        const int rank = int(__builtin_amdgcn_mbcnt_hi(unsigned(m >> 32), __builtin_amdgcn_mbcnt_lo(unsigned(m), 0u)));
-        if (lane == 0) wcnt[wave] = __popcll(m);
-        __syncthreads();
-        int before = 0, sum = 0;
+    int p[kBinPer];
+    float R[kBinPer][9];
 #pragma unroll
-        for (int k = 0; k < kBinThreads / 64; ++k) {
-            before += k < wave ? wcnt[k] : 0;
-            sum += wcnt[k];
-        }
-        if (hit) out[total + before + rank] = (unsigned short)p;
-        total += sum;
-        __syncthreads();
+    for (int u = 0; u < kBinPer; ++u) {
+        p[u] = int(pb) * kBinPoses + u * kBinThreads + int(threadIdx.x);
+        load_rot(rotb + int64_t(min(p[u], P - 1)) * 9, R[u]);
     }
-    if (tid == 0) bg.count[w] = total;
+    unsigned hits[kBinPer];  // bit i: the pose crosses bin i
+#pragma unroll
+    for (int u = 0; u < kBinPer; ++u) hits[u] = 0u;
+    for (int i = 0; i < nreach; ++i) {
+        box_c(i);
+#pragma unroll
+        for (int u = 0; u < kBinPer; ++u) hits[u] |= (p[u] < P && plane_hits(R[u], lo, hi)) ? 1u << i : 0u;
+    }
+    const int64_t bin0 = (rb * nrow + row) * int64_t(bg.nb[0]);
+    for (int i = 0; i < nreach; ++i) {
+        uint64_t m[kBinPer];
+        int total = 0;
+#pragma unroll
+        for (int u = 0; u < kBinPer; ++u) {
+            m[u] = __ballot((hits[u] >> i) & 1u);
+            total += __popcll(m[u]);
+        }
+        if (total == 0) continue;
+        int base = 0;
+        if (lane == 0) base = atomicAdd(&bg.count[bin0 + i], total);
+        base = __builtin_amdgcn_readfirstlane(base);
+        unsigned short* out = bg.list + (bin0 + i) * g.P;
+#pragma unroll
+        for (int u = 0; u < kBinPer; ++u) {
+            if ((hits[u] >> i) & 1u) {
+                const int rank = int(
+                    __builtin_amdgcn_mbcnt_hi(unsigned(m[u] >> 32), __builtin_amdgcn_mbcnt_lo(unsigned(m[u]), 0u)));
+                out[base + rank] = (unsigned short)p[u];
+            }
+            base += __popcll(m[u]);
+        }
+    }
 }
 
 // Work items of the forward tile grid: the unit grid (rotations), or for GEN the whole wide
@@ -1371,8 +1403,11 @@ hipError_t forw_store(bool cubic, const Geom& g, const TileSpec& ts, const void*
 
 hipError_t launch_pose_bins(const Geom& g, const void* rot, const BinGrid& bg, const BinBox& bb, const CallPoses* cp,
                             hipStream_t s) {
-    const int64_t blocks = g.B_rot * int64_t(bg.n);
+    const int64_t blocks = g.B_rot * int64_t(bg.nb[1]) * bg.nb[2] * ((g.P + kBinPoses - 1) / kBinPoses);
     if (blocks == 0) return hipSuccess;
+    if (blocks > int64_t(UINT32_MAX / kBinThreads)) return hipErrorInvalidValue;
+    const hipError_t e = launch_zero(bg.count, g.B_rot * int64_t(bg.n), s);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_pose_bins, dim3(unsigned(blocks)), dim3(kBinThreads), 0, s, g, (const float*)rot, bg, bb, cp);
     return hipGetLastError();
 }
