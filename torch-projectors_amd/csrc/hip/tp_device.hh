@@ -88,6 +88,30 @@ template <typename T> __device__ __forceinline__ T cubic_dw(T s) {
     return 0.0;
 }
 
+// Catmull-Rom weight (a = -0.5) of a tap at signed distance s and its derivative d/ds in fp32 with
+// fused multiply-adds, from the factored polynomials (1 - |s|)(1 + |s| - 1.5 s^2) for |s| <= 1 and
+// -0.5 (|s| - 1)(2 - |s|)^2 for 1 < |s| <= 2 (0 beyond): a few ulps from the true value everywhere,
+// so within a few ulps of cubic_w / cubic_dw away from the double root at |s| = 2, where the
+// reference's double evaluation carries ~1e-15 absolute error.  For the gradient sums only, whose
+// bar is relative (gathered values and scatter taps keep cubic_w's rounding).
+__device__ __forceinline__ float cubic_w_fast(float s) {
+    const float a = fabsf(s), t = 2.0f - a;
+    const float in = (1.0f - a) * fmaf(a, fmaf(a, -1.5f, 1.0f), 1.0f);
+    const float out = -0.5f * (a - 1.0f) * t * t;
+    return a <= 1.0f ? in : (a <= 2.0f ? out : 0.0f);
+}
+__device__ __forceinline__ float cubic_dw_fast(float s) {
+    const float a = fabsf(s);
+    const float in = a * fmaf(a, 4.5f, -5.0f);
+    const float out = (2.0f - a) * fmaf(a, 1.5f, -2.0f);
+    const float d = a <= 1.0f ? in : (a <= 2.0f ? out : 0.0f);
+    return s < 0.0f ? -d : d;
+}
+// acc + a * s with one rounding per component (gradient sums only).
+__device__ __forceinline__ Cx<float> cfma(Cx<float> a, float s, Cx<float> acc) {
+    return {fmaf(a.re, s, acc.re), fmaf(a.im, s, acc.im)};
+}
+
 // ---------------------------------------------------------------- gather taps
 // Friedel-aware FFTW-layout fetch with edge replication (fftw_sampling.h:42-76,
 // 96-137): c < 0 mirrors all coordinates and conjugates; c is clamped to N/2,

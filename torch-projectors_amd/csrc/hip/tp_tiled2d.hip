@@ -637,35 +637,37 @@ constexpr int GC = kGat2, GR = kGat2;
 constexpr double kTwoPi2 = 6.283185307179586476925286766559;
 
 // Bicubic value and gradient with the 16 taps reduced along c first (value
-// and d/dc weights), then r.  EXACT_V keeps the value in the reference's order
-// ((s * wr) * wc summed over r then c, interpolation_kernels.h:258-322) for
-// outputs that are gathers; the gradient carries the 1e-4 bar either way.
+// and d/dc weights), then r, with fused multiply-adds and the fp32 weight
+// polynomials: the gradient carries the 1e-4 bar.  EXACT_V keeps the value in
+// the reference's order and rounding ((s * wr) * wc summed over r then c, with
+// its weights, interpolation_kernels.h:258-322) for outputs that are gathers.
 template <bool EXACT_V, typename F>
 __device__ __forceinline__ Interp<float> cubic2_grads(F&& fetch, float r, float c) {
     float cx, rx;
     const int cf = split_as<false>(c, cx), rf = split_as<false>(r, rx);
+    auto w_of = [](float s) { return EXACT_V ? cubic_w<float>(s) : cubic_w_fast(s); };
     float wc[4], dwc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        wc[j] = cubic_w<float>(cx - float(j - 1));
-        dwc[j] = cubic_dw<float>(cx - float(j - 1));
+        wc[j] = w_of(cx - float(j - 1));
+        dwc[j] = cubic_dw_fast(cx - float(j - 1));
     }
     Interp<float> o;
     o.v = o.g[0] = o.g[1] = o.g[2] = {0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float wr = cubic_w<float>(rx - float(i - 1)), dwr = cubic_dw<float>(rx - float(i - 1));
+        const float wr = w_of(rx - float(i - 1)), dwr = cubic_dw_fast(rx - float(i - 1));
         Cx<float> a = {0.f, 0.f}, bc = {0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const Cx<float> t = fetch(rf + i - 1, cf + j - 1);
             if (EXACT_V) o.v = cadd(o.v, cscale(cscale(t, wr), wc[j]));
-            a = cadd(a, cscale(t, wc[j]));
-            bc = cadd(bc, cscale(t, dwc[j]));
+            a = cfma(t, wc[j], a);
+            bc = cfma(t, dwc[j], bc);
         }
-        if (!EXACT_V) o.v = cadd(o.v, cscale(a, wr));
-        o.g[0] = cadd(o.g[0], cscale(bc, wr));
-        o.g[1] = cadd(o.g[1], cscale(a, dwr));
+        if (!EXACT_V) o.v = cfma(a, wr, o.v);
+        o.g[0] = cfma(bc, wr, o.g[0]);
+        o.g[1] = cfma(a, dwr, o.g[1]);
     }
     return o;
 }

@@ -423,27 +423,29 @@ constexpr double kTwoPi = 6.283185307179586476925286766559;
 // Tricubic value and spatial gradient for the gradient sums (which carry the
 // 1e-4 bar, not bit-identity): the 64 taps are reduced along c first (value
 // and d/dc weights), then r, then d, instead of forming the four triple
-// products per tap.  EXACT_V also forms the value in the reference's order
-// (((s * wd) * wr) * wc summed over d, r, c) for outputs that are gathers.
-// Weights and taps as cubic3 (interpolation_kernels.h:345-425).
+// products per tap, with fused multiply-adds and the fp32 weight polynomials.
+// EXACT_V also forms the value in the reference's order
+// (((s * wd) * wr) * wc summed over d, r, c, with its weights) for outputs
+// that are gathers.  Weights and taps as cubic3 (interpolation_kernels.h:345-425).
 template <bool EXACT_V, typename F>
 __device__ __forceinline__ Interp<float> cubic3_grads(F&& fetch, float d, float r, float c) {
     float dx, rx, cx;
     const int df = split_as<false>(d, dx), rf = split_as<false>(r, rx), cf = split_as<false>(c, cx);
+    auto w_of = [](float s) { return EXACT_V ? cubic_w<float>(s) : cubic_w_fast(s); };
     float wc[4], dwc[4], wr[4], dwr[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        wc[j] = cubic_w<float>(cx - float(j - 1));
-        dwc[j] = cubic_dw<float>(cx - float(j - 1));
-        wr[j] = cubic_w<float>(rx - float(j - 1));
-        dwr[j] = cubic_dw<float>(rx - float(j - 1));
+        wc[j] = w_of(cx - float(j - 1));
+        dwc[j] = cubic_dw_fast(cx - float(j - 1));
+        wr[j] = w_of(rx - float(j - 1));
+        dwr[j] = cubic_dw_fast(rx - float(j - 1));
     }
     Interp<float> o;
     o.v = o.g[0] = o.g[1] = o.g[2] = {0.f, 0.f};
     Cx<float> ve = {0.f, 0.f};  // EXACT_V: the value in the reference's order
 #pragma unroll 1
     for (int k = 0; k < 4; ++k) {
-        const float wd = cubic_w<float>(dx - float(k - 1)), dwd = cubic_dw<float>(dx - float(k - 1));
+        const float wd = w_of(dx - float(k - 1)), dwd = cubic_dw_fast(dx - float(k - 1));
         Cx<float> pv = {0.f, 0.f}, pc = {0.f, 0.f}, pr = {0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -452,17 +454,17 @@ __device__ __forceinline__ Interp<float> cubic3_grads(F&& fetch, float d, float 
             for (int j = 0; j < 4; ++j) {
                 const Cx<float> t = fetch(df + k - 1, rf + i - 1, cf + j - 1);
                 if (EXACT_V) ve = cadd(ve, cscale(cscale(cscale(t, wd), wr[i]), wc[j]));
-                a = cadd(a, cscale(t, wc[j]));
-                bc = cadd(bc, cscale(t, dwc[j]));
+                a = cfma(t, wc[j], a);
+                bc = cfma(t, dwc[j], bc);
             }
-            pv = cadd(pv, cscale(a, wr[i]));
-            pc = cadd(pc, cscale(bc, wr[i]));
-            pr = cadd(pr, cscale(a, dwr[i]));
+            pv = cfma(a, wr[i], pv);
+            pc = cfma(bc, wr[i], pc);
+            pr = cfma(a, dwr[i], pr);
         }
-        o.v = cadd(o.v, cscale(pv, wd));
-        o.g[0] = cadd(o.g[0], cscale(pc, wd));
-        o.g[1] = cadd(o.g[1], cscale(pr, wd));
-        o.g[2] = cadd(o.g[2], cscale(pv, dwd));
+        o.v = cfma(pv, wd, o.v);
+        o.g[0] = cfma(pc, wd, o.g[0]);
+        o.g[1] = cfma(pr, wd, o.g[1]);
+        o.g[2] = cfma(pv, dwd, o.g[2]);
     }
     if (EXACT_V) o.v = ve;
     return o;
