@@ -72,12 +72,29 @@ template <bool CLAMP, typename T> __device__ __forceinline__ int split_as(T x, T
 // Catmull-Rom, a = -0.5 (cubic_kernels.h:25-43, 50-67).  `a` has the real type
 // but the literals are double, so the float instantiation evaluates most terms
 // in double -- except a*s*s*s, which is a float product -- and rounds once.
-template <typename T> __device__ __forceinline__ T cubic_w(T s) {
+// The two pieces, for s = |s| <= 1 and 1 < |s| <= 2.
+template <typename T> __device__ __forceinline__ T cubic_w_in(T s) {
     const T a = -0.5;
+    return (a + 2.0) * s * s * s - (a + 3.0) * s * s + 1.0;
+}
+template <typename T> __device__ __forceinline__ T cubic_w_out(T s) {
+    const T a = -0.5;
+    return a * s * s * s - 5.0 * a * s * s + 8.0 * a * s - 4.0 * a;
+}
+template <typename T> __device__ __forceinline__ T cubic_w(T s) {
     s = s < T(0) ? -s : s;
-    if (s <= 1.0) return (a + 2.0) * s * s * s - (a + 3.0) * s * s + 1.0;
-    if (s <= 2.0) return a * s * s * s - 5.0 * a * s * s + 8.0 * a * s - 4.0 * a;
+    if (s <= 1.0) return cubic_w_in<T>(s);
+    if (s <= 2.0) return cubic_w_out<T>(s);
     return 0.0;
+}
+// cubic_w(f - (j - 1)) of tap j < 4 for a fractional part f in [0, 1] (the tiled kernels, whose
+// coordinates are finite), bit for bit: taps 0 and 3 then lie at 1 <= |s| <= 2, taps 1 and 2 at
+// |s| <= 1, and at |s| = 1, where the pieces meet, both give +0, so each tap evaluates one piece.
+// (Compared with cubic_w over every float f in [0, 1): identical.  A NaN f, which cubic_w maps to
+// 0, must not reach it.)
+template <typename T> __device__ __forceinline__ T cubic_w_tap(T f, int j) {
+    const T s = f - T(j - 1), as = s < T(0) ? -s : s;
+    return (j == 1 || j == 2) ? cubic_w_in<T>(as) : cubic_w_out<T>(as);
 }
 template <typename T> __device__ __forceinline__ T cubic_dw(T s) {
     const T a = -0.5;
@@ -201,7 +218,7 @@ __device__ __forceinline__ Interp<T> cubic2(F&& fetch, T r, T c) {
     T wc[4], dwc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        wc[j] = cubic_w<T>(cx - T(j - 1));
+        wc[j] = CLAMP ? cubic_w<T>(cx - T(j - 1)) : cubic_w_tap<T>(cx, j);
         if (GRADS) dwc[j] = cubic_dw<T>(cx - T(j - 1));
     }
     Interp<T> o;
@@ -209,7 +226,7 @@ __device__ __forceinline__ Interp<T> cubic2(F&& fetch, T r, T c) {
     o.g[0] = o.g[1] = o.g[2] = {0, 0};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const T wr = cubic_w<T>(rx - T(i - 1));
+        const T wr = CLAMP ? cubic_w<T>(rx - T(i - 1)) : cubic_w_tap<T>(rx, i);
         const T dwr = GRADS ? cubic_dw<T>(rx - T(i - 1)) : T(0);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -271,8 +288,8 @@ __device__ __forceinline__ Interp<T> cubic3(F&& fetch, T d, T r, T c) {
     T wc[4], dwc[4], wr[4], dwr[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        wc[j] = cubic_w<T>(cx - T(j - 1));
-        wr[j] = cubic_w<T>(rx - T(j - 1));
+        wc[j] = CLAMP ? cubic_w<T>(cx - T(j - 1)) : cubic_w_tap<T>(cx, j);
+        wr[j] = CLAMP ? cubic_w<T>(rx - T(j - 1)) : cubic_w_tap<T>(rx, j);
         if (GRADS) {
             dwc[j] = cubic_dw<T>(cx - T(j - 1));
             dwr[j] = cubic_dw<T>(rx - T(j - 1));
@@ -283,7 +300,7 @@ __device__ __forceinline__ Interp<T> cubic3(F&& fetch, T d, T r, T c) {
     o.g[0] = o.g[1] = o.g[2] = {0, 0};
 #pragma unroll 1
     for (int k = 0; k < 4; ++k) {
-        const T wd = cubic_w<T>(dx - T(k - 1));
+        const T wd = CLAMP ? cubic_w<T>(dx - T(k - 1)) : cubic_w_tap<T>(dx, k);
         const T dwd = GRADS ? cubic_dw<T>(dx - T(k - 1)) : T(0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {

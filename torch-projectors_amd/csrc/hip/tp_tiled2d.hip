@@ -213,7 +213,7 @@ __device__ __forceinline__ void scatter_sample2(const Geom& g, const Slot2& sd, 
         for (int j = 0; j < K; ++j) {
             const int l = l0 + tm.sgn * j;
             loc[a][j] = (unsigned)(l - tm.lmin[a]) < (unsigned)(S[a] - tm.lmin[a]) ? l : -1;
-            if (CUBIC) wt[a][j] = double(cubic_w<float>(f - float(j - LOW)));
+            if (CUBIC) wt[a][j] = double(cubic_w_tap<float>(f, j));
         }
         if (!CUBIC) {
             wt[a][1] = double(f);
@@ -269,7 +269,7 @@ __device__ __forceinline__ void scatter_sample2_priv(const Geom& g, const Slot2&
         for (int j = 0; j < K; ++j) {
             const int l = l0 + tm.sgn * j;
             loc[a][j] = (unsigned)(l - tm.lmin[a]) < (unsigned)(S[a] - tm.lmin[a]) ? l : -1;
-            if (CUBIC) wt[a][j] = cubic_w<float>(f - float(j - LOW));
+            if (CUBIC) wt[a][j] = cubic_w_tap<float>(f, j);
         }
         if (!CUBIC) {
             wt[a][1] = f;
@@ -645,18 +645,18 @@ template <bool EXACT_V, typename F>
 __device__ __forceinline__ Interp<float> cubic2_grads(F&& fetch, float r, float c) {
     float cx, rx;
     const int cf = split_as<false>(c, cx), rf = split_as<false>(r, rx);
-    auto w_of = [](float s) { return EXACT_V ? cubic_w<float>(s) : cubic_w_fast(s); };
+    auto w_of = [](float f, int j) { return EXACT_V ? cubic_w_tap<float>(f, j) : cubic_w_fast(f - float(j - 1)); };
     float wc[4], dwc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        wc[j] = w_of(cx - float(j - 1));
+        wc[j] = w_of(cx, j);
         dwc[j] = cubic_dw_fast(cx - float(j - 1));
     }
     Interp<float> o;
     o.v = o.g[0] = o.g[1] = o.g[2] = {0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float wr = w_of(rx - float(i - 1)), dwr = cubic_dw_fast(rx - float(i - 1));
+        const float wr = w_of(rx, i), dwr = cubic_dw_fast(rx - float(i - 1));
         Cx<float> a = {0.f, 0.f}, bc = {0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {

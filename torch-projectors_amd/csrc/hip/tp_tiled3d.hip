@@ -431,13 +431,13 @@ template <bool EXACT_V, typename F>
 __device__ __forceinline__ Interp<float> cubic3_grads(F&& fetch, float d, float r, float c) {
     float dx, rx, cx;
     const int df = split_as<false>(d, dx), rf = split_as<false>(r, rx), cf = split_as<false>(c, cx);
-    auto w_of = [](float s) { return EXACT_V ? cubic_w<float>(s) : cubic_w_fast(s); };
+    auto w_of = [](float f, int j) { return EXACT_V ? cubic_w_tap<float>(f, j) : cubic_w_fast(f - float(j - 1)); };
     float wc[4], dwc[4], wr[4], dwr[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        wc[j] = w_of(cx - float(j - 1));
+        wc[j] = w_of(cx, j);
         dwc[j] = cubic_dw_fast(cx - float(j - 1));
-        wr[j] = w_of(rx - float(j - 1));
+        wr[j] = w_of(rx, j);
         dwr[j] = cubic_dw_fast(rx - float(j - 1));
     }
     Interp<float> o;
@@ -445,7 +445,7 @@ __device__ __forceinline__ Interp<float> cubic3_grads(F&& fetch, float d, float 
     Cx<float> ve = {0.f, 0.f};  // EXACT_V: the value in the reference's order
 #pragma unroll 1
     for (int k = 0; k < 4; ++k) {
-        const float wd = w_of(dx - float(k - 1)), dwd = cubic_dw_fast(dx - float(k - 1));
+        const float wd = w_of(dx, k), dwd = cubic_dw_fast(dx - float(k - 1));
         Cx<float> pv = {0.f, 0.f}, pc = {0.f, 0.f}, pr = {0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -857,7 +857,7 @@ __device__ __forceinline__ void scatter_sample(const Geom& g, const ScSlot& sd, 
         for (int j = 0; j < K; ++j) {
             const int l = l0 + tm.sgn * j;
             loc[a][j] = (unsigned)(l - tm.lmin[a]) < (unsigned)(S[a] - tm.lmin[a]) ? l : -1;
-            if (CUBIC) wt[a][j] = double(cubic_w<float>(f - float(j - LOW)));
+            if (CUBIC) wt[a][j] = double(cubic_w_tap<float>(f, j));
         }
         if (!CUBIC) {
             wt[a][1] = double(f);
