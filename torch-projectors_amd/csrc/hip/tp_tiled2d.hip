@@ -243,8 +243,11 @@ __device__ __forceinline__ void scatter_sample2(const Geom& g, const Slot2& sd, 
 // lie in distinct cells: the lanes of one tap never share a cell.  A wave's
 // LDS operations execute in order; the signal fence keeps the compiler from
 // moving one tap's read above the previous tap's write (another lane's tap
-// may have written that cell).  Products as the reference forms them:
-// (v * wr) * wc in fp32.
+// may have written that cell).  v * wr is rounded as the reference forms it;
+// the product with wc is fused into the fp32 sum (and the weight tap
+// wpix * |wr * wc| into its sum as (wpix * |wr|) * |wc|), one rounding per tap
+// fewer than the reference's order, far below the per-cell bar, and still
+// exactly 0 where every tap weight is.
 template <bool CUBIC, int MODE, bool WEIGHTS>
 __device__ __forceinline__ void scatter_sample2_priv(const Geom& g, const Slot2& sd, int rr, int cc, Cx<float> v,
                                                      float wpix, bool shifted, bool flip, const TapMap2& tm,
@@ -282,19 +285,17 @@ __device__ __forceinline__ void scatter_sample2_priv(const Geom& g, const Slot2&
         if (loc[1][i] < 0) continue;
         const int row = loc[1][i] * TC, rot = swizzle2(loc[1][i]);
         const float rre = vre * wt[1][i], rim = vim * wt[1][i];
+        const float rw = wpix * (CUBIC ? fabsf(wt[1][i]) : wt[1][i]);
 #pragma unroll
         for (int j = 0; j < K; ++j) {
             if (loc[0][j] < 0) continue;
             const int li = row + ((loc[0][j] + rot) & (TC - 1));
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             float2 t = pc[li];
-            t.x += rre * wt[0][j];
-            t.y += rim * wt[0][j];
+            t.x = fmaf(rre, wt[0][j], t.x);
+            t.y = fmaf(rim, wt[0][j], t.y);
             pc[li] = t;
-            if (WEIGHTS) {
-                const float w = wt[1][i] * wt[0][j];
-                pw[li] += wpix * (CUBIC ? fabsf(w) : w);
-            }
+            if (WEIGHTS) pw[li] = fmaf(rw, CUBIC ? fabsf(wt[0][j]) : wt[0][j], pw[li]);
         }
     }
 }
