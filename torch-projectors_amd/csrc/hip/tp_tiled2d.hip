@@ -858,19 +858,21 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
                                 const Cx<float> gg = shifts ? cmul(g0, cconj(ph)) : g0;
                                 const Cx<float> sv_ = GMODE == 1 ? g0 : gg;
                                 const Cx<float> mv = GMODE == 1 ? cmul(ip.v, ph) : ip.v;
+                                // Re(gg conj(dF/dx_row * s)) = s Re(gg conj(dF/dx_row)) with s = (c, r) * os, and
+                                // Re(sv conj(i k mv)) = k (sv.im mv.re - sv.re mv.im) with k = -2 pi (r, c) / n:
+                                // the sums take (c, r) and the constants os and -2 pi / n scale the pose's totals
                                 if (grot) {
-                                    const float sc = float(double(fc) * g.os), sr = float(double(fr) * g.os);
 #pragma unroll
                                     for (int row = 0; row < 2; ++row) {
-                                        acc[row * 2 + 0] += cmul(gg, cconj(cscale(ip.g[row], sc))).re;
-                                        acc[row * 2 + 1] += cmul(gg, cconj(cscale(ip.g[row], sr))).re;
+                                        const float d = fmaf(gg.re, ip.g[row].re, gg.im * ip.g[row].im);
+                                        acc[row * 2 + 0] = fmaf(d, fc, acc[row * 2 + 0]);
+                                        acc[row * 2 + 1] = fmaf(d, fr, acc[row * 2 + 1]);
                                     }
                                 }
                                 if (gshift) {
-                                    const Cx<float> kr = {0.f, float(-kTwoPi2 * double(fr) / double(g.n))};
-                                    const Cx<float> kc = {0.f, float(-kTwoPi2 * double(fc) / double(g.n))};
-                                    acc[4] += cmul(sv_, cconj(cmul(kr, mv))).re;
-                                    acc[5] += cmul(sv_, cconj(cmul(kc, mv))).re;
+                                    const float cr = fmaf(sv_.im, mv.re, -(sv_.re * mv.im));
+                                    acc[4] = fmaf(cr, fr, acc[4]);
+                                    acc[5] = fmaf(cr, fc, acc[5]);
                                 }
                             }
                         }
@@ -878,14 +880,16 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
                 }
                 if constexpr (GRADS) {
                     if (grot) {
+                        const float os = float(g.os);
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
-                            const float t = wave_sum(acc[k]);
+                            const float t = wave_sum(acc[k]) * os;
                             if (lane == 0 && sv) atomic_add(&grot[(rb * g.P + pp) * 4 + k], t);
                         }
                     }
                     if (gshift) {
-                        const float t0 = wave_sum(acc[4]), t1 = wave_sum(acc[5]);
+                        const float kn = float(-kTwoPi2 / double(g.n));
+                        const float t0 = wave_sum(acc[4]) * kn, t1 = wave_sum(acc[5]) * kn;
                         if (lane == 0 && sv) {
                             atomic_add(&gshift[(sb * g.P + pp) * 2], t0);
                             atomic_add(&gshift[(sb * g.P + pp) * 2 + 1], t1);

@@ -470,6 +470,27 @@ __device__ __forceinline__ Interp<float> cubic3_grads(F&& fetch, float d, float 
     return o;
 }
 
+// One sample's terms of the pose gradients: with s = (c, r) * os the rotation term of row k is
+// Re(a conj(dF/dx_k * s)) = s Re(a conj(dF/dx_k)), and with k = -2 pi (r, c) / n the shift terms are
+// Re(b conj(i k m)) = k (b.im m.re - b.re m.im).  The sums acc[3 row + {0, 1}] take (c, r) and
+// acc[9], acc[10] take (r, c); the pose's totals are scaled by os and -2 pi / n once.
+__device__ __forceinline__ void grad_terms(const Interp<float>& ip, Cx<float> a, Cx<float> b, Cx<float> m, float fr,
+                                           float fc, bool rot, bool shift, float* acc) {
+    if (rot) {
+#pragma unroll
+        for (int row = 0; row < 3; ++row) {
+            const float d = fmaf(a.re, ip.g[row].re, a.im * ip.g[row].im);
+            acc[row * 3 + 0] = fmaf(d, fc, acc[row * 3 + 0]);
+            acc[row * 3 + 1] = fmaf(d, fr, acc[row * 3 + 1]);
+        }
+    }
+    if (shift) {
+        const float cr = fmaf(b.im, m.re, -(b.re * m.im));
+        acc[9] = fmaf(cr, fr, acc[9]);
+        acc[10] = fmaf(cr, fc, acc[10]);
+    }
+}
+
 template <bool CUBIC, int KP, bool OSX, int GMODE = 0, bool RS = true, bool WG = false, typename VS = float,
           bool GEN = false>
 __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec ts, const Cx<VS>* __restrict__ rec,
@@ -717,23 +738,10 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                             }
                             if constexpr (GRADS) {
                                 // proj * conj(phase) against dF/dx * s and against -i 2 pi k / n * F
+                                // (grad_terms: the sums take (c, r), the pose's totals the constants)
                                 Cx<float> pv = gsrc[pidx];
                                 if (shifts) pv = cmul(pv, cconj(ph));
-                                if (grot) {
-                                    const float sc = OSX ? fc * float(g.os) : float(double(fc) * g.os);
-                                    const float sr = OSX ? fr * float(g.os) : float(double(fr) * g.os);
-#pragma unroll
-                                    for (int row = 0; row < 3; ++row) {
-                                        acc[row * 3 + 0] += cmul(pv, cconj(cscale(ip.g[row], sc))).re;
-                                        acc[row * 3 + 1] += cmul(pv, cconj(cscale(ip.g[row], sr))).re;
-                                    }
-                                }
-                                if (gshift) {
-                                    const Cx<float> kr = {0.f, float(-kTwoPi * double(fr) / double(g.n))};
-                                    const Cx<float> kc = {0.f, float(-kTwoPi * double(fc) / double(g.n))};
-                                    acc[9] += cmul(pv, cconj(cmul(kr, ip.v))).re;
-                                    acc[10] += cmul(pv, cconj(cmul(kc, ip.v))).re;
-                                }
+                                grad_terms(ip, pv, pv, ip.v, fr, fc, grot != nullptr, gshift != nullptr, acc);
                             }
                         } else {
                             const Interp<float> ip = CUBIC ? cubic3_grads<false>(lds, x[2], x[1], x[0])
@@ -741,24 +749,11 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                             const Cx<float> g0 = gsrc[sd.base + pix];
                             const Cx<float> ph = shifts ? phase_hw(fr, fc, sd.s0, sd.s1, g.phase_k)
                                                         : Cx<float>{1.f, 0.f};
-                            if (grot) {
-                                // g' = g * phase(-r, -c) = g * conj(phase(r, c)); s = (sc, sr, 0)
-                                const Cx<float> gg = shifts ? cmul(g0, cconj(ph)) : g0;
-                                const float sc = OSX ? fc * float(g.os) : float(double(fc) * g.os);
-                                const float sr = OSX ? fr * float(g.os) : float(double(fr) * g.os);
-#pragma unroll
-                                for (int row = 0; row < 3; ++row) {
-                                    acc[row * 3 + 0] += cmul(gg, cconj(cscale(ip.g[row], sc))).re;
-                                    acc[row * 3 + 1] += cmul(gg, cconj(cscale(ip.g[row], sr))).re;
-                                }
-                            }
-                            if (gshift) {
-                                const Cx<float> mod = cmul(ip.v, ph);
-                                const Cx<float> kr = {0.f, float(-kTwoPi * double(fr) / double(g.n))};
-                                const Cx<float> kc = {0.f, float(-kTwoPi * double(fc) / double(g.n))};
-                                acc[9] += cmul(g0, cconj(cmul(kr, mod))).re;
-                                acc[10] += cmul(g0, cconj(cmul(kc, mod))).re;
-                            }
+                            // g' = g * phase(-r, -c) = g * conj(phase(r, c)) against dF/dx * s, s = (sc, sr, 0);
+                            // g against -i 2 pi k / n * (F * phase)
+                            const Cx<float> gg = shifts ? cmul(g0, cconj(ph)) : g0;
+                            const Cx<float> mod = shifts ? cmul(ip.v, ph) : ip.v;
+                            grad_terms(ip, gg, g0, mod, fr, fc, grot != nullptr, gshift != nullptr, acc);
                         }
                       }
                     }
@@ -766,16 +761,18 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                 if constexpr (GRADS) {
                     // the pose's sums (every lane of the wave takes part; one adds them)
                     if (grot) {
+                        const float os = float(g.os);
 #pragma unroll
                         for (int row = 0; row < 3; ++row)
 #pragma unroll
                             for (int k = 0; k < 2; ++k) {
-                                const float t = wave_sum(acc[row * 3 + k]);
+                                const float t = wave_sum(acc[row * 3 + k]) * os;
                                 if (lane == 0 && sv) atomic_add(&grot[(rb * g.P + pp) * 9 + row * 3 + k], t);
                             }
                     }
                     if (gshift) {
-                        const float t0 = wave_sum(acc[9]), t1 = wave_sum(acc[10]);
+                        const float kn = float(-kTwoPi / double(g.n));
+                        const float t0 = wave_sum(acc[9]) * kn, t1 = wave_sum(acc[10]) * kn;
                         if (lane == 0 && sv) {
                             atomic_add(&gshift[(sb * g.P + pp) * 2], t0);
                             atomic_add(&gshift[(sb * g.P + pp) * 2 + 1], t1);
