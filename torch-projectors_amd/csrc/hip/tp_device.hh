@@ -4,7 +4,9 @@
 // (paths relative to the reference repository) with the same IEEE operation
 // sequence, so that sample coordinates, stencil indices, Friedel decisions
 // and per-tap products are bit-identical to the CPU kernels.  The library is
-// compiled with -ffp-contract=off: no FMA may be formed anywhere in here.
+// compiled with -ffp-contract=off: the compiler forms no FMA anywhere in here;
+// the only fused arithmetic is the explicit fmaf of the gradient-sum helpers
+// (cubic_w_fast, cubic_dw_fast, cfma), whose outputs carry a relative bar.
 //
 // Coordinate convention: a sample position is x = (c, r, d) -- x[0] is the
 // rfft column (the Hermitian half axis), x[1] the row, x[2] the slice.
@@ -73,15 +75,15 @@ template <bool CLAMP, typename T> __device__ __forceinline__ int split_as(T x, T
 // but the literals are double, so the float instantiation evaluates most terms
 // in double -- except a*s*s*s, which is a float product -- and rounds once.
 // The two pieces, for s = |s| <= 1 and 1 < |s| <= 2.
-template <typename T> __device__ __forceinline__ T cubic_w_in(T s) {
+template <typename T> __host__ __device__ __forceinline__ T cubic_w_in(T s) {
     const T a = -0.5;
     return (a + 2.0) * s * s * s - (a + 3.0) * s * s + 1.0;
 }
-template <typename T> __device__ __forceinline__ T cubic_w_out(T s) {
+template <typename T> __host__ __device__ __forceinline__ T cubic_w_out(T s) {
     const T a = -0.5;
     return a * s * s * s - 5.0 * a * s * s + 8.0 * a * s - 4.0 * a;
 }
-template <typename T> __device__ __forceinline__ T cubic_w(T s) {
+template <typename T> __host__ __device__ __forceinline__ T cubic_w(T s) {
     s = s < T(0) ? -s : s;
     if (s <= 1.0) return cubic_w_in<T>(s);
     if (s <= 2.0) return cubic_w_out<T>(s);
@@ -90,13 +92,13 @@ template <typename T> __device__ __forceinline__ T cubic_w(T s) {
 // cubic_w(f - (j - 1)) of tap j < 4 for a fractional part f in [0, 1] (the tiled kernels, whose
 // coordinates are finite), bit for bit: taps 0 and 3 then lie at 1 <= |s| <= 2, taps 1 and 2 at
 // |s| <= 1, and at |s| = 1, where the pieces meet, both give +0, so each tap evaluates one piece.
-// (Compared with cubic_w over every float f in [0, 1): identical.  A NaN f, which cubic_w maps to
-// 0, must not reach it.)
-template <typename T> __device__ __forceinline__ T cubic_w_tap(T f, int j) {
+// (tests/cubic_weights_check.hip compares it with cubic_w over every float f in [0, 1].  A NaN f,
+// which cubic_w maps to 0, must not reach it.)
+template <typename T> __host__ __device__ __forceinline__ T cubic_w_tap(T f, int j) {
     const T s = f - T(j - 1), as = s < T(0) ? -s : s;
     return (j == 1 || j == 2) ? cubic_w_in<T>(as) : cubic_w_out<T>(as);
 }
-template <typename T> __device__ __forceinline__ T cubic_dw(T s) {
+template <typename T> __host__ __device__ __forceinline__ T cubic_dw(T s) {
     const T a = -0.5;
     const T sign = (s < 0) ? -1.0 : 1.0;
     s = s < T(0) ? -s : s;
@@ -111,13 +113,13 @@ template <typename T> __device__ __forceinline__ T cubic_dw(T s) {
 // so within a few ulps of cubic_w / cubic_dw away from the double root at |s| = 2, where the
 // reference's double evaluation carries ~1e-15 absolute error.  For the gradient sums only, whose
 // bar is relative (gathered values and scatter taps keep cubic_w's rounding).
-__device__ __forceinline__ float cubic_w_fast(float s) {
+__host__ __device__ __forceinline__ float cubic_w_fast(float s) {
     const float a = fabsf(s), t = 2.0f - a;
     const float in = (1.0f - a) * fmaf(a, fmaf(a, -1.5f, 1.0f), 1.0f);
     const float out = -0.5f * (a - 1.0f) * t * t;
     return a <= 1.0f ? in : (a <= 2.0f ? out : 0.0f);
 }
-__device__ __forceinline__ float cubic_dw_fast(float s) {
+__host__ __device__ __forceinline__ float cubic_dw_fast(float s) {
     const float a = fabsf(s);
     const float in = a * fmaf(a, 4.5f, -5.0f);
     const float out = (2.0f - a) * fmaf(a, 1.5f, -2.0f);
