@@ -36,6 +36,25 @@ def random_cases(count, seed, max_n=40, min_p=1):
     return out
 
 
+def binned_cases():
+    """The 3D scatters with enough poses for the per-call pose bins (16 or more): a rotation per
+    batch item (B_rot = 2, one set of bin lists each) or broadcast, both interpolations, every other
+    pose scaled in the per-item cases (the bins also serve the kernels of other tiled poses)."""
+    rng = random.Random(9090)
+    out = []
+    seed = 9090
+    for op in ("backproject_2d_to_3d_forw", "project_3d_to_2d_back"):
+        for interp in ("linear", "cubic"):
+            for B_rot in (1, 2):
+                seed += 1
+                c = _case(f"binned_{op}_{interp}_brot{B_rot}", op, interp=interp,
+                          os=rng.choice([1.0, 1.5, 2.0]), cutoff=rng.choice([None, 9.5]), B=2,
+                          P=rng.choice([16, 40, 70]), n=2 * rng.randint(8, 18), B_rot=B_rot, B_shift=2, seed=seed)
+                c["scaled"] = B_rot == 2
+                out.append(c)
+    return out
+
+
 def scale_poses(args, case):
     """Scale every other pose matrix by 1.05 (a matrix that is not a rotation)."""
     idx = {"project_3d_to_2d_forw": 1, "project_2d_forw": 1, "project_3d_to_2d_back": 2, "project_2d_back": 2,
