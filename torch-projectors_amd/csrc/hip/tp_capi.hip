@@ -346,10 +346,16 @@ struct CallScratch {
     StreamScratch* area = nullptr;  // the (device, stream) area, when not static_area
     // A pose-bin workspace of `need` bytes on the call's stream, or nullptr: the static area has
     // none, and a failed allocation leaves the call without bins (the kernels then cull every pose).
-    // Growing waits for the stream's queued work, which may still read the old workspace.
+    // Growing waits for the stream's queued work, which may still read the old workspace; a stream
+    // under graph capture can neither wait nor allocate, so there the call goes without bins.
     void* bins(size_t need, hipStream_t st) {
         if (static_area || !area) return nullptr;
         if (need > area->bins_cap) {
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+                hipGetLastError();
+                return nullptr;
+            }
             if (hipStreamSynchronize(st) != hipSuccess) return nullptr;
             if (area->bins) hipFree(area->bins);
             area->bins = nullptr;
@@ -380,6 +386,16 @@ struct CallScratch {
             std::lock_guard<std::mutex> lk(g_scratch_mu);
             std::unique_ptr<StreamScratch>& slot = g_scratch[{dev, st}];
             if (!slot) {
+                // the area is allocated by the first call on the stream, which cannot happen under
+                // graph capture
+                hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+                TP_TRY(launched(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing"));
+                if (cs != hipStreamCaptureStatusNone) {
+                    g_scratch.erase({dev, st});
+                    return fail("the first call on a stream allocates its scratch, which graph capture forbids: "
+                                "call once on that stream before capturing, or use "
+                                "tp_project_3d_to_2d_forw_noalloc");
+                }
                 std::unique_ptr<StreamScratch> fresh(new StreamScratch);
                 TP_TRY(launched(hipMalloc(reinterpret_cast<void**>(&fresh->p), tp::kCallScratchBytes),
                                 "scratch allocation"));
