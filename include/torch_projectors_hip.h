@@ -49,9 +49,11 @@ extern "C" {
 
 #define TP_F32 0 /* complex64 + float32 */
 #define TP_F64 1 /* complex128 + float64 */
-/* Forward projections only (tp_project_2d_forw, tp_project_3d_to_2d_forw):
+/* Forward projections and their gradients only (tp_project_2d_forw,
+ * tp_project_3d_to_2d_forw, tp_project_2d_back, tp_project_3d_to_2d_back):
  * the reconstruction is stored as complex half (interleaved binary16 pairs,
- * torch.complex32); rotations, shifts and projections are TP_F32, and every
+ * torch.complex32); rotations, shifts, projections, grad_projections and the
+ * gradient outputs (grad_reconstruction complex64) are TP_F32, and every
  * stored value is widened exactly to fp32 before the TP_F32 arithmetic.  No
  * counterpart in the reference: an opt-in low-precision volume storage that
  * halves the volume's footprint and the bytes its staging reads. */

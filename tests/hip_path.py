@@ -22,9 +22,9 @@ def _dt(t):
         return capi.TP_F32
     if t.dtype == torch.complex128:
         return capi.TP_F64
-    if t.dtype == torch.complex32:  # forward projections of a complex-half volume
+    if t.dtype == torch.complex32:  # a complex-half volume (the projections and their gradients)
         return capi.TP_F16S
-    raise RuntimeError("complex64, complex128 or (forward) complex32 expected")
+    raise RuntimeError("complex64, complex128 or (volume) complex32 expected")
 
 
 def _proj_dtype(rec):
@@ -105,8 +105,8 @@ def _project_back(name, dims, grad_projections, reconstruction, rotations, shift
                   fourier_radius_cutoff):
     g, rec, rot, sh = _g(grad_projections), _g(reconstruction), _g(rotations), _g(shifts)
     B, P, n, hp = g.shape
-    grec = _poisoned(rec.shape, rec.dtype)
-    grot, gsh = _grad_outputs(rotations, shifts, rec)
+    grec = _poisoned(rec.shape, _proj_dtype(rec))  # complex64 for a complex-half volume
+    grot, gsh = _grad_outputs(rotations, shifts, grec)
     rec_dims = list(rec.shape[1:])
     capi.call(name, _dt(rec), _p(g), B, P, n, hp, _p(rec), *rec_dims, _p(rot), rot.shape[0], _p(sh),
               sh.shape[0] if sh is not None else 1, *_tail(interpolation, oversampling, fourier_radius_cutoff),

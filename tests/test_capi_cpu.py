@@ -93,15 +93,20 @@ def test_half_volume_forward_checks_arguments(kw, msg):
     assert msg in capi.lib().tp_last_error().decode()
 
 
-def test_half_volume_storage_is_forward_only():
+def test_half_volume_storage_is_projection_only():
     """TP_F16S (complex-half volume) is accepted by the two forward projections
-    only; every other entry point rejects it before enqueuing anything."""
+    and their backward ops only; every other entry point rejects it before
+    enqueuing anything."""
     lib = capi.lib()
     assert _forw3(dtype=capi.TP_F16S, P=0) == capi.TP_OK  # nothing to do, valid arguments
     rc = lib.tp_project_2d_forw(capi.TP_F16S, _P(8), 1, 16, 9, _P(8), 1, 0, _P(None), 1, 8, 0, 1.0, 0, 0.0, _P(8),
                                 _P(None))
     assert rc == capi.TP_OK
-    rc = lib.tp_project_3d_to_2d_back(capi.TP_F16S, _P(8), 1, 2, 8, 5, _P(8), 16, 16, 9, _P(8), 1, _P(None), 1, 0,
+    # the backward's argument checks run for TP_F16S (a depth other than the height is rejected)
+    rc = lib.tp_project_3d_to_2d_back(capi.TP_F16S, _P(8), 1, 2, 8, 5, _P(8), 8, 16, 9, _P(8), 1, _P(None), 1, 0,
+                                      1.0, 0, 0.0, _P(8), _P(None), _P(None), _P(None))
+    assert rc == capi.TP_ERR_INVALID and "depth" in lib.tp_last_error().decode()
+    rc = lib.tp_project_3d_to_2d_back(3, _P(8), 1, 2, 8, 5, _P(8), 16, 16, 9, _P(8), 1, _P(None), 1, 0,
                                       1.0, 0, 0.0, _P(8), _P(None), _P(None), _P(None))
     assert rc == capi.TP_ERR_INVALID and "dtype" in lib.tp_last_error().decode()
     rc = lib.tp_backproject_2d_forw(capi.TP_F16S, _P(8), 1, 1, 8, 5, _P(None), _P(8), 1, _P(None), 1, 0, 2.0, 0,

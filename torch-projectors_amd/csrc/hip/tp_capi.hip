@@ -501,6 +501,12 @@ int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, in
                  int64_t D, int64_t N, int64_t H, const void* rot, int64_t B_rot, const void* shifts,
                  int64_t B_shift, int interp, double os, int has_cut, double cut, void* grec, void* grot,
                  void* gshift, void* stream) {
+    // TP_F16S: the reconstruction is stored as complex half, widened exactly to fp32 on load;
+    // everything else (gradients of projections, poses and shifts, the outputs) is the TP_F32 path
+    const bool rec_half = dtype == TP_F16S;
+    if (dtype != TP_F32 && dtype != TP_F64 && !rec_half)
+        return fail("dtype must be TP_F32, TP_F64 or (a complex-half reconstruction) TP_F16S");
+    if (rec_half) dtype = TP_F32;
     tp::Geom g{};
     TP_TRY(check_common(dtype, interp, B, P, B_rot, shifts, B_shift, g));
     if (dim == 3 && D != N) return fail("reconstruction depth must equal its height");
@@ -530,7 +536,8 @@ int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, in
         TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, sc.p, 0,
                                                   s),
                         "tiled reconstruction-gradient launch"));
-        TP_TRY(launched(tp::launch_grads3_tiled(cubic, g, ts, gproj, rec, rot, shifts, grot, gshift, sc.p, 1, s),
+        TP_TRY(launched(tp::launch_grads3_tiled(cubic, g, ts, gproj, rec, rot, shifts, grot, gshift, sc.p, 1, s,
+                                                rec_half),
                         "tiled rotation/shift-gradient launch"));
     }
     if (tiles2) {
@@ -540,11 +547,11 @@ int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, in
                                                   s),
                         "tiled reconstruction-gradient launch"));
         TP_TRY(launched(tp::launch_gather2_tiled(cubic, 1, g, ts, rec, nullptr, rot, shifts, nullptr, nullptr, gproj,
-                                                 grot, gshift, sc.p, 1, s),
+                                                 grot, gshift, sc.p, 1, s, rec_half),
                         "tiled rotation/shift-gradient launch"));
     }
-    return launched(tp::launch_project_back(dim, dtype, cubic, g, gproj, rec, rot, shifts, grec, grot, gshift, s,
-                                            (tiles || tiles2) ? 1 : 0),
+    return launched(tp::launch_project_back(dim, rec_half ? 2 : dtype, cubic, g, gproj, rec, rot, shifts, grec, grot,
+                                            gshift, s, (tiles || tiles2) ? 1 : 0),
                     "projection backward launch");
 }
 

@@ -145,6 +145,7 @@ hipError_t launch_project_forw(int dim, int dt, bool cubic, const Geom& g, const
 // `rest` != 0 (fp32): tiled poses are left to the tiled kernels
 // entirely (the tiled scatter gives their reconstruction gradient,
 // launch_grads3_tiled / launch_gather2_tiled their rotation/shift gradients).
+// `dt` 2: a complex-half volume with fp32 arithmetic, gradients and outputs.
 hipError_t launch_project_back(int dim, int dt, bool cubic, const Geom& g, const void* gproj, const void* rec,
                                const void* rot, const void* shifts, void* grec, void* grot, void* gshift,
                                hipStream_t s, int rest = 0);
@@ -162,10 +163,10 @@ hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec&
                                       const void* rot, const void* shifts, void* out, CallPoses* cp, int gl,
                                       hipStream_t s, bool rec_half = false);
 // Rotation/shift gradients of project_3d_to_2d_back for tiled poses, added
-// into zero-filled grot / gshift (either may be null).
+// into zero-filled grot / gshift (either may be null); `rec_half` as for the forward.
 hipError_t launch_grads3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gproj, const void* rec,
                                const void* rot, const void* shifts, void* grot, void* gshift, CallPoses* cp, int gl,
-                               hipStream_t s);
+                               hipStream_t s, bool rec_half = false);
 // backproject_2d_to_3d_back for tiled poses into zero-filled outputs:
 // grad_projections from grad_data_rec, grad_weights from grad_weight_rec (when
 // both gw and gweights are given), rotation/shift gradients (either may be null).
@@ -190,7 +191,7 @@ hipError_t launch_scatter2_tiled(bool cubic, int mode, const Geom& g, const Tile
 // grad_projections) into zero-filled grot / gshift; mode 2:
 // backproject_2d_back (rec = grad_data_rec -> out, gw -> wout, and with gsrc =
 // projections the gradients).
-// `rec_half` (mode 0): the volume is stored as complex half and widened to fp32 on load.
+// `rec_half` (modes 0 and 1): the volume is stored as complex half and widened to fp32 on load.
 hipError_t launch_gather2_tiled(bool cubic, int mode, const Geom& g, const TileSpec2& ts, const void* rec,
                                 const void* gw, const void* rot, const void* shifts, void* out, void* wout,
                                 const void* gsrc, void* grot, void* gshift, CallPoses* cp, int gl, hipStream_t s,

@@ -108,10 +108,11 @@ __global__ __launch_bounds__(kBlock) void k_project_forw_rest(Geom g, const Cx<V
 // REST (fp32) 1: the reconstruction gradient of tiled poses comes from the
 // tiled scatter; only the other poses are scattered here.  REST 2: the tiled
 // kernels also give the rotation/shift gradients of tiled poses, which are
-// skipped here entirely.
-template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT, int REST>
+// skipped here entirely.  VS: the volume's storage type (complex half is widened
+// exactly to fp32 on load, with T = float).
+template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT, int REST, typename VS = T>
 __global__ __launch_bounds__(kBlock) void k_project_back(Geom g, const Cx<T>* __restrict__ gproj,
-                                                         const Cx<T>* __restrict__ rec, const T* __restrict__ rot,
+                                                         const Cx<VS>* __restrict__ rec, const T* __restrict__ rot,
                                                          const T* __restrict__ shifts, Cx<T>* __restrict__ grec,
                                                          T* __restrict__ grot, T* __restrict__ gshift) {
     constexpr int RS = DIM * DIM;
@@ -209,25 +210,25 @@ hipError_t forw_rest(const Geom& g, const void* rec, const void* rot, const void
     return hipGetLastError();
 }
 
-template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT, int REST>
+template <int DIM, typename T, bool CUBIC, bool ROT, bool SHIFT, int REST, typename VS>
 hipError_t back4(const Geom& g, const void* gproj, const void* rec, const void* rot, const void* shifts, void* grec,
                  void* grot, void* gshift, hipStream_t s) {
     // with REST most (pose, chunk) items are skipped at once: fewer, longer-lived blocks
     const unsigned grid = REST ? grid_for(g.B * g.P) : grid_for(g.work);
-    hipLaunchKernelGGL((k_project_back<DIM, T, CUBIC, ROT, SHIFT, REST>), dim3(grid), dim3(kBlock), 0,
-                       s, g, (const Cx<T>*)gproj, (const Cx<T>*)rec, (const T*)rot, (const T*)shifts, (Cx<T>*)grec,
+    hipLaunchKernelGGL((k_project_back<DIM, T, CUBIC, ROT, SHIFT, REST, VS>), dim3(grid), dim3(kBlock), 0,
+                       s, g, (const Cx<T>*)gproj, (const Cx<VS>*)rec, (const T*)rot, (const T*)shifts, (Cx<T>*)grec,
                        (T*)grot, (T*)gshift);
     return hipGetLastError();
 }
 
-template <int DIM, typename T, bool CUBIC, int REST = 0>
+template <int DIM, typename T, bool CUBIC, int REST = 0, typename VS = T>
 hipError_t back(const Geom& g, const void* gproj, const void* rec, const void* rot, const void* shifts, void* grec,
                 void* grot, void* gshift, hipStream_t s) {
     if (grot && gshift)
-        return back4<DIM, T, CUBIC, true, true, REST>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
-    if (grot) return back4<DIM, T, CUBIC, true, false, REST>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
-    if (gshift) return back4<DIM, T, CUBIC, false, true, REST>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
-    return back4<DIM, T, CUBIC, false, false, REST>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+        return back4<DIM, T, CUBIC, true, true, REST, VS>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+    if (grot) return back4<DIM, T, CUBIC, true, false, REST, VS>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+    if (gshift) return back4<DIM, T, CUBIC, false, true, REST, VS>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+    return back4<DIM, T, CUBIC, false, false, REST, VS>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
 }
 
 #define TP_DISPATCH(dim, dt, cubic, FN, ...)                                                  \
@@ -270,6 +271,20 @@ hipError_t launch_project_forw(int dim, int dt, bool cubic, const Geom& g, const
 hipError_t launch_project_back(int dim, int dt, bool cubic, const Geom& g, const void* gproj, const void* rec,
                                const void* rot, const void* shifts, void* grec, void* grot, void* gshift,
                                hipStream_t s, int rest) {
+    if (dt == 2) {  // complex-half volume, fp32 arithmetic, gradients and outputs
+        if (rest != 0) {
+            if (dim == 2)
+                return cubic ? back<2, float, true, 2, __half>(g, gproj, rec, rot, shifts, grec, grot, gshift, s)
+                             : back<2, float, false, 2, __half>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+            return cubic ? back<3, float, true, 2, __half>(g, gproj, rec, rot, shifts, grec, grot, gshift, s)
+                         : back<3, float, false, 2, __half>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+        }
+        if (dim == 2)
+            return cubic ? back<2, float, true, 0, __half>(g, gproj, rec, rot, shifts, grec, grot, gshift, s)
+                         : back<2, float, false, 0, __half>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+        return cubic ? back<3, float, true, 0, __half>(g, gproj, rec, rot, shifts, grec, grot, gshift, s)
+                     : back<3, float, false, 0, __half>(g, gproj, rec, rot, shifts, grec, grot, gshift, s);
+    }
     if (rest != 0 && dt == 0) {
         if (dim == 2)
             return cubic ? back<2, float, true, 2>(g, gproj, rec, rot, shifts, grec, grot, gshift, s)

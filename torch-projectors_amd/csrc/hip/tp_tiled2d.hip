@@ -683,7 +683,7 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
                                                             float* __restrict__ grot, float* __restrict__ gshift,
                                                             CallPoses* __restrict__ cp, int gl) {
     static_assert(GMODE == 0 || KP == 1, "the gradient modes sum one pose per wave batch");
-    static_assert(GMODE == 0 || std::is_same<VS, float>::value, "complex-half volumes are read by the forward only");
+    static_assert(GMODE != 2 || std::is_same<VS, float>::value, "complex-half volumes: forward and its gradients only");
     constexpr int LO = CUBIC ? 1 : 0, HI = CUBIC ? 2 : 1, WC = GC + LO + HI, WR = GR + LO + HI, W2 = WC * WR;
     constexpr int WW = (GMODE == 2 && WG) ? (GC + 1) * (GR + 1) : 1;  // bilinear weight taps
     constexpr int RPS = 64 / KP, NW = kThreads / 64, CH = 2048;
@@ -963,9 +963,15 @@ hipError_t launch_gather2_tiled(bool cubic, int mode, const Geom& g, const TileS
                                 const void* gw, const void* rot, const void* shifts, void* out, void* wout,
                                 const void* gsrc, void* grot, void* gshift, CallPoses* cp, int gl, hipStream_t s, bool rec_half) {
     if (rec_half) {
-        if (mode != 0) return hipErrorInvalidValue;
-        return cubic ? gather2_forw<true, __half>(g, ts, rec, rot, shifts, out, cp, gl, s)
-                     : gather2_forw<false, __half>(g, ts, rec, rot, shifts, out, cp, gl, s);
+        if (mode == 0)
+            return cubic ? gather2_forw<true, __half>(g, ts, rec, rot, shifts, out, cp, gl, s)
+                         : gather2_forw<false, __half>(g, ts, rec, rot, shifts, out, cp, gl, s);
+        if (mode != 1) return hipErrorInvalidValue;
+        if (!grot && !gshift) return hipSuccess;
+        return cubic ? gather2_launch<true, 1, 1, true, false, __half>(g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot,
+                                                                     gshift, cp, gl, s)
+                     : gather2_launch<false, 1, 1, true, false, __half>(g, ts, rec, gw, rot, shifts, out, wout, gsrc,
+                                                                      grot, gshift, cp, gl, s);
     }
     if (mode == 1 && !grot && !gshift) return hipSuccess;
     return cubic ? gather2_modes<true>(mode, g, ts, rec, gw, rot, shifts, out, wout, gsrc, grot, gshift, cp, gl, s)

@@ -503,7 +503,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                                                         const float* __restrict__ gw = nullptr,
                                                         float* __restrict__ wout = nullptr) {
     static_assert(GMODE == 0 || KP == 1, "the gradient modes sum one pose per wave batch");
-    static_assert(GMODE == 0 || std::is_same<VS, float>::value, "complex-half volumes are read by the forward only");
+    static_assert(GMODE != 2 || std::is_same<VS, float>::value, "complex-half volumes: forward and its gradients only");
     constexpr bool GRADS = GMODE == 1 || (GMODE == 2 && RS);
     constexpr int WW = (GMODE == 2 && WG) ? (L + 1) * (L + 1) * (LD + 1) : 1;  // trilinear weight taps
     __shared__ float wt[WW];
@@ -1420,13 +1420,17 @@ hipError_t launch_project3_forw_tiled(bool cubic, const Geom& g, const TileSpec&
 
 hipError_t launch_grads3_tiled(bool cubic, const Geom& g, const TileSpec& ts, const void* gproj, const void* rec,
                                const void* rot, const void* shifts, void* grot, void* gshift, CallPoses* cp, int gl,
-                               hipStream_t s) {
+                               hipStream_t s, bool rec_half) {
     if (!grot && !gshift) return hipSuccess;
-#define TP_GRADS(C, O) \
-    forw_both<C, 1, O, 1, true, false, float>(g, ts, rec, rot, shifts, nullptr, cp, gl, gproj, grot, gshift, nullptr, \
-                                              nullptr, s)
-    if (cubic) return ts.os_exact ? TP_GRADS(true, true) : TP_GRADS(true, false);
-    return ts.os_exact ? TP_GRADS(false, true) : TP_GRADS(false, false);
+#define TP_GRADS(C, O, V) \
+    forw_both<C, 1, O, 1, true, false, V>(g, ts, rec, rot, shifts, nullptr, cp, gl, gproj, grot, gshift, nullptr, \
+                                          nullptr, s)
+    if (rec_half) {
+        if (cubic) return ts.os_exact ? TP_GRADS(true, true, __half) : TP_GRADS(true, false, __half);
+        return ts.os_exact ? TP_GRADS(false, true, __half) : TP_GRADS(false, false, __half);
+    }
+    if (cubic) return ts.os_exact ? TP_GRADS(true, true, float) : TP_GRADS(true, false, float);
+    return ts.os_exact ? TP_GRADS(false, true, float) : TP_GRADS(false, false, float);
 #undef TP_GRADS
 }
 

@@ -96,10 +96,10 @@ int dtype_code(const Tensor& complex_tensor) {
 }
 
 // Opt-in low-precision volume storage (no counterpart in the reference): a
-// complex32 reconstruction is projected natively (TP_F16S, widened to fp32 on
-// load, complex64 projections); the backward ops work on its exact complex64
-// widening and return the reconstruction gradient as complex32, the dtype
-// autograd expects for that input.
+// complex32 reconstruction is read natively by the projection and its backward
+// (TP_F16S: every value widened exactly to fp32 on load, complex64 projections
+// and fp32 gradient arithmetic); the backward returns the reconstruction
+// gradient as complex32, the dtype autograd expects for that input.
 bool is_half_volume(const Tensor& reconstruction) { return reconstruction.scalar_type() == at::kComplexHalf; }
 
 int interp_code(const std::string& s) { return s == "cubic" ? TP_CUBIC : TP_LINEAR; }
@@ -195,10 +195,11 @@ std::tuple<Tensor, Tensor, Tensor> project_back(int dim, const Tensor& grad_proj
     c10::hip::HIPGuardMasqueradingAsCUDA guard(dev);
     TORCH_CHECK(grad_projections.device() == dev, "all tensors must be on the same GPU");
     const Tensor g = grad_projections.contiguous();
-    const Tensor rec = half ? reconstruction.to(at::kComplexFloat).contiguous() : reconstruction.contiguous();
-    const int dt = dtype_code(rec);
-    check_real_dtypes(rec.scalar_type(), rotations, c10::nullopt);
-    const auto real = c10::toRealValueType(rec.scalar_type());
+    const Tensor rec = reconstruction.contiguous();
+    const int dt = half ? TP_F16S : dtype_code(rec);
+    const auto cplx = half ? at::kComplexFloat : rec.scalar_type();
+    check_real_dtypes(cplx, rotations, c10::nullopt);
+    const auto real = c10::toRealValueType(cplx);
     const Prep rot = prep(rotations, real, dev), sh = prep_opt(shifts, real, dev);
     PoseGrads pg = pose_grads(rotations, shifts, rot, sh);
     Tensor grec = at::empty(rec.sizes(), grad_projections.options());
