@@ -243,16 +243,21 @@ __device__ __forceinline__ void scatter_sample2(const Geom& g, const Slot2& sd, 
 // lie in distinct cells: the lanes of one tap never share a cell.  A wave's
 // LDS operations execute in order; the signal fence keeps the compiler from
 // moving one tap's read above the previous tap's write (another lane's tap
-// may have written that cell).  v * wr is rounded as the reference forms it;
-// the product with wc is fused into the fp32 sum (and the weight tap
-// wpix * |wr * wc| into its sum as (wpix * |wr|) * |wc|), one rounding per tap
-// fewer than the reference's order, far below the per-cell bar, and still
+// may have written that cell).  The private tile has rows of PS = TC + 1
+// cells (the odd stride spreads a column over the banks) and one row more: a
+// tap outside the tile goes to that row or to a row's last cell, which are
+// never written out, so every tap runs without a test or branch (lanes that
+// share those cells only lose garbage).  v * wr is rounded as the reference
+// forms it; the product with wc is fused into the fp32 sum (and the weight
+// tap wpix * |wr * wc| into its sum as (wpix * |wr|) * |wc|), one rounding per
+// tap fewer than the reference's order, far below the per-cell bar, and still
 // exactly 0 where every tap weight is.
+constexpr int PS = TC + 1, PT = (TR + 1) * PS;  // private tile: row stride, cells
 template <bool CUBIC, int MODE, bool WEIGHTS>
 __device__ __forceinline__ void scatter_sample2_priv(const Geom& g, const Slot2& sd, int rr, int cc, Cx<float> v,
                                                      float wpix, bool shifted, bool flip, const TapMap2& tm,
                                                      float2* pc, float* pw) {
-    constexpr int K = CUBIC ? 4 : 2, LOW = CUBIC ? 1 : 0;
+    constexpr int K = CUBIC ? 4 : 2;
     const float fr = float(rr), fc = float(cc);
     float x[2];
     rotate_pix(sd.R, fr, fc, g.os, x);
@@ -261,7 +266,7 @@ __device__ __forceinline__ void scatter_sample2_priv(const Geom& g, const Slot2&
         else v = cmul(v, phase_hw(-fr, -fc, sd.s0, sd.s1, g.phase_k));
     }
     constexpr int S[2] = {TC, TR};
-    int loc[2][K];
+    int loc[2][K];  // column, or row offset, of each tap; the spare cell / row outside the tile
     float wt[2][K];
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
@@ -271,7 +276,8 @@ __device__ __forceinline__ void scatter_sample2_priv(const Geom& g, const Slot2&
 #pragma unroll
         for (int j = 0; j < K; ++j) {
             const int l = l0 + tm.sgn * j;
-            loc[a][j] = (unsigned)(l - tm.lmin[a]) < (unsigned)(S[a] - tm.lmin[a]) ? l : -1;
+            const bool in = (unsigned)(l - tm.lmin[a]) < (unsigned)(S[a] - tm.lmin[a]);
+            loc[a][j] = a == 0 ? (in ? l : TC) : (in ? l : TR) * PS;
             if (CUBIC) wt[a][j] = cubic_w_tap<float>(f, j);
         }
         if (!CUBIC) {
@@ -282,14 +288,11 @@ __device__ __forceinline__ void scatter_sample2_priv(const Geom& g, const Slot2&
     const float vre = v.re, vim = flip ? -v.im : v.im;
 #pragma unroll
     for (int i = 0; i < K; ++i) {
-        if (loc[1][i] < 0) continue;
-        const int row = loc[1][i] * TC, rot = swizzle2(loc[1][i]);
         const float rre = vre * wt[1][i], rim = vim * wt[1][i];
         const float rw = wpix * (CUBIC ? fabsf(wt[1][i]) : wt[1][i]);
 #pragma unroll
         for (int j = 0; j < K; ++j) {
-            if (loc[0][j] < 0) continue;
-            const int li = row + ((loc[0][j] + rot) & (TC - 1));
+            const int li = loc[1][i] + loc[0][j];
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             float2 t = pc[li];
             t.x = fmaf(rre, wt[0][j], t.x);
@@ -318,7 +321,7 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
     constexpr int RPS = 64 / KP;
     constexpr int NW = kThreads / 64;
     static_assert(!PRIV || KP == 1, "private accumulation needs one pose per window");
-    constexpr int TS = PRIV ? 1 : T2, TP = PRIV ? T2 : 1;
+    constexpr int TS = PRIV ? 1 : T2, TP = PRIV ? PT : 1;
     __shared__ double acc_re[TS], acc_im[TS];
     __shared__ double acc_w[WEIGHTS ? TS : 1];
     __shared__ float2 pacc[NW][TP];
@@ -370,10 +373,11 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
         const float hi2[2] = {float(fc0 + TC + SH) + ts.eps, float(fr0 + TR + SH) + ts.eps};
         for (int e = tid; e < T2; e += kThreads) {
             if constexpr (PRIV) {
+                const int pe = (e / TC) * PS + e % TC;  // the private tile's cells (not its spare ones)
 #pragma unroll
                 for (int k = 0; k < NW; ++k) {
-                    pacc[k][e] = float2{0.f, 0.f};
-                    if (WEIGHTS) pwacc[k][e] = 0.f;
+                    pacc[k][pe] = float2{0.f, 0.f};
+                    if (WEIGHTS) pwacc[k][pe] = 0.f;
                 }
             } else {
                 acc_re[e] = 0.0;
@@ -518,12 +522,13 @@ __global__ __launch_bounds__(kThreads) void k_scatter2_tiled(Geom g, TileSpec2 t
                 const int a = (e - lc) + ((lc + swizzle2(lr)) & (TC - 1));
                 double vr, vi, vw = 0.0;
                 if constexpr (PRIV) {
+                    const int pa = lr * PS + lc;
                     vr = vi = 0.0;
 #pragma unroll
                     for (int k = 0; k < NW; ++k) {
-                        vr += double(pacc[k][a].x);
-                        vi += double(pacc[k][a].y);
-                        if (WEIGHTS) vw += double(pwacc[k][a]);
+                        vr += double(pacc[k][pa].x);
+                        vi += double(pacc[k][pa].y);
+                        if (WEIGHTS) vw += double(pwacc[k][pa]);
                     }
                 } else {
                     vr = acc_re[a];
