@@ -418,8 +418,9 @@ int call_poses(int dim, const tp::Geom& g, const void* rot, float rho_unit, Call
 
 // Pose bins of the tiled 3D scatter's tile grid for this call (tp::BinGrid), in 2 x 2 x 2 tiles,
 // filled by launch_pose_bins after the call's pose summary.  None below kBinsMinPoses poses,
-// from 65536 poses (list entries are 16-bit) or beyond kBinsMaxBytes, and none without a
-// workspace: the scatter then culls every pose of each tile.
+// from 65536 poses (list entries are 16-bit), beyond kBinsMaxBytes or tp::kBinMaxGroups
+// workgroups of the pre-pass, and none without a workspace: the scatter then culls every pose of
+// each tile.
 constexpr int64_t kBinsMinPoses = 16;
 constexpr size_t kBinsMaxBytes = size_t(1) << 30;
 int make_bins(bool cubic, const tp::Geom& g, tp::TileSpec& ts, const void* rot, CallScratch& sc, hipStream_t s) {
@@ -434,6 +435,8 @@ int make_bins(bool cubic, const tp::Geom& g, tp::TileSpec& ts, const void* rot, 
     const size_t cells = size_t(g.B_rot) * size_t(sb.n);
     const size_t counts = align(cells * sizeof(int)), lists = align(cells * size_t(g.P) * sizeof(unsigned short));
     if (counts + lists > kBinsMaxBytes) return TP_OK;
+    if (g.B_rot * int64_t(sb.nb[1]) * sb.nb[2] * ((g.P + tp::kBinPoses - 1) / tp::kBinPoses) > tp::kBinMaxGroups)
+        return TP_OK;
     char* w = static_cast<char*>(sc.bins(counts + lists, s));
     if (!w) return TP_OK;
     sb.count = reinterpret_cast<int*>(w);

@@ -43,6 +43,9 @@ constexpr int kScTC = 16, kScTR = 8, kScTD = 12;        // scatter tiles (c, r, 
 // box, in no particular order (any matrix: the plane is spanned by its first two columns).  The
 // scatter's tiles outside the core then cull only their bin's poses instead of all P, in fewer and
 // fuller phases.  list == nullptr: no bins (every tile culls all its poses).
+constexpr int kBinPoses = 1024;  // poses per workgroup of the bin pre-pass
+constexpr int64_t kBinMaxGroups = (int64_t(1) << 24) - 1;  // most workgroups of one bin pre-pass (256 lanes each
+                                                          // stay below 2^32 lanes); a larger call gets no bins
 struct BinGrid {
     unsigned short* list;  // [B_rot][n][P] pose indices (P < 65536); entries past the count unused
     int* count;            // [B_rot][n]

@@ -1187,7 +1187,8 @@ __global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<fl
 // per-tile lists that are unordered anyway).  A bin box holds every tile box of its 2 x 2 x 2 tiles
 // with half a voxel to spare on each side, far beyond the rounding of either plane test, so a pose
 // that crosses a tile's box is in its bin.  The counts start at zero (launch_pose_bins clears them).
-constexpr int kBinThreads = 256, kBinPer = 4, kBinPoses = kBinThreads * kBinPer;
+constexpr int kBinThreads = 256, kBinPer = kBinPoses / kBinThreads;
+static_assert(kBinPer * kBinThreads == kBinPoses, "bin pre-pass shape");
 __global__ __launch_bounds__(kBinThreads) void k_pose_bins(Geom g, const float* __restrict__ rot, BinGrid bg,
                                                            BinBox bb, const CallPoses* __restrict__ cp) {
     const int lane = threadIdx.x & 63;
@@ -1404,7 +1405,7 @@ hipError_t launch_pose_bins(const Geom& g, const void* rot, const BinGrid& bg, c
                             hipStream_t s) {
     const int64_t blocks = g.B_rot * int64_t(bg.nb[1]) * bg.nb[2] * ((g.P + kBinPoses - 1) / kBinPoses);
     if (blocks == 0) return hipSuccess;
-    if (blocks > int64_t(UINT32_MAX / kBinThreads)) return hipErrorInvalidValue;
+    if (blocks > kBinMaxGroups) return hipErrorInvalidValue;  // make_bins keeps calls below it
     const hipError_t e = launch_zero(bg.count, g.B_rot * int64_t(bg.n), s);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_pose_bins, dim3(unsigned(blocks)), dim3(kBinThreads), 0, s, g, (const float*)rot, bg, bb, cp);
