@@ -472,22 +472,33 @@ __device__ __forceinline__ Interp<float> cubic3_grads(F&& fetch, float d, float 
 
 // One sample's terms of the pose gradients: with s = (c, r) * os the rotation term of row k is
 // Re(a conj(dF/dx_k * s)) = s Re(a conj(dF/dx_k)), and with k = -2 pi (r, c) / n the shift terms are
-// Re(b conj(i k m)) = k (b.im m.re - b.re m.im).  The sums acc[3 row + {0, 1}] take (c, r) and
-// acc[9], acc[10] take (r, c); the pose's totals are scaled by os and -2 pi / n once.
+// Re(b conj(i k m)) = k (b.im m.re - b.re m.im).  The sums acc[.][3 row + {0, 1}] take (c, r) and
+// acc[.][9], acc[.][10] take (r, c); the pose's totals are scaled by os and -2 pi / n once.  With KS
+// poses per wave batch a lane keeps one set of sums per pose slot; the sample's terms go to its
+// slot's set, the others take 0 (selected, so a non-finite term stays with its own pose).
+template <int KS>
 __device__ __forceinline__ void grad_terms(const Interp<float>& ip, Cx<float> a, Cx<float> b, Cx<float> m, float fr,
-                                           float fc, bool rot, bool shift, float* acc) {
+                                           float fc, bool rot, bool shift, int sl, float (*acc)[11]) {
     if (rot) {
 #pragma unroll
         for (int row = 0; row < 3; ++row) {
             const float d = fmaf(a.re, ip.g[row].re, a.im * ip.g[row].im);
-            acc[row * 3 + 0] = fmaf(d, fc, acc[row * 3 + 0]);
-            acc[row * 3 + 1] = fmaf(d, fr, acc[row * 3 + 1]);
+#pragma unroll
+            for (int k = 0; k < KS; ++k) {
+                const float ds = (KS == 1 || sl == k) ? d : 0.f;
+                acc[k][row * 3 + 0] = fmaf(ds, fc, acc[k][row * 3 + 0]);
+                acc[k][row * 3 + 1] = fmaf(ds, fr, acc[k][row * 3 + 1]);
+            }
         }
     }
     if (shift) {
         const float cr = fmaf(b.im, m.re, -(b.re * m.im));
-        acc[9] = fmaf(cr, fr, acc[9]);
-        acc[10] = fmaf(cr, fc, acc[10]);
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            const float cs = (KS == 1 || sl == k) ? cr : 0.f;
+            acc[k][9] = fmaf(cs, fr, acc[k][9]);
+            acc[k][10] = fmaf(cs, fc, acc[k][10]);
+        }
     }
 }
 
@@ -502,7 +513,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                                                         float* __restrict__ gshift = nullptr,
                                                         const float* __restrict__ gw = nullptr,
                                                         float* __restrict__ wout = nullptr) {
-    static_assert(GMODE == 0 || KP == 1, "the gradient modes sum one pose per wave batch");
+    static_assert(GMODE == 0 || KP <= 2, "the gradient modes keep a set of sums per pose of a wave batch");
     static_assert(GMODE != 2 || std::is_same<VS, float>::value, "complex-half volumes: forward and its gradients only");
     constexpr bool GRADS = GMODE == 1 || (GMODE == 2 && RS);
     constexpr int WW = (GMODE == 2 && WG) ? (L + 1) * (L + 1) * (LD + 1) : 1;  // trilinear weight taps
@@ -655,9 +666,12 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                     sd.base = (b * g.P + pp) * int64_t(g.npix);
                 }
                 __builtin_amdgcn_wave_barrier();
-                float acc[11];  // GMODE 1: this lane's share of the pose's 9 rotation and 2 shift sums
+                constexpr int KS = GRADS ? KP : 1;
+                float acc[KS][11];  // gradient modes: this lane's share of each slot's 9 rotation and 2 shift sums
 #pragma unroll
-                for (int k = 0; k < 11; ++k) acc[k] = 0.f;
+                for (int s2 = 0; s2 < KS; ++s2)
+#pragma unroll
+                    for (int k = 0; k < 11; ++k) acc[s2][k] = 0.f;
                 int r0, r1;
                 box_rows<GEN>(R, lo, hi, ts, r0, r1);
                 const int nr = sv ? max(0, r1 - r0 + 1) : 0;
@@ -741,7 +755,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                                 // (grad_terms: the sums take (c, r), the pose's totals the constants)
                                 Cx<float> pv = gsrc[pidx];
                                 if (shifts) pv = cmul(pv, cconj(ph));
-                                grad_terms(ip, pv, pv, ip.v, fr, fc, grot != nullptr, gshift != nullptr, acc);
+                                grad_terms<KS>(ip, pv, pv, ip.v, fr, fc, grot != nullptr, gshift != nullptr, sl, acc);
                             }
                         } else {
                             const Interp<float> ip = CUBIC ? cubic3_grads<false>(lds, x[2], x[1], x[0])
@@ -753,29 +767,34 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                             // g against -i 2 pi k / n * (F * phase)
                             const Cx<float> gg = shifts ? cmul(g0, cconj(ph)) : g0;
                             const Cx<float> mod = shifts ? cmul(ip.v, ph) : ip.v;
-                            grad_terms(ip, gg, g0, mod, fr, fc, grot != nullptr, gshift != nullptr, acc);
+                            grad_terms<KS>(ip, gg, g0, mod, fr, fc, grot != nullptr, gshift != nullptr, sl, acc);
                         }
                       }
                     }
                 }
                 if constexpr (GRADS) {
-                    // the pose's sums (every lane of the wave takes part; one adds them)
-                    if (grot) {
-                        const float os = float(g.os);
+                    // each slot's sums (every lane of the wave takes part; the slot's first lane, which
+                    // holds its pose, adds them)
 #pragma unroll
-                        for (int row = 0; row < 3; ++row)
+                    for (int s2 = 0; s2 < KS; ++s2) {
+                        const bool mine = lane == s2 * RPS && sv;
+                        if (grot) {
+                            const float os = float(g.os);
 #pragma unroll
-                            for (int k = 0; k < 2; ++k) {
-                                const float t = wave_sum(acc[row * 3 + k]) * os;
-                                if (lane == 0 && sv) atomic_add(&grot[(rb * g.P + pp) * 9 + row * 3 + k], t);
+                            for (int row = 0; row < 3; ++row)
+#pragma unroll
+                                for (int k = 0; k < 2; ++k) {
+                                    const float t = wave_sum(acc[s2][row * 3 + k]) * os;
+                                    if (mine) atomic_add(&grot[(rb * g.P + pp) * 9 + row * 3 + k], t);
+                                }
+                        }
+                        if (gshift) {
+                            const float kn = float(-kTwoPi / double(g.n));
+                            const float t0 = wave_sum(acc[s2][9]) * kn, t1 = wave_sum(acc[s2][10]) * kn;
+                            if (mine) {
+                                atomic_add(&gshift[(sb * g.P + pp) * 2], t0);
+                                atomic_add(&gshift[(sb * g.P + pp) * 2 + 1], t1);
                             }
-                    }
-                    if (gshift) {
-                        const float kn = float(-kTwoPi / double(g.n));
-                        const float t0 = wave_sum(acc[9]) * kn, t1 = wave_sum(acc[10]) * kn;
-                        if (lane == 0 && sv) {
-                            atomic_add(&gshift[(sb * g.P + pp) * 2], t0);
-                            atomic_add(&gshift[(sb * g.P + pp) * 2 + 1], t1);
                         }
                     }
                 }
@@ -1424,7 +1443,7 @@ hipError_t launch_grads3_tiled(bool cubic, const Geom& g, const TileSpec& ts, co
                                hipStream_t s, bool rec_half) {
     if (!grot && !gshift) return hipSuccess;
 #define TP_GRADS(C, O, V) \
-    forw_both<C, 1, O, 1, true, false, V>(g, ts, rec, rot, shifts, nullptr, cp, gl, gproj, grot, gshift, nullptr, \
+    forw_both<C, 2, O, 1, true, false, V>(g, ts, rec, rot, shifts, nullptr, cp, gl, gproj, grot, gshift, nullptr, \
                                           nullptr, s)
     if (rec_half) {
         if (cubic) return ts.os_exact ? TP_GRADS(true, true, __half) : TP_GRADS(true, false, __half);
