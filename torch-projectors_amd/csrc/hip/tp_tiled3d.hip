@@ -513,7 +513,8 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                                                         float* __restrict__ gshift = nullptr,
                                                         const float* __restrict__ gw = nullptr,
                                                         float* __restrict__ wout = nullptr) {
-    static_assert(GMODE == 0 || KP <= 2, "the gradient modes keep a set of sums per pose of a wave batch");
+    static_assert(!(GMODE == 1 || (GMODE == 2 && RS)) || KP <= 2,
+                  "the gradient modes keep a set of sums per pose of a wave batch");
     static_assert(GMODE != 2 || std::is_same<VS, float>::value, "complex-half volumes: forward and its gradients only");
     constexpr bool GRADS = GMODE == 1 || (GMODE == 2 && RS);
     constexpr int WW = (GMODE == 2 && WG) ? (L + 1) * (L + 1) * (LD + 1) : 1;  // trilinear weight taps
@@ -1384,16 +1385,20 @@ template <bool CUBIC, bool OSX>
 hipError_t bpback_flags(const Geom& g, const TileSpec& ts, const void* gdata, const void* gw, const void* proj,
                         const void* rot, const void* shifts, void* gproj, void* gweights, void* grot, void* gshift,
                         CallPoses* cp, int gl, hipStream_t s) {
+    // poses per wave batch: the forward's count, at most two with gradient sums (a set per pose)
     const bool rs = grot || gshift, wg = gw && gweights;
-    if (rs)
-        return wg ? forw_both<CUBIC, 1, OSX, 2, true, true, float>(g, ts, gdata, rot, shifts, gproj, cp, gl, proj, grot,
-                                                                   gshift, gw, gweights, s)
-                  : forw_both<CUBIC, 1, OSX, 2, true, false, float>(g, ts, gdata, rot, shifts, gproj, cp, gl, proj,
-                                                                    grot, gshift, gw, nullptr, s);
-    return wg ? forw_both<CUBIC, 1, OSX, 2, false, true, float>(g, ts, gdata, rot, shifts, gproj, cp, gl, proj, grot,
-                                                                gshift, gw, gweights, s)
-              : forw_both<CUBIC, 1, OSX, 2, false, false, float>(g, ts, gdata, rot, shifts, gproj, cp, gl, proj, grot,
-                                                                 gshift, gw, nullptr, s);
+    const int kp = ts.kp_forw >= 4 ? 4 : (ts.kp_forw == 2 ? 2 : 1);
+#define TP_BPB(KPV, RSV, WGV)                                                                                   \
+    forw_both<CUBIC, KPV, OSX, 2, RSV, WGV, float>(g, ts, gdata, rot, shifts, gproj, cp, gl, proj, grot, gshift, gw, \
+                                                   WGV ? gweights : nullptr, s)
+    if (rs) {
+        if (kp >= 2) return wg ? TP_BPB(2, true, true) : TP_BPB(2, true, false);
+        return wg ? TP_BPB(1, true, true) : TP_BPB(1, true, false);
+    }
+    if (kp == 4) return wg ? TP_BPB(4, false, true) : TP_BPB(4, false, false);
+    if (kp == 2) return wg ? TP_BPB(2, false, true) : TP_BPB(2, false, false);
+    return wg ? TP_BPB(1, false, true) : TP_BPB(1, false, false);
+#undef TP_BPB
 }
 
 template <bool CUBIC, bool OSX, typename VS>
