@@ -6,6 +6,10 @@ neither wait nor allocate) and runs without bins.  Every replay, with eager work
 synchronisations between replays and new pose values written into the captured input, is compared
 with eager calls of the same ops: forward projections bit for bit (they do not depend on the bins),
 the backprojected volumes within relative L2 1e-5 (they differ only in the order of the fp64 sums).
+
+The second test captures calls that do use the stream's pose bins (the warm-up had as many poses),
+then grows that workspace with an eager call of twice the poses on the same stream: the replays
+must still read the workspace the capture recorded, which stays allocated.
 """
 import pytest
 import torch
@@ -68,3 +72,45 @@ def test_forward_and_backprojection_replayed(gpu):
         assert torch.equal(proj_g, proj_e), f"replay {replay}: projections differ"
         assert _rel(data_g, data_e) <= 1e-5, f"replay {replay}: data volume {_rel(data_g, data_e):.3e}"
         assert _rel(wrec_g, wrec_e) <= 1e-5, f"replay {replay}: weight volume {_rel(wrec_g, wrec_e):.3e}"
+
+
+def test_replay_after_the_bin_workspace_grew(gpu):
+    T = torch.ops.torch_projectors
+    gen = torch.Generator().manual_seed(8090)
+    P, n, os_, N = 48, 32, 2.0, 64
+    vol = torch.randn(1, N, N, N // 2 + 1, generator=gen, dtype=torch.complex64).to(gpu)
+    rot = _rotations(2 * P, gen).to(gpu)
+    sh = (torch.rand(1, 2 * P, 2, generator=gen) * 4 - 2).to(gpu)
+    w = torch.rand(1, 2 * P, n, n // 2 + 1, generator=gen).to(gpu)
+    proj = T.project_3d_to_2d_forw(vol, rot, sh, [n, n], "linear", os_, None)
+    r1, s1, p1, w1 = (t[:, :P].contiguous() for t in (rot, sh, proj, w))
+
+    def bp(p, ww, r, s):
+        return T.backproject_2d_to_3d_forw(p, ww, r, s, "linear", os_, None)
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        bp(p1, w1, r1, s1)  # the stream's scratch, with a pose-bin workspace for P poses
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        data_g, wrec_g = bp(p1, w1, r1, s1)  # fits the workspace: the captured calls use the bins
+    torch.cuda.synchronize()
+
+    with torch.cuda.stream(stream):
+        bp(proj, w, rot, sh)  # twice the poses: the workspace grows
+    torch.cuda.synchronize()
+    data_e, wrec_e = bp(p1, w1, r1, s1)
+    torch.cuda.synchronize()
+    for replay in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"[graph] replay {replay} after growth", flush=True)
+        assert _rel(data_g, data_e) <= 1e-5, f"replay {replay}: data volume {_rel(data_g, data_e):.3e}"
+        assert _rel(wrec_g, wrec_e) <= 1e-5, f"replay {replay}: weight volume {_rel(wrec_g, wrec_e):.3e}"
+        with torch.cuda.stream(stream):
+            bp(proj, w, rot, sh)  # eager work on the capture stream between replays
+        torch.cuda.synchronize()

@@ -16,6 +16,7 @@
 #include <mutex>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "../../../include/torch_projectors_hip.h"
 #include "tp_launch.hh"
@@ -285,6 +286,11 @@ struct StreamScratch {
     std::mutex busy;
     void* bins = nullptr;  // pose-bin workspace of the tiled 3D kernels, grown on demand
     size_t bins_cap = 0;
+    // A graph captured on the stream keeps the address of the workspace its calls used, so a
+    // workspace that a capture has used is never freed: growing it retires it instead (kept
+    // until the process ends; growth is geometric, so these stay a small multiple of the last).
+    bool bins_captured = false;
+    std::vector<void*> bins_retired;
 };
 std::mutex g_scratch_mu;
 std::map<std::pair<int, hipStream_t>, std::unique_ptr<StreamScratch>> g_scratch;
@@ -347,17 +353,24 @@ struct CallScratch {
     // A pose-bin workspace of `need` bytes on the call's stream, or nullptr: the static area has
     // none, and a failed allocation leaves the call without bins (the kernels then cull every pose).
     // Growing waits for the stream's queued work, which may still read the old workspace; a stream
-    // under graph capture can neither wait nor allocate, so there the call goes without bins.
+    // under graph capture can neither wait nor allocate, so there the call goes without bins, and
+    // a workspace that a captured call uses is retired rather than freed when it grows later.
     void* bins(size_t need, hipStream_t st) {
         if (static_area || !area) return nullptr;
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+            hipGetLastError();
+            return nullptr;
+        }
+        const bool capturing = cs != hipStreamCaptureStatusNone;
         if (need > area->bins_cap) {
-            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-            if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
-                hipGetLastError();
-                return nullptr;
-            }
+            if (capturing) return nullptr;
             if (hipStreamSynchronize(st) != hipSuccess) return nullptr;
-            if (area->bins) hipFree(area->bins);
+            if (area->bins) {
+                if (area->bins_captured) area->bins_retired.push_back(area->bins);
+                else hipFree(area->bins);
+            }
+            area->bins_captured = false;
             area->bins = nullptr;
             area->bins_cap = 0;
             const size_t cap = need + need / 4;
@@ -368,6 +381,7 @@ struct CallScratch {
             }
             area->bins_cap = cap;
         }
+        if (capturing) area->bins_captured = true;
         return area->bins;
     }
     int get(hipStream_t st) {
