@@ -114,3 +114,38 @@ def test_replay_after_the_bin_workspace_grew(gpu):
         with torch.cuda.stream(stream):
             bp(proj, w, rot, sh)  # eager work on the capture stream between replays
         torch.cuda.synchronize()
+
+
+def test_fourier_transforms_replayed_after_plan_eviction(gpu):
+    """hipFFT transforms captured after one eager call of their shape on the capture stream, then
+    replayed after more distinct shapes on that stream than the plan cache holds (32): the plans a
+    graph uses are never evicted, so every replay matches an eager transform."""
+    from torch_projectors import fourier as FM
+    gen = torch.Generator().manual_seed(8100)
+    x = torch.randn(2, 32, 32, 32, generator=gen).to(gpu)
+    others = [torch.randn(b, 8, 8, generator=gen).to(gpu) for b in range(1, 41)]
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        FM._irfftn_consuming(FM._rfftn(x, 3), 3)  # the stream's plans of both shapes
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        spec_g = FM._rfftn(x, 3)
+        back_g = FM._irfftn_consuming(spec_g.clone(), 3)
+    torch.cuda.synchronize()
+
+    spec_e = FM._rfftn(x, 3)
+    back_e = FM._irfftn_consuming(spec_e.clone(), 3)
+    torch.cuda.synchronize()
+    for replay in range(3):
+        with torch.cuda.stream(stream):
+            for t in others:  # eager transforms on the capture stream: the cache evicts its other plans
+                FM._rfftn(t, 2)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"[graph] fourier replay {replay}", flush=True)
+        assert _rel(spec_g, spec_e) <= 1e-6, f"replay {replay}: spectrum {_rel(spec_g, spec_e):.3e}"
+        assert _rel(back_g, back_e) <= 1e-6, f"replay {replay}: inverse {_rel(back_g, back_e):.3e}"

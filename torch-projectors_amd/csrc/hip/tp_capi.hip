@@ -851,6 +851,9 @@ int tp_rfftn(int dtype, int dim, int64_t batch, int64_t boxsize, const void* rea
     TP_TRY(need(real, "real"));
     TP_TRY(need(spectrum, "spectrum"));
     const int r = tp::fft_forward(dtype, dim, batch, boxsize, real, spectrum, static_cast<hipStream_t>(stream));
+    if (r == tp::kFftNoPlanUnderCapture)
+        return fail("the first transform of this shape on a stream makes its hipFFT plan, which graph capture "
+                    "forbids: run it once on that stream before capturing");
     if (r != 0) {
         g_err = "hipFFT forward transform failed (hipfftResult " + std::to_string(r) + ")";
         return TP_ERR_HIP;
@@ -868,6 +871,9 @@ int tp_irfftn(int dtype, int dim, int64_t batch, int64_t boxsize, void* spectrum
     TP_TRY(need(spectrum, "spectrum"));
     TP_TRY(need(real, "real"));
     const int r = tp::fft_inverse(dtype, dim, batch, boxsize, spectrum, real, static_cast<hipStream_t>(stream));
+    if (r == tp::kFftNoPlanUnderCapture)
+        return fail("the first transform of this shape on a stream makes its hipFFT plan, which graph capture "
+                    "forbids: run it once on that stream before capturing");
     if (r != 0) {
         g_err = "hipFFT inverse transform failed (hipfftResult " + std::to_string(r) + ")";
         return TP_ERR_HIP;

@@ -206,13 +206,17 @@ hipError_t launch_ifftshift_crop(int elem_bytes, int dim, const void* src, int64
 // once on the GPU never share one; calls on one stream run in order.  The
 // cache holds at most kMaxPlans plans: the least recently used one is
 // destroyed after its device has finished all queued work (its transforms may
-// still be running).  The cache lock serialises the enqueues.
+// still be running).  A plan that a graph capture used is never destroyed (the
+// graph keeps its work area), and no plan is made on a capturing stream (that
+// allocates): such a call fails with kFftNoPlanUnderCapture.  The cache lock
+// serialises the enqueues.
 namespace {
 
 using PlanKey = std::tuple<int, int, int, int64_t, int64_t, int, hipStream_t>;
 struct PlanEntry {
     hipfftHandle h;
-    uint64_t used;  // tick of the last call
+    uint64_t used;   // tick of the last call
+    bool captured;   // used by a call under graph capture: kept until the process ends
 };
 constexpr size_t kMaxPlans = 32;
 std::mutex g_fft_mu;
@@ -220,9 +224,10 @@ std::map<PlanKey, PlanEntry> g_plans;
 uint64_t g_fft_tick = 0;
 
 hipfftResult evict_oldest_plan() {
-    auto old = g_plans.begin();
+    auto old = g_plans.end();
     for (auto it = g_plans.begin(); it != g_plans.end(); ++it)
-        if (it->second.used < old->second.used) old = it;
+        if (!it->second.captured && (old == g_plans.end() || it->second.used < old->second.used)) old = it;
+    if (old == g_plans.end()) return HIPFFT_SUCCESS;  // every plan is held by a graph: the cache grows
     int cur = 0;
     if (hipGetDevice(&cur) != hipSuccess) return HIPFFT_INTERNAL_ERROR;
     const int dev = std::get<5>(old->first);
@@ -236,16 +241,21 @@ hipfftResult evict_oldest_plan() {
     return r;
 }
 
-hipfftResult plan_for(bool forward, int dt, int dim, int64_t N, int64_t batch, hipStream_t s, hipfftHandle& out) {
+int plan_for(bool forward, int dt, int dim, int64_t N, int64_t batch, hipStream_t s, hipfftHandle& out) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return HIPFFT_INTERNAL_ERROR;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess) return HIPFFT_INTERNAL_ERROR;
+    const bool capturing = cs != hipStreamCaptureStatusNone;
     const PlanKey key{forward ? 1 : 0, dt, dim, N, batch, dev, s};
     auto it = g_plans.find(key);
     if (it != g_plans.end()) {
         it->second.used = ++g_fft_tick;
+        it->second.captured |= capturing;
         out = it->second.h;
         return HIPFFT_SUCCESS;
     }
+    if (capturing) return kFftNoPlanUnderCapture;
     if (g_plans.size() >= kMaxPlans) {
         const hipfftResult e = evict_oldest_plan();
         if (e != HIPFFT_SUCCESS) return e;
@@ -268,7 +278,7 @@ hipfftResult plan_for(bool forward, int dt, int dim, int64_t N, int64_t batch, h
         hipfftDestroy(h);
         return r;
     }
-    g_plans.emplace(key, PlanEntry{h, ++g_fft_tick});
+    g_plans.emplace(key, PlanEntry{h, ++g_fft_tick, false});
     out = h;
     return HIPFFT_SUCCESS;
 }
@@ -278,8 +288,8 @@ hipfftResult plan_for(bool forward, int dt, int dim, int64_t N, int64_t batch, h
 int fft_forward(int dt, int dim, int64_t batch, int64_t N, const void* real, void* spec, hipStream_t s) {
     std::lock_guard<std::mutex> lock(g_fft_mu);
     hipfftHandle h;
-    const hipfftResult r = plan_for(true, dt, dim, N, batch, s, h);
-    if (r != HIPFFT_SUCCESS) return int(r);
+    const int r = plan_for(true, dt, dim, N, batch, s, h);
+    if (r != HIPFFT_SUCCESS) return r;
     // out-of-place real-to-complex transforms leave their input intact
     if (dt == 0) return int(hipfftExecR2C(h, (hipfftReal*)real, (hipfftComplex*)spec));
     return int(hipfftExecD2Z(h, (hipfftDoubleReal*)real, (hipfftDoubleComplex*)spec));
@@ -288,8 +298,8 @@ int fft_forward(int dt, int dim, int64_t batch, int64_t N, const void* real, voi
 int fft_inverse(int dt, int dim, int64_t batch, int64_t N, void* spec, void* real, hipStream_t s) {
     std::lock_guard<std::mutex> lock(g_fft_mu);
     hipfftHandle h;
-    const hipfftResult r = plan_for(false, dt, dim, N, batch, s, h);
-    if (r != HIPFFT_SUCCESS) return int(r);
+    const int r = plan_for(false, dt, dim, N, batch, s, h);
+    if (r != HIPFFT_SUCCESS) return r;
     if (dt == 0) return int(hipfftExecC2R(h, (hipfftComplex*)spec, (hipfftReal*)real));
     return int(hipfftExecZ2D(h, (hipfftDoubleComplex*)spec, (hipfftDoubleReal*)real));
 }

@@ -215,6 +215,9 @@ hipError_t launch_normalize(int dt, const void* data, const void* weights, int64
 // rfftn / irfftn (norm="forward") of `batch` contiguous N^dim boxes through
 // hipFFT (rocFFT), with cached plans; return a hipfftResult (0 = success).
 // The inverse overwrites its input.
+// fft_forward / fft_inverse return a hipfftResult, or kFftNoPlanUnderCapture: the stream is under
+// graph capture and has no plan of this shape yet (making one allocates).
+constexpr int kFftNoPlanUnderCapture = -1;
 int fft_forward(int dt, int dim, int64_t batch, int64_t N, const void* real, void* spec, hipStream_t s);
 int fft_inverse(int dt, int dim, int64_t batch, int64_t N, void* spec, void* real, hipStream_t s);
 
