@@ -824,15 +824,26 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
                         const int rr = __shfl(r, lw, 64);
                         const int cc = __shfl(c0, lw, 64) + (e - __shfl(excl, lw, 64));
                         if (e >= total) continue;
-                        const Slot2& sd = slots[wave][lw / RPS];
+                        // every field of the sample's pose slot is read before the tests, so that the
+                        // reads go out together (one LDS round trip) instead of one per test
+                        const Slot2& sdl = slots[wave][lw / RPS];
+                        Slot2 sd;
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) sd.R[k] = sdl.R[k];
+                        sd.s0 = sdl.s0;
+                        sd.s1 = sdl.s1;
+                        sd.p = sdl.p;
                         const float fr = float(rr), fc = float(cc);
-                        if (filtered(fr, fc, cut2)) continue;
-                        // the backward ops skip the Friedel half of the x = 0 line
-                        if (GMODE != 0 && cc == 0 && (rr == g.n / 2 || rr < 0)) continue;
                         float x[2];
                         rotate_pix(sd.R, fr, fc, g.os, x);
                         const int fxc = int(floorf(x[0])), fxr = int(floorf(x[1]));
-                        if (fxc < tc || fxc >= tc + GC || fxr < tr || fxr >= tr + GR) continue;
+                        // outside the cutoff, the Friedel half of the x = 0 line (the backward ops skip
+                        // it), or not owned by this tile
+                        bool skip = filtered(fr, fc, cut2);
+                        if (GMODE != 0) skip |= cc == 0 & (rr == g.n / 2 | rr < 0);
+                        skip |= (fxc < tc) | (fxc >= tc + GC) | (fxr < tr) | (fxr >= tr + GR);
+                        asm volatile("" ::"v"(sd.s0), "v"(sd.s1), "v"(sd.p));
+                        if (skip) continue;
                         const int i = rr >= 0 ? rr : rr + g.n;
                         const int64_t pidx = (pose0 + sd.p) * int64_t(g.npix) + i * g.hp + cc;
                         Interp<float> ip;

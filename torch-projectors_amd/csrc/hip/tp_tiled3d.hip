@@ -696,16 +696,26 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                         if (e0 + lane >= m) continue;
                         int rr, cc, sl;
                         q_unpack(queue[wave][e0 + lane], rr, cc, sl);
-                        const Slot& sd = slots[wave][sl];
+                        // every field of the sample's pose slot is read before the tests, so that the
+                        // reads go out together (one LDS round trip) instead of one per test
+                        const Slot& sdl = slots[wave][sl];
+                        Slot sd;
+#pragma unroll
+                        for (int e = 0; e < 9; ++e) sd.R[e] = (e % 3 == 2) ? 0.f : sdl.R[e];
+                        sd.s0 = sdl.s0;
+                        sd.s1 = sdl.s1;
+                        sd.base = sdl.base;
                         const float fr = float(rr), fc = float(cc);
-                        if (filtered(fr, fc, cut2)) continue;
-                        // the backward ops skip the Friedel half of the x = 0 line
-                        if (GMODE != 0 && cc == 0 && (rr == g.n / 2 || rr < 0)) continue;
                         float x[3];
                         rotate_slice<OSX>(sd.R, fr, fc, g.os, x);
                         const int fxc = int(floorf(x[0])), fxr = int(floorf(x[1])), fxd = int(floorf(x[2]));
-                        if (fxc < tc || fxc >= tc + L || fxr < tr || fxr >= tr + L || fxd < td || fxd >= td + LD)
-                            continue;
+                        // outside the cutoff, the Friedel half of the x = 0 line (the backward ops skip
+                        // it), or not owned by this tile
+                        bool skip = filtered(fr, fc, cut2);
+                        if (GMODE != 0) skip |= cc == 0 & (rr == g.n / 2 | rr < 0);
+                        skip |= (fxc < tc) | (fxc >= tc + L) | (fxr < tr) | (fxr >= tr + L) | (fxd < td) | (fxd >= td + LD);
+                        asm volatile("" ::"v"(sd.s0), "v"(sd.s1), "v"(int(sd.base)), "v"(int(sd.base >> 32)));
+                        if (skip) continue;
                         // staged cell of the tap at floor(x); the interpolation reads its taps at
                         // constant offsets from it (the interpolators split x the same way)
                         const unsigned eb = __umul24(__umul24(unsigned(fxd - (td - LO)), unsigned(W)) + unsigned(fxr - (tr - LO)),
