@@ -359,7 +359,7 @@ struct CallScratch {
         if (static_area || !area) return nullptr;
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
-            hipGetLastError();
+            (void)hipGetLastError();
             return nullptr;
         }
         const bool capturing = cs != hipStreamCaptureStatusNone;
@@ -368,7 +368,7 @@ struct CallScratch {
             if (hipStreamSynchronize(st) != hipSuccess) return nullptr;
             if (area->bins) {
                 if (area->bins_captured) area->bins_retired.push_back(area->bins);
-                else hipFree(area->bins);
+                else (void)hipFree(area->bins);
             }
             area->bins_captured = false;
             area->bins = nullptr;
@@ -376,7 +376,7 @@ struct CallScratch {
             const size_t cap = need + need / 4;
             if (hipMalloc(&area->bins, cap) != hipSuccess) {
                 area->bins = nullptr;
-                hipGetLastError();  // clear the allocation error
+                (void)hipGetLastError();  // clear the allocation error
                 return nullptr;
             }
             area->bins_cap = cap;

@@ -232,7 +232,7 @@ hipfftResult evict_oldest_plan() {
     if (hipGetDevice(&cur) != hipSuccess) return HIPFFT_INTERNAL_ERROR;
     const int dev = std::get<5>(old->first);
     if (hipSetDevice(dev) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
-        hipSetDevice(cur);
+        (void)hipSetDevice(cur);
         return HIPFFT_INTERNAL_ERROR;
     }
     const hipfftResult r = hipfftDestroy(old->second.h);

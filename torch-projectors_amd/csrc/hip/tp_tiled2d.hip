@@ -193,7 +193,7 @@ template <bool CUBIC, int MODE, bool WEIGHTS>
 __device__ __forceinline__ void scatter_sample2(const Geom& g, const Slot2& sd, int rr, int cc, Cx<float> v,
                                                 float wpix, bool shifted, bool flip, const TapMap2& tm,
                                                 double* acc_re, double* acc_im, double* acc_w) {
-    constexpr int K = CUBIC ? 4 : 2, LOW = CUBIC ? 1 : 0;
+    constexpr int K = CUBIC ? 4 : 2;
     const float fr = float(rr), fc = float(cc);
     float x[2];
     rotate_pix(sd.R, fr, fc, g.os, x);
@@ -840,7 +840,7 @@ __global__ __launch_bounds__(kThreads) void k_gather2_tiled(Geom g, TileSpec2 ts
                         // outside the cutoff, the Friedel half of the x = 0 line (the backward ops skip
                         // it), or not owned by this tile
                         bool skip = filtered(fr, fc, cut2);
-                        if (GMODE != 0) skip |= cc == 0 & (rr == g.n / 2 | rr < 0);
+                        if (GMODE != 0) skip |= (cc == 0) & ((rr == g.n / 2) | (rr < 0));
                         skip |= (fxc < tc) | (fxc >= tc + GC) | (fxr < tr) | (fxr >= tr + GR);
                         asm volatile("" ::"v"(sd.s0), "v"(sd.s1), "v"(sd.p));
                         if (skip) continue;

@@ -172,7 +172,7 @@ __device__ __forceinline__ void rotate_slice(const float* __restrict__ R, float 
 // column c0 at flattened index `excl`; entries [q0, q0 + QCAP) are written.
 constexpr unsigned kQRowBias = 0x8000u;  // r + bias in bits 0-15, c in bits 16-29, slot in 30-31
 __device__ __forceinline__ unsigned q_pack(int r, int c, int slot) {
-    return (unsigned(r) + kQRowBias) & 0xffffu | (unsigned(c) << 16) | (unsigned(slot) << 30);
+    return ((unsigned(r) + kQRowBias) & 0xffffu) | (unsigned(c) << 16) | (unsigned(slot) << 30);
 }
 __device__ __forceinline__ void q_unpack(unsigned e, int& r, int& c, int& slot) {
     r = int(e & 0xffffu) - int(kQRowBias);
@@ -712,7 +712,7 @@ __global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec t
                         // outside the cutoff, the Friedel half of the x = 0 line (the backward ops skip
                         // it), or not owned by this tile
                         bool skip = filtered(fr, fc, cut2);
-                        if (GMODE != 0) skip |= cc == 0 & (rr == g.n / 2 | rr < 0);
+                        if (GMODE != 0) skip |= (cc == 0) & ((rr == g.n / 2) | (rr < 0));
                         skip |= (fxc < tc) | (fxc >= tc + L) | (fxr < tr) | (fxr >= tr + L) | (fxd < td) | (fxd >= td + LD);
                         asm volatile("" ::"v"(sd.s0), "v"(sd.s1), "v"(int(sd.base)), "v"(int(sd.base >> 32)));
                         if (skip) continue;
@@ -863,7 +863,7 @@ template <bool CUBIC, int MODE, bool WEIGHTS, bool OSX>
 __device__ __forceinline__ void scatter_sample(const Geom& g, const ScSlot& sd, int rr, int cc, Cx<float> v,
                                                float wpix, bool shifted, bool flip, const TapMap& tm,
                                                double* acc_re, double* acc_im, double* acc_w) {
-    constexpr int K = CUBIC ? 4 : 2, LOW = CUBIC ? 1 : 0;  // taps at floor(x) - LOW + j, j < K
+    constexpr int K = CUBIC ? 4 : 2;  // taps at floor(x) - (CUBIC ? 1 : 0) + j, j < K
     const float fr = float(rr), fc = float(cc);
     float x[3];
     rotate_slice6<OSX>(sd.R6, fr, fc, g.os, x);
