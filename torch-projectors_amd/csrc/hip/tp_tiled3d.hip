@@ -24,7 +24,7 @@
 //   k_scatter3_tiled  backprojection (data + weights) and the reconstruction
 //                     gradient of the projection backward.  Contributions are
 //                     accumulated in fp64 LDS (gfx950's LDS fp32 atomic add
-//                     runs at ~0.3 lanes/clk/CU, fp64 at ~2.6) and every
+//                     runs at ~0.3 lanes/clk/CU, fp64 at ~7.7) and every
 //                     stored cell of the tile is written once with a plain
 //                     store: no zero fill and no global atomics, except for
 //                     the split core tiles, which add their partial tiles
@@ -502,9 +502,18 @@ __device__ __forceinline__ void grad_terms(const Interp<float>& ip, Cx<float> a,
     }
 }
 
+// Waves per SIMD the forward is compiled for: the linear forward of a complex-half volume fits five
+// workgroups per CU in LDS, which its registers must allow too (96 VGPRs, for rotation poses; the
+// other poses' instantiation would spill there); the others (1: no target) are limited to four
+// workgroups or fewer by LDS or registers anyway.
+template <bool CUBIC, int GMODE, typename VS, bool GEN>
+constexpr int forw_waves_per_eu() {
+    return (!CUBIC && GMODE == 0 && kHalfVolume<VS> && !GEN) ? 5 : 1;
+}
 template <bool CUBIC, int KP, bool OSX, int GMODE = 0, bool RS = true, bool WG = false, typename VS = float,
           bool GEN = false>
-__global__ __launch_bounds__(kForwThreads) void k_forw3_tiled(Geom g, TileSpec ts, const Cx<VS>* __restrict__ rec,
+__global__ __launch_bounds__(kForwThreads)
+__attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>()))) void k_forw3_tiled(Geom g, TileSpec ts, const Cx<VS>* __restrict__ rec,
                                                         const float* __restrict__ rot,
                                                         const float* __restrict__ shifts,
                                                         Cx<float>* __restrict__ out, CallPoses* __restrict__ cp,
