@@ -55,6 +55,25 @@ def binned_cases():
     return out
 
 
+def odd_cases():
+    """Odd projection sizes n (rows i <= n // 2 are frequencies 0..m, the others -m..-1 for
+    n = 2m + 1: one more negative row than an even size has), every op, both interpolations, with
+    and without a cutoff, every other case's pose matrices scaled."""
+    rng = random.Random(6060)
+    out = []
+    seed = 6060
+    for op in OPS:
+        for interp in ("linear", "cubic"):
+            seed += 1
+            n = rng.choice([9, 15, 21, 33])
+            c = _case(f"odd_{op}_{interp}_n{n}", op, interp=interp, os=rng.choice([1.0, 1.5, 2.0]),
+                      cutoff=rng.choice([None, round(rng.uniform(2.0, n / 2), 3)]), B=2, P=5, n=n,
+                      B_rot=rng.choice([1, 2]), seed=seed)
+            c["scaled"] = interp == "cubic"
+            out.append(c)
+    return out
+
+
 def scale_poses(args, case):
     """Scale every other pose matrix by 1.05 (a matrix that is not a rotation)."""
     idx = {"project_3d_to_2d_forw": 1, "project_2d_forw": 1, "project_3d_to_2d_back": 2, "project_2d_back": 2,
