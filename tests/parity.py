@@ -6,7 +6,8 @@ grad_weights gathers of the backprojection backward) within relative L2
 (same stencil indices, Friedel/clamp decisions, per-tap products and
 summation order); scatters (data/weight volumes, reconstruction gradients)
 and per-pose rotation/shift gradients, whose float-atomic or reduction
-order differs, within relative L2 1e-4.  fp64 runs use 1e-12 / 1e-10.
+order differs, within relative L2 1e-4 (scatter volumes with fp32 inputs:
+of the exact sum of the reference's taps, below).  fp64 runs use 1e-12 / 1e-10.
 
 Scatter volumes are also checked cell by cell (`check_cells`) against the
 exact sum of the reference's fp32 tap values (oracle.scatter_wide: the
@@ -152,7 +153,11 @@ def check_outputs(op, got, expected, has_shifts, label="", cells=None):
                                      f"max |d| = {d:.3e}")
             continue
         tol = (GATHER_TOL if gather else SCATTER_TOL)[real_dtype(e)]
-        err = rel_l2(g, e)
+        # a scatter volume with fp32 inputs is compared with the exact sum of the reference's taps:
+        # the oracle's own fp32 sum, in one order as the reference's atomics, departs from it with
+        # the number of contributions per cell (2.2e-4 rel-L2 for 66000 poses of unit-range weights)
+        exact = cells[k][2] if (cells and k in cells and not gather) else None
+        err = rel_l2(g, e if exact is None else exact)
         assert err <= tol, f"{label} output {k}: relative L2 {err:.3e} > {tol:.0e}"
         if cells and k in cells:
             U, vmax, exact = cells[k]

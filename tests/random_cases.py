@@ -55,6 +55,22 @@ def binned_cases():
     return out
 
 
+def many_pose_cases():
+    """66000 poses in one call (small projections): past the 65536 poses from which the 3D scatters
+    go without pose bins (their list entries are 16-bit) and past any 16-bit pose index, in the
+    forward, both 3D scatters and the 2D scatter."""
+    out = []
+    seed = 7070
+    for op, interp in (("project_3d_to_2d_forw", "linear"), ("backproject_2d_to_3d_forw", "linear"),
+                       ("backproject_2d_to_3d_forw", "cubic"), ("project_3d_to_2d_back", "linear"),
+                       ("backproject_2d_forw", "linear")):
+        seed += 1
+        out.append(_case(f"many_{op}_{interp}", op, interp=interp, os=2.0, B=1, P=66000, n=8, seed=seed,
+                         rg_rot=False, rg_sh=False))
+        out[-1]["scaled"] = False
+    return out
+
+
 def odd_cases():
     """Odd projection sizes n (rows i <= n // 2 are frequencies 0..m, the others -m..-1 for
     n = 2m + 1: one more negative row than an even size has), every op, both interpolations, with

@@ -4,19 +4,21 @@ The same seeded configuration generator as tests/test_oracle_ref_random.py
 (where the oracle is pinned bit for bit to the reference's compiled CPU
 kernels), plus empty pose sets and cutoffs of +inf, NaN and beyond any int
 (the tiled kernels cap each row's columns by the disc only where that cap is
-a finite int), and 3D scatters with enough poses for the per-call pose bins.
+a finite int), 3D scatters with enough poses for the per-call pose bins, odd projection
+sizes, and calls of 66000 poses (past the bins' 16-bit lists).
 Bar: tests/parity.py.
 """
 import pytest
 
 from tests.golden.cases import make_inputs
 from tests.parity import check_outputs, scatter_cells
-from tests.random_cases import binned_cases, nonfinite_cutoff_cases, odd_cases, random_cases, scale_poses
+from tests.random_cases import (binned_cases, many_pose_cases, nonfinite_cutoff_cases, odd_cases, random_cases,
+                                scale_poses)
 
 pytestmark = pytest.mark.gpu
 
 CASES = (random_cases(160, seed=424242) + random_cases(40, seed=777, min_p=0) + nonfinite_cutoff_cases()
-         + binned_cases() + odd_cases())
+         + binned_cases() + odd_cases() + many_pose_cases())
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c["name"] for c in CASES])
