@@ -111,7 +111,7 @@ def make_inputs(case):
     three = is_3d(op)
     rot_fn = rotations_3d if three else rotations_2d
     R = torch.stack([rot_fn(P, g, rdt, case["special"]) for _ in range(case["B_rot"])])
-    sh = (torch.randn(case["B_shift"], P, 2, generator=g, dtype=torch.float64) * 2.5).to(rdt) \
+    sh = (torch.randn(case["B_shift"], P, 2, generator=g, dtype=torch.float64) * case.get("shift_scale", 2.5)).to(rdt) \
         if case["shifts"] else None
     t = {"rotations": R, "shifts": sh}
     if op in FORW + PBACK:

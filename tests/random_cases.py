@@ -71,6 +71,20 @@ def many_pose_cases():
     return out
 
 
+def large_shift_cases():
+    """Shifts of a few hundred pixels (N(0, 500^2)): phase angles r s0 + c s1 up to ~1e5 rad, whose
+    fp32 value the reference rounds before its sine and cosine, for every op with a phase."""
+    out = []
+    seed = 8080
+    for op in OPS:
+        for interp in ("linear", "cubic"):
+            seed += 1
+            out.append(_case(f"bigshift_{op}_{interp}", op, interp=interp, os=2.0, B=1, P=7, n=32, seed=seed,
+                             shift_scale=500.0))
+            out[-1]["scaled"] = False
+    return out
+
+
 def odd_cases():
     """Odd projection sizes n (rows i <= n // 2 are frequencies 0..m, the others -m..-1 for
     n = 2m + 1: one more negative row than an even size has), every op, both interpolations, with

@@ -12,13 +12,14 @@ import pytest
 
 from tests.golden.cases import make_inputs
 from tests.parity import check_outputs, scatter_cells
-from tests.random_cases import (binned_cases, many_pose_cases, nonfinite_cutoff_cases, odd_cases, random_cases,
-                                scale_poses)
+from tests.random_cases import (binned_cases, large_shift_cases, many_pose_cases, nonfinite_cutoff_cases, odd_cases,
+                                random_cases, scale_poses)
 
 pytestmark = pytest.mark.gpu
 
 CASES = (random_cases(160, seed=424242) + random_cases(40, seed=777, min_p=0) + nonfinite_cutoff_cases()
-         + binned_cases() + odd_cases() + many_pose_cases())
+         + binned_cases() + odd_cases() + many_pose_cases()
+         + large_shift_cases())
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c["name"] for c in CASES])

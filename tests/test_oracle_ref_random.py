@@ -9,10 +9,10 @@ import torch
 
 from oracle import oracle as O
 from tests.golden.cases import make_inputs
-from tests.random_cases import nonfinite_cutoff_cases, odd_cases, random_cases, scale_poses
+from tests.random_cases import large_shift_cases, nonfinite_cutoff_cases, odd_cases, random_cases, scale_poses
 
 CASES = (random_cases(160, seed=424242) + random_cases(40, seed=777, min_p=0) + nonfinite_cutoff_cases()
-         + odd_cases())
+         + odd_cases() + large_shift_cases())
 
 
 @pytest.fixture(scope="module")
