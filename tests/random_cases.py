@@ -85,6 +85,36 @@ def large_shift_cases():
     return out
 
 
+def reflect_poses(args, case):
+    """Negate column 0 of every other pose matrix: orthonormal columns with determinant -1 (a
+    reflection), which the tiled kernels take as they take rotations."""
+    idx = {"project_3d_to_2d_forw": 1, "project_2d_forw": 1, "project_3d_to_2d_back": 2, "project_2d_back": 2,
+           "backproject_2d_to_3d_forw": 2, "backproject_2d_forw": 2,
+           "backproject_2d_to_3d_back": 4, "backproject_2d_back": 4}[case["op"]]
+    rot = args[idx]
+    rg = rot.requires_grad
+    r = rot.detach().clone()
+    r[:, ::2, :, 0] *= -1
+    args[idx] = r.requires_grad_(rg)
+    return args
+
+
+def reflect_cases():
+    """Every op, both interpolations, with every other pose a reflection (reflect_poses)."""
+    rng = random.Random(9191)
+    out = []
+    seed = 9191
+    for op in OPS:
+        for interp in ("linear", "cubic"):
+            seed += 1
+            c = _case(f"reflect_{op}_{interp}", op, interp=interp, os=rng.choice([1.0, 1.5, 2.0]), B=2, P=6,
+                      n=2 * rng.randint(6, 16), B_rot=rng.choice([1, 2]), seed=seed)
+            c["scaled"] = False
+            c["reflect"] = True
+            out.append(c)
+    return out
+
+
 def odd_cases():
     """Odd projection sizes n (rows i <= n // 2 are frequencies 0..m, the others -m..-1 for
     n = 2m + 1: one more negative row than an even size has), every op, both interpolations, with

@@ -9,10 +9,11 @@ import torch
 
 from oracle import oracle as O
 from tests.golden.cases import make_inputs
-from tests.random_cases import large_shift_cases, nonfinite_cutoff_cases, odd_cases, random_cases, scale_poses
+from tests.random_cases import (large_shift_cases, nonfinite_cutoff_cases, odd_cases, random_cases, reflect_cases,
+                                reflect_poses, scale_poses)
 
 CASES = (random_cases(160, seed=424242) + random_cases(40, seed=777, min_p=0) + nonfinite_cutoff_cases()
-         + odd_cases() + large_shift_cases())
+         + odd_cases() + large_shift_cases() + reflect_cases())
 
 
 @pytest.fixture(scope="module")
@@ -28,6 +29,8 @@ def test_oracle_matches_reference_build(case, ref):
     args, _ = make_inputs(case)
     if case["scaled"]:
         args = scale_poses(args, case)
+    if case.get("reflect"):
+        args = reflect_poses(args, case)
     threads = torch.get_num_threads()
     torch.set_num_threads(1)
     try:
