@@ -53,3 +53,41 @@ def test_two_streams_match_serial_calls(gpu, interp):
             assert torch.equal(got[0], exp[0]), f"{tag}: projections differ"
             assert _rel(got[1], exp[1]) <= 1e-5, f"{tag}: data volume {_rel(got[1], exp[1]):.3e}"
             assert _rel(got[2], exp[2]) <= 1e-5, f"{tag}: weight volume {_rel(got[2], exp[2]):.3e}"
+
+
+@pytest.mark.parametrize("shared_stream", [False, True])
+def test_two_host_threads_match_serial_calls(gpu, shared_stream):
+    """Two host threads enqueue at once, each on its own stream or both on one stream: the
+    (device, stream) scratch table is shared between threads, and calls on one stream take its
+    area's lock while they enqueue, so the results equal the serial calls'."""
+    import threading
+    a = _inputs(48, 9200, gpu)
+    b = _inputs(80, 9201, gpu)
+    serial = [_step(*a, "linear"), _step(*b, "linear")]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream()] * 2 if shared_stream else [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    results, errors = [None, None], []
+
+    def work(i, inp):
+        try:
+            torch.cuda.set_device(gpu)
+            with torch.cuda.stream(streams[i]):
+                for _ in range(5):
+                    results[i] = _step(*inp, "linear")
+        except Exception as e:  # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=work, args=(0, a)), threading.Thread(target=work, args=(1, b))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    print(f"[streams] two host threads, shared stream {shared_stream}", flush=True)
+    for got, exp, tag in ((results[0], serial[0], "a"), (results[1], serial[1], "b")):
+        assert torch.equal(got[0], exp[0]), f"{tag}: projections differ"
+        assert _rel(got[1], exp[1]) <= 1e-5, f"{tag}: data volume {_rel(got[1], exp[1]):.3e}"
+        assert _rel(got[2], exp[2]) <= 1e-5, f"{tag}: weight volume {_rel(got[2], exp[2]):.3e}"
