@@ -67,6 +67,29 @@ __global__ __launch_bounds__(kBlock) void k_project_forw_rest(Geom g, const Cx<V
                                                               Cx<float>* __restrict__ out) {
     constexpr int RS = DIM * DIM;
     const float cut2 = float(g.cut2);
+    // For a tiled pose only the masked pixels are written.  The mask test r^2 + c^2 > cut2
+    // (rounded as the reference rounds it) is monotone in c, so they are the row's tail: the scan
+    // starts at an estimate of its first column, sqrt(cut2 - r^2) - 2, once the exact test has
+    // passed the column before it (otherwise at 0).  The start depends on the row only, so up to
+    // kRestRows rows it is formed once per workgroup for all of its poses.
+    constexpr int kRestRows = 1024;
+    __shared__ int scan_start[kRestRows];
+    auto scan_of = [&](int i) {
+        const float r = freq_of<float>(i, g.n);
+        int c_scan = 0;
+        const float rem = cut2 - r * r;
+        if (rem >= 4.f) {  // false for NaN: then every column is tested (none is masked)
+            int cs = rem < 1.0e9f ? int(__builtin_amdgcn_sqrtf(rem)) - 2 : g.hp;
+            cs = min(g.hp, max(0, cs));
+            c_scan = (cs > 0 && filtered(r, float(cs - 1), cut2)) ? 0 : cs;
+        }
+        return c_scan;
+    };
+    const bool table = g.n <= kRestRows;
+    if (table) {
+        for (int i = threadIdx.x; i < g.n; i += kBlock) scan_start[i] = scan_of(i);
+        __syncthreads();
+    }
     for (int64_t bp = blockIdx.x; bp < g.B * g.P; bp += gridDim.x) {
         const int64_t b = bp / g.P, p = bp - b * g.P;
         const float* R = rot + ((g.B_rot == 1 ? 0 : b) * g.P + p) * RS;
@@ -74,23 +97,11 @@ __global__ __launch_bounds__(kBlock) void k_project_forw_rest(Geom g, const Cx<V
         const bool tiled = pose_tiled_d<DIM>(R);
         if (ZEROED && tiled) continue;  // block-uniform
         Cx<float>* outp = out + bp * g.npix;
-        // one row per wave, lanes along the row (no per-pixel division).  For a tiled pose only
-        // the masked pixels are written.  The mask test r^2 + c^2 > cut2 (rounded as the
-        // reference rounds it) is monotone in c, so they are the row's tail: the scan starts at
-        // an estimate of its first column, sqrt(cut2 - r^2) - 2, once the exact test has passed
-        // the column before it (otherwise at 0).
+        // one row per wave, lanes along the row (no per-pixel division)
         for (int i = threadIdx.x / 64; i < g.n; i += kBlock / 64) {
             const float r = freq_of<float>(i, g.n);
             Cx<float>* row = outp + int64_t(i) * g.hp;
-            int c_scan = 0;
-            if (tiled) {
-                const float rem = cut2 - r * r;
-                if (rem >= 4.f) {  // false for NaN: then every column is tested (none is masked)
-                    int cs = rem < 1.0e9f ? int(__builtin_amdgcn_sqrtf(rem)) - 2 : g.hp;
-                    cs = min(g.hp, max(0, cs));
-                    c_scan = (cs > 0 && filtered(r, float(cs - 1), cut2)) ? 0 : cs;
-                }
-            }
+            const int c_scan = tiled ? (table ? scan_start[i] : scan_of(i)) : 0;
             for (int j = c_scan + threadIdx.x % 64; j < g.hp; j += 64) {
                 const float c = float(j);
                 if (filtered(r, c, cut2)) row[j] = Cx<float>{0.f, 0.f};
