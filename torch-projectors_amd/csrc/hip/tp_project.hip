@@ -97,12 +97,16 @@ __global__ __launch_bounds__(kBlock) void k_project_forw_rest(Geom g, const Cx<V
         const bool tiled = pose_tiled_d<DIM>(R);
         if (ZEROED && tiled) continue;  // block-uniform
         Cx<float>* outp = out + bp * g.npix;
-        // one row per wave, lanes along the row (no per-pixel division)
-        for (int i = threadIdx.x / 64; i < g.n; i += kBlock / 64) {
+        // four rows per wave step, 16 lanes along each row (no per-pixel division): most rows'
+        // masked tails are short
+        constexpr int RL = 16, RW = 64 / RL;
+        for (int i0 = (threadIdx.x / 64) * RW; i0 < g.n; i0 += (kBlock / 64) * RW) {
+            const int i = i0 + (threadIdx.x % 64) / RL;
+            if (i >= g.n) continue;
             const float r = freq_of<float>(i, g.n);
             Cx<float>* row = outp + int64_t(i) * g.hp;
             const int c_scan = tiled ? (table ? scan_start[i] : scan_of(i)) : 0;
-            for (int j = c_scan + threadIdx.x % 64; j < g.hp; j += 64) {
+            for (int j = c_scan + threadIdx.x % RL; j < g.hp; j += RL) {
                 const float c = float(j);
                 if (filtered(r, c, cut2)) row[j] = Cx<float>{0.f, 0.f};
                 else if (!tiled) row[j] = project_pixel<DIM, float, CUBIC>(g, rec + b * g.vol, R, S, r, c);
