@@ -121,6 +121,14 @@ int poses_per_batch(double w, double eps, double os) {
     return rows <= 16 ? 4 : (rows <= 32 ? 2 : 1);
 }
 
+// Poses per wavefront batch of the 3D scatter, whose lanes take the batch's rows (all its poses' in
+// turn) in blocks of 64: about 64 / (typical rows of a pose), measured best at 6 for a pose with
+// about 10 rows (a 17-voxel box at oversampling 2); poses with more rows share the batch with fewer.
+int scatter_poses_per_batch(double w, double eps, double os) {
+    const int rows = int(std::floor(1.5 * (w + 2.0 * eps) / os)) + 2;
+    return rows <= 16 ? 6 : (rows <= 32 ? 3 : 1);
+}
+
 tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
     constexpr int L = tp::kTileEdge;
     tp::TileSpec ts{};
@@ -183,7 +191,7 @@ tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
     // plus fp32 rounding of the bounds themselves.
     ts.eps = 0.01f + 2.0f * tp::kRotationTol * ts.smax;
     ts.kp_forw = poses_per_batch(L, ts.eps, g.os);
-    ts.kp_scatter = poses_per_batch(tp::kScTC + (cubic ? 3 : 1), ts.eps, g.os);
+    ts.kp_scatter = scatter_poses_per_batch(tp::kScTC + (cubic ? 3 : 1), ts.eps, g.os);
     const int cl = int(std::floor(cutr)) + 1;
     ts.cmax = std::min(g.n / 2, cl);
     ts.rmin = std::max(g.n / 2 + 1 - g.n, -cl);

@@ -205,18 +205,19 @@ hipError_t launch_ifftshift_crop(int elem_bytes, int dim, const void* src, int64
 // calls on different streams their own work areas, so transforms that run at
 // once on the GPU never share one; calls on one stream run in order.  The
 // cache holds at most kMaxPlans plans: the least recently used one is
-// destroyed after its device has finished all queued work (its transforms may
-// still be running).  A plan that a graph capture used is never destroyed (the
-// graph keeps its work area), and no plan is made on a capturing stream (that
-// allocates): such a call fails with kFftNoPlanUnderCapture.  The cache lock
-// serialises the enqueues.
+// destroyed once its last transform has finished (an event recorded after
+// each transform; no device-wide synchronisation).  A plan that a graph
+// capture used is never destroyed (the graph keeps its work area), and no
+// plan is made on a capturing stream (that allocates): such a call fails with
+// kFftNoPlanUnderCapture.  The cache lock serialises the enqueues.
 namespace {
 
 using PlanKey = std::tuple<int, int, int, int64_t, int64_t, int, hipStream_t>;
 struct PlanEntry {
     hipfftHandle h;
-    uint64_t used;   // tick of the last call
-    bool captured;   // used by a call under graph capture: kept until the process ends
+    hipEvent_t done;  // recorded after each transform made outside a capture
+    uint64_t used;    // tick of the last call
+    bool captured;    // used by a call under graph capture: kept until the process ends
 };
 constexpr size_t kMaxPlans = 32;
 std::mutex g_fft_mu;
@@ -228,31 +229,29 @@ hipfftResult evict_oldest_plan() {
     for (auto it = g_plans.begin(); it != g_plans.end(); ++it)
         if (!it->second.captured && (old == g_plans.end() || it->second.used < old->second.used)) old = it;
     if (old == g_plans.end()) return HIPFFT_SUCCESS;  // every plan is held by a graph: the cache grows
-    int cur = 0;
-    if (hipGetDevice(&cur) != hipSuccess) return HIPFFT_INTERNAL_ERROR;
-    const int dev = std::get<5>(old->first);
-    if (hipSetDevice(dev) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
-        (void)hipSetDevice(cur);
-        return HIPFFT_INTERNAL_ERROR;
-    }
+    // its work area may still be in use by its last transform: wait for that one only
+    if (hipEventSynchronize(old->second.done) != hipSuccess) return HIPFFT_INTERNAL_ERROR;
     const hipfftResult r = hipfftDestroy(old->second.h);
+    (void)hipEventDestroy(old->second.done);
     g_plans.erase(old);
-    if (hipSetDevice(cur) != hipSuccess) return HIPFFT_INTERNAL_ERROR;
     return r;
 }
 
-int plan_for(bool forward, int dt, int dim, int64_t N, int64_t batch, hipStream_t s, hipfftHandle& out) {
+// The cached plan for a transform on stream s (made on first use); `capturing` tells whether s is
+// being captured into a graph.
+int plan_for(bool forward, int dt, int dim, int64_t N, int64_t batch, hipStream_t s, PlanEntry*& out,
+             bool& capturing) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return HIPFFT_INTERNAL_ERROR;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &cs) != hipSuccess) return HIPFFT_INTERNAL_ERROR;
-    const bool capturing = cs != hipStreamCaptureStatusNone;
+    capturing = cs != hipStreamCaptureStatusNone;
     const PlanKey key{forward ? 1 : 0, dt, dim, N, batch, dev, s};
     auto it = g_plans.find(key);
     if (it != g_plans.end()) {
         it->second.used = ++g_fft_tick;
         it->second.captured |= capturing;
-        out = it->second.h;
+        out = &it->second;
         return HIPFFT_SUCCESS;
     }
     if (capturing) return kFftNoPlanUnderCapture;
@@ -260,9 +259,14 @@ int plan_for(bool forward, int dt, int dim, int64_t N, int64_t batch, hipStream_
         const hipfftResult e = evict_oldest_plan();
         if (e != HIPFFT_SUCCESS) return e;
     }
+    hipEvent_t ev;
+    if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) return HIPFFT_ALLOC_FAILED;
     hipfftHandle h;
     hipfftResult r = hipfftCreate(&h);
-    if (r != HIPFFT_SUCCESS) return r;
+    if (r != HIPFFT_SUCCESS) {
+        (void)hipEventDestroy(ev);
+        return r;
+    }
     // norm="forward": the forward transform carries 1/N^dim, the inverse none
     double scale = 1.0;
     if (forward)
@@ -276,32 +280,42 @@ int plan_for(bool forward, int dt, int dim, int64_t N, int64_t batch, hipStream_
     if (r == HIPFFT_SUCCESS) r = hipfftSetStream(h, s);
     if (r != HIPFFT_SUCCESS) {
         hipfftDestroy(h);
+        (void)hipEventDestroy(ev);
         return r;
     }
-    g_plans.emplace(key, PlanEntry{h, ++g_fft_tick, false});
-    out = h;
+    out = &g_plans.emplace(key, PlanEntry{h, ev, ++g_fft_tick, false}).first->second;
     return HIPFFT_SUCCESS;
+}
+
+// After a transform: outside a capture, mark where its work area is free again.
+int transformed(hipfftResult r, const PlanEntry& pe, bool capturing, hipStream_t s) {
+    if (r != HIPFFT_SUCCESS || capturing) return int(r);
+    return hipEventRecord(pe.done, s) == hipSuccess ? HIPFFT_SUCCESS : HIPFFT_EXEC_FAILED;
 }
 
 }  // namespace
 
 int fft_forward(int dt, int dim, int64_t batch, int64_t N, const void* real, void* spec, hipStream_t s) {
     std::lock_guard<std::mutex> lock(g_fft_mu);
-    hipfftHandle h;
-    const int r = plan_for(true, dt, dim, N, batch, s, h);
+    PlanEntry* pe = nullptr;
+    bool capturing = false;
+    const int r = plan_for(true, dt, dim, N, batch, s, pe, capturing);
     if (r != HIPFFT_SUCCESS) return r;
     // out-of-place real-to-complex transforms leave their input intact
-    if (dt == 0) return int(hipfftExecR2C(h, (hipfftReal*)real, (hipfftComplex*)spec));
-    return int(hipfftExecD2Z(h, (hipfftDoubleReal*)real, (hipfftDoubleComplex*)spec));
+    const hipfftResult e = dt == 0 ? hipfftExecR2C(pe->h, (hipfftReal*)real, (hipfftComplex*)spec)
+                                   : hipfftExecD2Z(pe->h, (hipfftDoubleReal*)real, (hipfftDoubleComplex*)spec);
+    return transformed(e, *pe, capturing, s);
 }
 
 int fft_inverse(int dt, int dim, int64_t batch, int64_t N, void* spec, void* real, hipStream_t s) {
     std::lock_guard<std::mutex> lock(g_fft_mu);
-    hipfftHandle h;
-    const int r = plan_for(false, dt, dim, N, batch, s, h);
+    PlanEntry* pe = nullptr;
+    bool capturing = false;
+    const int r = plan_for(false, dt, dim, N, batch, s, pe, capturing);
     if (r != HIPFFT_SUCCESS) return r;
-    if (dt == 0) return int(hipfftExecC2R(h, (hipfftComplex*)spec, (hipfftReal*)real));
-    return int(hipfftExecZ2D(h, (hipfftDoubleComplex*)spec, (hipfftDoubleReal*)real));
+    const hipfftResult e = dt == 0 ? hipfftExecC2R(pe->h, (hipfftComplex*)spec, (hipfftReal*)real)
+                                   : hipfftExecZ2D(pe->h, (hipfftDoubleComplex*)spec, (hipfftDoubleReal*)real);
+    return transformed(e, *pe, capturing, s);
 }
 
 hipError_t launch_normalize(int dt, const void* data, const void* weights, int64_t elems, double reg, void* out,

@@ -74,7 +74,7 @@ struct TileSpec {
     float os, inv_os;         // oversampling and its inverse
     float smax;               // bound on |c*os| over the pixel grid
     int cmax, rmin, rmax;     // pixel-grid limits of c and r (grid and cutoff)
-    int kp_forw, kp_scatter;  // poses per wavefront batch (1, 2 or 4)
+    int kp_forw, kp_scatter;  // poses per wavefront batch (forward 1, 2 or 4; scatter 1, 3 or 6)
     bool os_exact;            // float(os) == os: c * os can be formed in float exactly as in double
     BinGrid sbins;            // pose bins of the scatter tile grid (list null: none)
 };

@@ -170,14 +170,15 @@ __device__ __forceinline__ void rotate_slice(const float* __restrict__ R, float 
 // flattened order, as packed (slot, c, r) entries; windows of 64 lanes then
 // read their samples straight from the queue.  Rows hold `cnt` samples from
 // column c0 at flattened index `excl`; entries [q0, q0 + QCAP) are written.
-constexpr unsigned kQRowBias = 0x8000u;  // r + bias in bits 0-15, c in bits 16-29, slot in 30-31
+// |r| and c are at most n / 2 <= 16383 (use_tiles keeps n <= 32766).
+constexpr unsigned kQRowBias = 0x4000u;  // r + bias in bits 0-14, c in bits 15-28, slot in 29-31
 __device__ __forceinline__ unsigned q_pack(int r, int c, int slot) {
-    return ((unsigned(r) + kQRowBias) & 0xffffu) | (unsigned(c) << 16) | (unsigned(slot) << 30);
+    return ((unsigned(r) + kQRowBias) & 0x7fffu) | (unsigned(c) << 15) | (unsigned(slot) << 29);
 }
 __device__ __forceinline__ void q_unpack(unsigned e, int& r, int& c, int& slot) {
-    r = int(e & 0xffffu) - int(kQRowBias);
-    c = int((e >> 16) & 0x3fffu);
-    slot = int(e >> 30);
+    r = int(e & 0x7fffu) - int(kQRowBias);
+    c = int((e >> 15) & 0x3fffu);
+    slot = int(e >> 29);
 }
 template <int QCAP>
 __device__ __forceinline__ void q_fill(unsigned* q, int r, int c0, int cnt, int excl, int slot, int q0) {
@@ -188,11 +189,14 @@ __device__ __forceinline__ void q_fill(unsigned* q, int r, int c0, int cnt, int 
 }
 
 // Per-wave copy of the poses of one batch; `base` is the pose's first pixel
-// in the [B, P, n, n/2+1] projections.
+// in the [B, P, n, n/2+1] projections.  The forward's batches also keep the
+// first row of the pose's samples in the box and the index of that row in the
+// batch's flattened row list.
 struct Slot {
     float R[9];
     float s0, s1;
     int64_t base;
+    int r0, start;
 };
 
 // The tiled kernels read columns 0 and 1 of a pose only (the slice plane and
@@ -215,6 +219,7 @@ __device__ __forceinline__ void load_pose(const float* __restrict__ rotb, const 
 }
 
 constexpr int kRunForw = 64, kRunScatter = 128;  // measured at the headline
+constexpr int kForwFlatKP = 5;  // forward poses per wave batch for poses of up to 16 rows (about 11 rows each)
 
 // Work items: first the core tiles, one item per (batch, tile, pose range),
 // then every tile of every batch with all poses (core tiles skipped there).
@@ -529,7 +534,11 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
     constexpr int WW = (GMODE == 2 && WG) ? (L + 1) * (L + 1) * (LD + 1) : 1;  // trilinear weight taps
     __shared__ float wt[WW];
     constexpr int LO = CUBIC ? 1 : 0, HI = CUBIC ? 2 : 1, W = L + LO + HI, WD = LD + LO + HI, W3 = W * W * WD;
-    constexpr int RPS = 64 / KP;
+    // GMODE 0 spreads the rows of a batch's KP poses over the wave's lanes in blocks of 64 (FLAT);
+    // the gradient modes keep a set of sums per pose slot and give each pose RPS = 64 / KP lanes
+    constexpr bool FLAT = GMODE == 0;
+    static_assert(KP >= 1 && KP <= 8, "poses per wave batch (three bits of a queue entry)");
+    constexpr int RPS = FLAT ? 64 : 64 / KP;
     constexpr int NT = kForwThreads, NW = NT / 64;
     constexpr int LOADS = (W3 + NT - 1) / NT;
     // the staged tile keeps the volume's storage type: a complex-half volume takes half the LDS
@@ -543,9 +552,12 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
     constexpr int QCAP = 256;
     __shared__ Slot slots[NW][KP];
     __shared__ unsigned queue[NW][QCAP];
+    __shared__ unsigned char marks[FLAT ? NW : 1][64];  // FLAT: pose lookup of the batch's rows
     __shared__ int gen_sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int slot = lane / RPS, jrow = lane % RPS;
+    // FLAT: lane k < KP holds pose k of the batch; otherwise lane = slot * RPS + row
+    const int slot = FLAT ? (lane < KP ? lane : 0) : lane / RPS, jrow = FLAT ? 0 : lane % RPS;
+    const bool pose_lane = FLAT ? lane < KP : true;
     // samples lie within |x| <= rho_k: rotations reach rho_unit + 1 (and have nothing to do when
     // the call has none); GEN poses the call's own reach, up to kScaleMax times farther, over
     // the part of the wide grid that this reach needs
@@ -657,7 +669,7 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
             float Rn[9], Sn[2];
             load_pose(rotb, shifts ? shifts + sb * g.P * 2 : nullptr, pose_of(plist[min(base + slot, np - 1)]), Rn, Sn);
             for (; base < np; base += NW * KP) {
-                const bool sv = base + slot < np;
+                const bool sv = pose_lane && base + slot < np;
                 const int pp = pose_of(plist[min(base + slot, np - 1)]);
                 float R[9], Sh[2];
 #pragma unroll
@@ -667,6 +679,19 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
                 if (base + NW * KP < np)
                     load_pose(rotb, shifts ? shifts + sb * g.P * 2 : nullptr,
                               pose_of(plist[min(base + NW * KP + slot, np - 1)]), Rn, Sn);
+                constexpr int KS = GRADS ? KP : 1;
+                float acc[KS][11];  // gradient modes: this lane's share of each slot's 9 rotation and 2 shift sums
+#pragma unroll
+                for (int s2 = 0; s2 < KS; ++s2)
+#pragma unroll
+                    for (int k = 0; k < 11; ++k) acc[s2][k] = 0.f;
+                int r0 = 0, r1 = -1;
+                if (sv || !FLAT) box_rows<GEN>(R, lo, hi, ts, r0, r1);
+                const int nr = sv ? max(0, r1 - r0 + 1) : 0;
+                // FLAT: the batch's rows (each pose's in turn) and each pose's first one among them
+                const int rincl = FLAT ? dpp_scan_add(nr) : 0;
+                const int start = rincl - nr;
+                const int rows = FLAT ? __builtin_amdgcn_readlane(rincl, 63) : 0;
                 if (jrow == 0 && sv) {
                     Slot& sd = slots[wave][slot];
 #pragma unroll
@@ -674,32 +699,44 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
                     sd.s0 = Sh[0];
                     sd.s1 = Sh[1];
                     sd.base = (b * g.P + pp) * int64_t(g.npix);
+                    sd.r0 = r0;
+                    sd.start = start;
                 }
                 __builtin_amdgcn_wave_barrier();
-                constexpr int KS = GRADS ? KP : 1;
-                float acc[KS][11];  // gradient modes: this lane's share of each slot's 9 rotation and 2 shift sums
+                int pcarry = 0;
+                // row blocks: FLAT, 64 rows of the batch at a time; otherwise RPS rows per pose while
+                // some pose has rows left
+                for (int rbase = 0; FLAT ? rbase < rows : __ballot(nr > rbase) != 0; rbase += RPS) {
+                    int r, c0 = 0, cnt = 0, sk = slot;
+                    if constexpr (FLAT) {
+                        // row rbase + lane of the batch: its pose (the pose lane whose rows hold it)
+                        sk = window_owner(nr, start, rbase, pcarry, marks[wave]);
+                        const int f = rbase + lane;
+                        r = 0;
+                        if (f < rows) {
+                            const Slot& sd = slots[wave][sk];
+                            float Rk[9];
 #pragma unroll
-                for (int s2 = 0; s2 < KS; ++s2)
-#pragma unroll
-                    for (int k = 0; k < 11; ++k) acc[s2][k] = 0.f;
-                int r0, r1;
-                box_rows<GEN>(R, lo, hi, ts, r0, r1);
-                const int nr = sv ? max(0, r1 - r0 + 1) : 0;
-                // row blocks of RPS rows per pose while some pose has rows left
-                for (int rbase = 0; __ballot(nr > rbase) != 0; rbase += RPS) {
-                    const int jr = rbase + jrow;
-                    const int r = r0 + jr;
-                    int c0 = 0, cnt = 0;
-                    if (jr < nr) {
-                        int c1;
-                        row_span(R, r, lo, hi, ts, cut2, c0, c1);
-                        cnt = max(0, c1 - c0 + 1);
+                            for (int e = 0; e < 9; ++e) Rk[e] = (e % 3 == 2) ? 0.f : sd.R[e];
+                            r = sd.r0 + (f - sd.start);
+                            int c1;
+                            row_span(Rk, r, lo, hi, ts, cut2, c0, c1);
+                            cnt = max(0, c1 - c0 + 1);
+                        }
+                    } else {
+                        const int jr = rbase + jrow;
+                        r = r0 + jr;
+                        if (jr < nr) {
+                            int c1;
+                            row_span(R, r, lo, hi, ts, cut2, c0, c1);
+                            cnt = max(0, c1 - c0 + 1);
+                        }
                     }
                     const int incl = dpp_scan_add(cnt);
                     const int excl = incl - cnt;
                     const int total = __builtin_amdgcn_readlane(incl, 63);
                     for (int q0 = 0; q0 < total; q0 += QCAP) {
-                      q_fill<QCAP>(queue[wave], r, c0, cnt, excl, slot, q0);
+                      q_fill<QCAP>(queue[wave], r, c0, cnt, excl, sk, q0);
                       const int m = min(QCAP, total - q0);
                       for (int e0 = 0; e0 < m; e0 += 64) {
                         if (e0 + lane >= m) continue;
@@ -852,12 +889,13 @@ struct TapMap {
 
 // Per-wave copy of a pose of the scatter's current batch: columns 0 and 1 of
 // the matrix (R6 = R[0], R[1], R[3], R[4], R[6], R[7]), the shifts, the pose's
-// first pixel in the projections and the first row of its samples in the box.
+// first pixel in the projections, the first row of its samples in the box and
+// the index of that row in the batch's flattened row list.
 struct ScSlot {
     float R6[6];
     float s0, s1;
     int64_t base;
-    int r0;
+    int r0, start;
 };
 // rotate_slice on the R6 layout (the same products in the same order).
 template <bool OSX>
@@ -867,6 +905,15 @@ __device__ __forceinline__ void rotate_slice6(const float* __restrict__ R6, floa
     x[1] = R6[2] * sc + R6[3] * sr;
     x[2] = R6[4] * sc + R6[5] * sr;
 }
+// row_span on the R6 layout.
+__device__ __forceinline__ void row_span6(const float* R6, int r, const float* lo, const float* hi,
+                                          const TileSpec& ts, float cut2, int& c0, int& c1) {
+    const float R[9] = {R6[0], R6[1], 0.f, R6[2], R6[3], 0.f, R6[4], R6[5], 0.f};
+    row_span(R, r, lo, hi, ts, cut2, c0, c1);
+}
+// A sample's row as (batch pose, row) in one word: row + bias in bits 0-15, pose in 16-31.
+constexpr unsigned kRowBias = 0x8000u;
+__device__ __forceinline__ unsigned kr_pack(int k, int r) { return ((unsigned(r) + kRowBias) & 0xffffu) | (unsigned(k) << 16); }
 
 template <bool CUBIC, int MODE, bool WEIGHTS, bool OSX>
 __device__ __forceinline__ void scatter_sample(const Geom& g, const ScSlot& sd, int rr, int cc, Cx<float> v,
@@ -937,17 +984,17 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                                                            CallPoses* __restrict__ cp, int gl) {
     constexpr int SL = CUBIC ? 2 : 1, SH = CUBIC ? 1 : 0;  // stencil reach below / above floor(x)
     constexpr int SLOW = CUBIC ? 1 : 0;                    // first tap at floor(x) - SLOW
-    constexpr int RPS = 64 / KP;
+    static_assert(KP >= 1 && KP <= 16, "poses per wave batch");
     constexpr int NT = kScatterThreads, NW = NT / 64;
     __shared__ double acc_re[S3], acc_im[S3];
     __shared__ double acc_w[WEIGHTS ? S3 : 1];
     __shared__ unsigned short plist[kChunk];
     __shared__ int pcnt[2];
     __shared__ ScSlot slots[NW][KP];
-    __shared__ int marks[NW][64];
+    __shared__ unsigned char marks[NW][64];
     __shared__ int gen_sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int slot = lane / RPS, jrow = lane % RPS;
+    const bool pose_lane = lane < KP;  // lane k holds pose k of the wave's batch
     const int N = g.N, H = g.H, half = N / 2;
     const int64_t items = g.B * (int64_t(ts.sd1 - ts.sd0) * (ts.sr1 - ts.sr0) * ts.sc1 * ts.ksplit +
                                  int64_t(ts.ntd) * ts.ntr * ts.ntc);
@@ -1035,22 +1082,30 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                 tm.off[2] = pass == 0 ? -SLOW - td : SLOW - td;
                 tm.lmin[0] = (pass == 1 && tc == 0) ? 1 : 0;
                 tm.lmin[1] = tm.lmin[2] = 0;
+                // wave batches of KP poses: lane k < KP holds pose k (the next batch's load in flight
+                // during this one), and the batch's rows, all poses' in turn, are spread over the
+                // wave's lanes in blocks of 64, so that a lane computes one row's column span
                 int base = wave * KP;
                 float Rn[9], Sn[2];
-                if (base < np) load_pose(rotb, shb, pose_at(min(base + slot, np - 1)), Rn, Sn);
+                if (base < np) load_pose(rotb, shb, pose_at(min(base + (pose_lane ? lane : 0), np - 1)), Rn, Sn);
                 for (; base < np; base += NW * KP) {
-                    const bool sv = base + slot < np;
-                    const int pp = pose_at(min(base + slot, np - 1));
+                    const bool sv = pose_lane && base + lane < np;
+                    const int pp = pose_at(min(base + (pose_lane ? lane : 0), np - 1));
                     float R[9], Sh[2];
 #pragma unroll
                     for (int e = 0; e < 9; ++e) R[e] = Rn[e];
                     Sh[0] = Sn[0];
                     Sh[1] = Sn[1];
-                    if (base + NW * KP < np) load_pose(rotb, shb, pose_at(min(base + NW * KP + slot, np - 1)), Rn, Sn);
-                    int r0, r1;
-                    box_rows<GEN>(R, lo, hi, ts, r0, r1);
-                    if (jrow == 0 && sv) {
-                        ScSlot& sd = slots[wave][slot];
+                    if (base + NW * KP < np)
+                        load_pose(rotb, shb, pose_at(min(base + NW * KP + (pose_lane ? lane : 0), np - 1)), Rn, Sn);
+                    int r0 = 0, r1 = -1;
+                    if (sv) box_rows<GEN>(R, lo, hi, ts, r0, r1);
+                    const int nr = sv ? max(0, r1 - r0 + 1) : 0;
+                    const int rincl = dpp_scan_add(nr);
+                    const int start = rincl - nr;  // the pose's first row in the batch's row list
+                    const int rows = __builtin_amdgcn_readlane(rincl, 63);
+                    if (sv) {
+                        ScSlot& sd = slots[wave][lane];
                         sd.R6[0] = R[0];
                         sd.R6[1] = R[1];
                         sd.R6[2] = R[3];
@@ -1061,20 +1116,26 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                         sd.s1 = Sh[1];
                         sd.base = (pose0 + pp) * int64_t(g.npix);
                         sd.r0 = r0;
+                        sd.start = start;
                     }
                     __builtin_amdgcn_wave_barrier();
-                    {
-                    const int nr = sv ? max(0, r1 - r0 + 1) : 0;
-                    // row blocks of RPS rows per pose while some pose has rows left
-                    for (int rbase = 0; __ballot(nr > rbase) != 0; rbase += RPS) {
-                        const int jr = rbase + jrow;
-                        const int r = r0 + jr;
-                        int c0 = 0, cnt = 0;
-                        if (jr < nr) {
+                    int pcarry = 0;
+                    for (int rbase = 0; rbase < rows; rbase += 64) {
+                        // row rbase + lane of the batch: its pose (the pose lane whose rows hold it)
+                        const int k = window_owner(nr, start, rbase, pcarry, marks[wave]);
+                        const int f = rbase + lane;
+                        int c0 = 0, cnt = 0, r = 0;
+                        if (f < rows) {
+                            const ScSlot& sd = slots[wave][k];
+                            float R6[6];
+#pragma unroll
+                            for (int e = 0; e < 6; ++e) R6[e] = sd.R6[e];
+                            r = sd.r0 + (f - sd.start);
                             int c1;
-                            row_span(R, r, lo, hi, ts, cut2, c0, c1);
+                            row_span6(R6, r, lo, hi, ts, cut2, c0, c1);
                             cnt = max(0, c1 - c0 + 1);
                         }
+                        const unsigned kr = kr_pack(k, r);
                         const int incl = dpp_scan_add(cnt);
                         const int excl = incl - cnt;
                         const int total = __builtin_amdgcn_readlane(incl, 63);
@@ -1083,16 +1144,17 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                         // sample e0 + lane of this row block: owner lane, pixel, validity and the
                         // element to load (element 0 for lanes without a sample, so that every
                         // load is issued on every path: a load under a branch makes the compiler
-                        // wait for it before the previous window's taps).  The owner's row is
-                        // its slot's first row plus its row index within the block.
+                        // wait for it before the previous window's taps).  The owner row's pose
+                        // and row come from its lane in one word.
                         auto locate = [&](int e0, int& rr, int& cc, int& sl, bool& ok, int64_t& pidx) {
                             const int e = e0 + lane;
                             const int lw = window_owner(cnt, excl, e0, carry, marks[wave]);
                             cc = __shfl(cx, lw, 64) + e;
-                            sl = lw / RPS;
+                            const unsigned krl = unsigned(__shfl(int(kr), lw, 64));
+                            sl = int(krl >> 16);
+                            rr = int(krl & 0xffffu) - int(kRowBias);
                             ok = e < total;
                             const ScSlot& sd = slots[wave][sl];
-                            rr = sd.r0 + rbase + (lw - sl * RPS);
                             ok = ok && !filtered(float(rr), float(cc), cut2) &&
                                  !(cc == 0 && (rr == g.n / 2 || rr < 0));  // Friedel half of x = 0
                             const int pix = int(__umul24(unsigned(rr >= 0 ? rr : rr + g.n), unsigned(g.hp))) + cc;
@@ -1123,7 +1185,6 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                             v = v2;
                             wv = wv2;
                         }
-                    }
                     }
                     __builtin_amdgcn_wave_barrier();
                 }
@@ -1272,36 +1333,41 @@ __global__ __launch_bounds__(kBinThreads) void k_pose_bins(Geom g, const float* 
         p[u] = int(pb) * kBinPoses + u * kBinThreads + int(threadIdx.x);
         load_rot(rotb + int64_t(min(p[u], P - 1)) * 9, R[u]);
     }
-    unsigned hits[kBinPer];  // bit i: the pose crosses bin i
-#pragma unroll
-    for (int u = 0; u < kBinPer; ++u) hits[u] = 0u;
-    for (int i = 0; i < nreach; ++i) {
-        box_c(i);
-#pragma unroll
-        for (int u = 0; u < kBinPer; ++u) hits[u] |= (p[u] < P && plane_hits(R[u], lo, hi)) ? 1u << i : 0u;
-    }
     const int64_t bin0 = (rb * nrow + row) * int64_t(bg.nb[0]);
-    for (int i = 0; i < nreach; ++i) {
-        uint64_t m[kBinPer];
-        int total = 0;
+    // the bins of the row in groups of 32, one hit mask bit per bin of the group (a volume of
+    // fewer than 2^31 cells has at most 26 bins along c, but the loop does not rely on it)
+    for (int i0 = 0; i0 < nreach; i0 += 32) {
+        const int ng = min(32, nreach - i0);
+        unsigned hits[kBinPer];  // bit i: the pose crosses bin i0 + i
 #pragma unroll
-        for (int u = 0; u < kBinPer; ++u) {
-            m[u] = __ballot((hits[u] >> i) & 1u);
-            total += __popcll(m[u]);
+        for (int u = 0; u < kBinPer; ++u) hits[u] = 0u;
+        for (int i = 0; i < ng; ++i) {
+            box_c(i0 + i);
+#pragma unroll
+            for (int u = 0; u < kBinPer; ++u) hits[u] |= (p[u] < P && plane_hits(R[u], lo, hi)) ? 1u << i : 0u;
         }
-        if (total == 0) continue;
-        int base = 0;
-        if (lane == 0) base = atomicAdd(&bg.count[bin0 + i], total);
-        base = __builtin_amdgcn_readfirstlane(base);
-        unsigned short* out = bg.list + (bin0 + i) * g.P;
+        for (int i = 0; i < ng; ++i) {
+            uint64_t m[kBinPer];
+            int total = 0;
 #pragma unroll
-        for (int u = 0; u < kBinPer; ++u) {
-            if ((hits[u] >> i) & 1u) {
-                const int rank = int(
-                    __builtin_amdgcn_mbcnt_hi(unsigned(m[u] >> 32), __builtin_amdgcn_mbcnt_lo(unsigned(m[u]), 0u)));
-                out[base + rank] = (unsigned short)p[u];
+            for (int u = 0; u < kBinPer; ++u) {
+                m[u] = __ballot((hits[u] >> i) & 1u);
+                total += __popcll(m[u]);
             }
-            base += __popcll(m[u]);
+            if (total == 0) continue;
+            int base = 0;
+            if (lane == 0) base = atomicAdd(&bg.count[bin0 + i0 + i], total);
+            base = __builtin_amdgcn_readfirstlane(base);
+            unsigned short* out = bg.list + (bin0 + i0 + i) * g.P;
+#pragma unroll
+            for (int u = 0; u < kBinPer; ++u) {
+                if ((hits[u] >> i) & 1u) {
+                    const int rank = int(__builtin_amdgcn_mbcnt_hi(unsigned(m[u] >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo(unsigned(m[u]), 0u)));
+                    out[base + rank] = (unsigned short)p[u];
+                }
+                base += __popcll(m[u]);
+            }
         }
     }
 }
@@ -1385,10 +1451,10 @@ hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, co
 template <bool CUBIC, int MODE, bool WEIGHTS, bool OSX>
 hipError_t scatter_kp_osx(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
                           const void* shifts, void* dst, void* wdst, CallPoses* cp, int gl, hipStream_t s) {
-    if (ts.kp_scatter >= 4)
-        return scatter_launch<CUBIC, MODE, WEIGHTS, 4, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
-    if (ts.kp_scatter == 2)
-        return scatter_launch<CUBIC, MODE, WEIGHTS, 2, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
+    if (ts.kp_scatter >= 6)
+        return scatter_launch<CUBIC, MODE, WEIGHTS, 6, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
+    if (ts.kp_scatter >= 3)
+        return scatter_launch<CUBIC, MODE, WEIGHTS, 3, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
     return scatter_launch<CUBIC, MODE, WEIGHTS, 1, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
 }
 
@@ -1426,8 +1492,9 @@ hipError_t forw_kp(const Geom& g, const TileSpec& ts, const void* rec, const voi
 #define TP_FORW(KPV) \
     forw_both<CUBIC, KPV, OSX, 0, true, false, VS>(g, ts, rec, rot, shifts, out, cp, gl, nullptr, nullptr, nullptr, \
                                                    nullptr, nullptr, s)
-    if (ts.kp_forw >= 4) return TP_FORW(4);
-    if (ts.kp_forw == 2) return TP_FORW(2);
+    // the forward's batches spread their rows over the lanes: about 64 / (rows of a pose) poses
+    if (ts.kp_forw >= 4) return TP_FORW(kForwFlatKP);
+    if (ts.kp_forw == 2) return TP_FORW(3);
     return TP_FORW(1);
 #undef TP_FORW
 }

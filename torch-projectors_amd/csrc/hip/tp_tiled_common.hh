@@ -73,15 +73,17 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // Row lanes hold `cnt` samples starting at flattened index `excl`.  For the
 // window [e0, e0 + 64) every lane gets the row lane owning index e0 + lane:
-// rows mark their first index in a per-wave LDS array, a prefix max carries
-// the marks forward, and `carry` brings the owner across windows.
-__device__ __forceinline__ int window_owner(int cnt, int excl, int e0, int& carry, int* marks) {
+// rows mark their first index in a per-wave LDS array (int or byte marks: a
+// mark is a lane + 1 <= 64), a prefix max carries the marks forward, and
+// `carry` brings the owner across windows.
+template <typename M>
+__device__ __forceinline__ int window_owner(int cnt, int excl, int e0, int& carry, M* marks) {
     const int lane = threadIdx.x & 63;
     marks[lane] = 0;
     __builtin_amdgcn_wave_barrier();
-    if (cnt > 0 && excl >= e0 && excl < e0 + 64) marks[excl - e0] = lane + 1;
+    if (cnt > 0 && excl >= e0 && excl < e0 + 64) marks[excl - e0] = M(lane + 1);
     __builtin_amdgcn_wave_barrier();
-    const int m = max(dpp_scan_max(marks[lane]), carry);
+    const int m = max(dpp_scan_max(int(marks[lane])), carry);
     carry = __builtin_amdgcn_readlane(m, 63);
     __builtin_amdgcn_wave_barrier();
     return m - 1;
