@@ -24,9 +24,9 @@ different things:
                    the commit it was measured at) / time
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--no-cpu]
-Configs: headline (default, the bench line), c2..c5 (the other BASELINE.json configurations),
-scaled (the headline with every pose matrix scaled by 1.02), published (the reference's
-published H100 rows: box 256, oversampling 1), prep, half.
+Configs: headline (default, the bench line), c1..c5 (the other BASELINE.json configurations),
+scaled / scaled06 / scaled14 (the headline with every pose matrix scaled by 1.02, 0.6, 1.4),
+published (the reference's published H100 rows: box 256, oversampling 1), prep, half.
 """
 import argparse
 import json
@@ -271,14 +271,53 @@ def make_headline(dev, scale=None):
            "interpolation": "linear", "shifts": "U(-8,8)", "weights": "sin^2(k rho^2)"}
     name = "headline"
     if scale is not None:
-        name = "scaled"
-        cfg["workload"] = f"scaled: the headline step with every pose matrix scaled by {scale}"
+        name = SCALED_NAMES[scale]
+        cfg["workload"] = f"{name}: the headline step with every pose matrix scaled by {scale}"
         cfg["pose_scale"] = scale
     return Workload(name, cfg["workload"], ops, cpu_sample, cfg)
 
 
+# the headline step with every pose matrix scaled: a magnification correction (x1.02) and strong
+# shrinking / enlarging (x0.6, x1.4)
+SCALED_NAMES = {1.02: "scaled", 0.6: "scaled06", 1.4: "scaled14"}
+
+
 def make_scaled(dev):
     return make_headline(dev, scale=1.02)
+
+
+def make_scaled06(dev):
+    return make_headline(dev, scale=0.6)
+
+
+def make_scaled14(dev):
+    return make_headline(dev, scale=1.4)
+
+
+def make_c1(dev):
+    """c1: 2D linear forward of a 64^2 noise image padded to 128, 256 poses of 64 x 33 (BASELINE.json
+    configs[0], the reference's CPU-runnable case; launch-bound on the GPU)."""
+    import torch
+    T = torch.ops.torch_projectors
+    gen = torch.Generator().manual_seed(20261201 + 1)
+    P, n, os_ = 256, 64, 2.0
+    rec = noise_image_rfft(1, 64, 128, gen, dev).to(torch.complex64)
+    rot = angle_rotations((1, P), gen).to(dev)
+    sh = (2 * torch.randn(1, P, 2, generator=gen)).to(dev)
+
+    def fwd():
+        T.project_2d_forw(rec, rot, sh, [n, n], "linear", os_, None)
+
+    def cpu_sample(p, threads, cpu_ops):
+        rc, r0, s0 = rec.cpu(), rot[:, :p].cpu(), sh[:, :p].cpu()
+        return timed_ops([("project_2d_forw", lambda: cpu_ops.project_2d_forw(
+            rc, r0, s0, [n, n], "linear", os_, None))], p * n * (n // 2 + 1))
+
+    samples = P * n * (n // 2 + 1)
+    cfg = {"workload": "c1: project_2d_forw, linear", "reconstruction": [1, 128, 65], "poses": P,
+           "proj": [n, n // 2 + 1], "oversampling": os_, "shifts": "2 N(0,1)"}
+    return Workload("c1", cfg["workload"], [("project_2d_forw", fwd, bytes_forward(P, n, 2, "linear"), samples, P,
+                                             compulsory_forward(samples, 128 * 65))], cpu_sample, cfg)
 
 
 def make_c2(dev):
@@ -588,13 +627,14 @@ def make_published(dev):
     return Workload("published", cfg["workload"], ops, cpu_sample, cfg, cpu_pmax=P, published=published)
 
 
-# headline is the bench line; c2-c5 are the other BASELINE configurations,
+# headline is the bench line; c1-c5 are the other BASELINE configurations,
 # prep the reference preparation around the headline volume, half the
-# headline forward from low-precision storage, scaled the headline with pose
-# matrices that are not rotations, published the reference's own published
-# rows (box 256, oversampling 1), run on request
-WORKLOADS = {"headline": make_headline, "c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5,
-             "prep": make_prep, "half": make_half, "scaled": make_scaled, "published": make_published}
+# headline forward from low-precision storage, scaled / scaled06 / scaled14 the
+# headline with pose matrices that are not rotations, published the
+# reference's own published rows (box 256, oversampling 1), run on request
+WORKLOADS = {"headline": make_headline, "c1": make_c1, "c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5,
+             "prep": make_prep, "half": make_half, "scaled": make_scaled, "scaled06": make_scaled06,
+             "scaled14": make_scaled14, "published": make_published}
 
 
 # ----------------------------------------------------------------------------- CPU baseline

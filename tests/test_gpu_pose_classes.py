@@ -2,10 +2,10 @@
 
 The reference treats every pose matrix alike (cpu/3d/projection_3d_to_2d_kernels.cpp:180-188,
 cpu/2d/projection_2d_kernels.cpp:173-178).  The tiled kernels take every matrix whose first two
-columns (3D) or two columns (2D) have singular values in [0.8, 1.25] (scaled, anisotropically
-magnified, sheared); the per-pixel kernels take the rest (strong scalings, degenerate matrices).
+columns (3D) or two columns (2D) have singular values in [0.5, 2] (scaled, anisotropically
+magnified, sheared); the per-pixel kernels take the rest (stronger scalings, degenerate matrices).
 These cases mix all of them in one call, and run calls whose poses all enlarge (samples beyond the
-unit-scale radius: the forward's wider tile grid) or all shrink.  Bar: tests/parity.py, with the
+unit-scale radius: the forward's wider tile grid, up to twice as far out) or all shrink.  Bar: tests/parity.py, with the
 per-cell check of the scatter volumes.
 """
 import math
@@ -35,9 +35,12 @@ def _classes(dim):
         R[..., :, 1] = R[..., :, 0]
         return R
 
+    strong = torch.diag(torch.tensor([1.8, 0.55, 1.0][:dim], dtype=torch.float64))
     return [(lambda R: R, True), (lambda R: 1.02 * R, True), (lambda R: 0.85 * R, True), (lambda R: 1.2 * R, True),
             (lambda R: aniso @ R, True), (lambda R: shear @ R, True), (lambda R: R @ shear, True),
-            (lambda R: 1.4 * R, False), (lambda R: 0.6 * R, False), (parallel, False)]
+            (lambda R: 1.4 * R, True), (lambda R: 0.6 * R, True), (lambda R: 1.9 * R, True),
+            (lambda R: strong @ R, True),
+            (lambda R: 2.3 * R, False), (lambda R: 0.4 * R, False), (parallel, False)]
 
 
 def _apply(args, case, mode):
@@ -51,7 +54,7 @@ def _apply(args, case, mode):
             f, _ = classes[p % len(classes)]
             r[:, p] = f(r[:, p])
     else:
-        s = {"enlarge": 1.2, "shrink": 0.85}[mode]
+        s = {"enlarge": 1.2, "shrink": 0.85, "enlarge_strong": 1.9, "shrink_strong": 0.55}[mode]
         r = s * r
     args[idx] = r.to(rot.dtype).requires_grad_(rot.requires_grad)
     return args
@@ -61,7 +64,7 @@ CASES = []
 seed = 4400
 for op in ROT_ARG:
     three = "3d" in op
-    for mode in ("mixed", "enlarge", "shrink"):
+    for mode in ("mixed", "enlarge", "shrink", "enlarge_strong", "shrink_strong"):
         for interp in ("linear", "cubic"):
             seed += 1
             n = (40 if interp == "linear" else 24) if three else 48
@@ -93,6 +96,6 @@ def test_pose_class_predicate_bounds():
         q = torch.linalg.qr(torch.randn(dim, dim, generator=g, dtype=torch.float64))[0]
         for f, tiled in _classes(dim):
             sv = torch.linalg.svdvals(f(q)[:, :2])
-            inside = bool((sv >= 0.8 - 1e-9).all() and (sv <= 1.25 + 1e-9).all())
+            inside = bool((sv >= 0.5 - 1e-9).all() and (sv <= 2.0 + 1e-9).all())
             assert inside == tiled, (dim, sv)
         assert math.isclose(float(torch.linalg.svdvals(1.02 * q[:, :2]).max()), 1.02)

@@ -29,9 +29,12 @@ struct Geom {
 // Pose matrices whose first two columns (3D) or two columns (2D) have both
 // singular values in [kScaleMin, kScaleMax] take the tiled kernels
 // (pose_tiled3 / pose_tiled2): rotations, and scaled or sheared matrices such
-// as magnification corrections.  Their bounds use the columns themselves when
-// the columns are orthonormal to kRotationTol, the dual basis otherwise.
-constexpr float kScaleMin = 0.8f, kScaleMax = 1.25f;
+// as magnification corrections, up to halving or doubling the sample grid.
+// Their bounds use the columns themselves when the columns are orthonormal to
+// kRotationTol, the dual basis otherwise (its conditioning is at most
+// kScaleMax / kScaleMin = 4).  Degenerate and stronger scalings take the
+// per-pixel kernels.
+constexpr float kScaleMin = 0.5f, kScaleMax = 2.0f;
 constexpr float kRotationTol = 1e-5f;
 
 // Tile-owner enumeration parameters of the fp32 3D kernels (tp_tiled3d.hip).
