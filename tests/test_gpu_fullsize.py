@@ -1,21 +1,21 @@
 """The BASELINE configurations at their full sizes, through the dispatcher ops.
 
-The oracle cannot redo whole full-size runs in seconds, so these tests use
-properties that hold at any size:
+Every output is compared whole with the oracle run on the same inputs (all host threads; poses
+are independent, so this is what the reference's CPU kernels compute,
+cpu/3d/projection_3d_to_2d_kernels.cpp:97-402):
 
-* poses are independent: the GPU result of a sampled pose (its projection,
-  its gradient rows, its grad_projections) equals the oracle's run on that
-  pose alone;
-* batch items are independent: a sampled item's volume sums equal the
-  oracle's on that item's poses;
-* a volume sum over every pose is compared whole where the oracle finishes
-  in seconds (the headline and c3 backprojections, c1), and there also cell
-  by cell (tests/parity.py `check_cells`: untouched cells exactly 0, every
-  other cell within 1e-5 * max|v| * sum|tap weight|).
+* the headline, c2 and c4 forwards over all their poses (bit-identical without shifts, relative
+  L2 1e-5 with them);
+* the headline and c3 backprojections and the c4 reconstruction gradient over all 2048 poses,
+  whole and cell by cell (tests/parity.py `check_cells`: untouched cells exactly 0, every other
+  cell within 1e-5 * max|v| * sum|tap weight| of the exact sum of the reference's taps);
+* c4's rotation and shift gradients of all 2048 poses;
+* c5 (16 images x 4096 poses, 2.16e9 projection elements): batch item 0 over all its 4096 poses
+  through the forward, the backprojection and both backward ops; item 15 on sampled poses and
+  its backprojected volume (batch items are independent).
 
-Inputs follow bench.py's synthetic recipes (seeded).  Bars as tests/parity.py:
-gathers bit-identical without shifts, else relative L2 1e-5; scatters and
-pose gradients relative L2 1e-4.
+Inputs follow bench.py's synthetic recipes (seeded).  Bars as tests/parity.py: gathers
+bit-identical without shifts, else relative L2 1e-5; scatters and pose gradients relative L2 1e-4.
 """
 import pytest
 import torch
@@ -61,20 +61,18 @@ def headline(gpu):
     return vol, rot, sh, w
 
 
-POSES = [0, 1, 1031, 2047]
-
-
-def test_headline_forward_sampled_poses(headline, ops, O):
+def test_headline_forward_whole(headline, ops, O):
     vol, rot, sh, _ = headline
-    say("headline forward, 2048 poses")
-    vol_c = vol.cpu()
+    say("headline forward, all 2048 poses against the oracle, with shifts")
+    vol_c, rot_c = vol.cpu(), rot.cpu()
     proj = ops.project_3d_to_2d_forw(vol, rot, sh, [256, 256], "linear", 2.0, None)
     assert proj.shape == (1, 2048, 256, 129)
-    exp = O.project_3d_to_2d_forw(vol_c, rot[:, POSES].cpu(), sh[:, POSES].cpu(), [256, 256], "linear", 2.0, None)
-    close(proj[:, POSES].cpu(), exp, GATHER_TOL[F32], "forward with shifts, sampled poses")
+    exp = O.project_3d_to_2d_forw(vol_c, rot_c, sh.cpu(), [256, 256], "linear", 2.0, None)
+    close(proj.cpu(), exp, GATHER_TOL[F32], "forward with shifts, all poses")
+    say("headline forward, all 2048 poses, no shifts: bit-identical")
     proj0 = ops.project_3d_to_2d_forw(vol, rot, None, [256, 256], "linear", 2.0, None)
-    exp0 = O.project_3d_to_2d_forw(vol_c, rot[:, POSES].cpu(), None, [256, 256], "linear", 2.0, None)
-    assert torch.equal(proj0[:, POSES].cpu(), exp0), "forward without shifts must be bit-identical"
+    exp0 = O.project_3d_to_2d_forw(vol_c, rot_c, None, [256, 256], "linear", 2.0, None)
+    assert torch.equal(proj0.cpu(), exp0), "forward without shifts must be bit-identical"
 
 
 def test_headline_backprojection_whole(headline, ops, O):
@@ -107,16 +105,19 @@ def test_c1_2d_linear_whole(ops, O, gpu):
     close(data.cpu(), ed, SCATTER_TOL[F32], "c1 backprojection")
 
 
-def test_c2_forward_sampled_poses(ops, O, gpu):
+def test_c2_forward_whole(ops, O, gpu):
     gen = torch.Generator().manual_seed(20261201 + 2)
     vol = bench.blob_volume_rfft(128, 256, 32, 40.0, gen, gpu)
     rot = bench.quat_rotations(4096, gen)[None].to(gpu)
     sh = ((torch.rand(1, 4096, 2, generator=gen) * 10) - 5).to(gpu)
-    say("c2 forward, 4096 poses of a 256^3 volume")
+    say("c2 forward, all 4096 poses of a 256^3 volume")
+    vol_c, rot_c = vol.cpu(), rot.cpu()
     proj = ops.project_3d_to_2d_forw(vol, rot, sh, [128, 128], "linear", 2.0, None)
-    idx = [0, 2049, 4095]
-    exp = O.project_3d_to_2d_forw(vol.cpu(), rot[:, idx].cpu(), sh[:, idx].cpu(), [128, 128], "linear", 2.0, None)
-    close(proj[:, idx].cpu(), exp, GATHER_TOL[F32], "c2 forward, sampled poses")
+    exp = O.project_3d_to_2d_forw(vol_c, rot_c, sh.cpu(), [128, 128], "linear", 2.0, None)
+    close(proj.cpu(), exp, GATHER_TOL[F32], "c2 forward, all poses")
+    proj0 = ops.project_3d_to_2d_forw(vol, rot, None, [128, 128], "linear", 2.0, None)
+    exp0 = O.project_3d_to_2d_forw(vol_c, rot_c, None, [128, 128], "linear", 2.0, None)
+    assert torch.equal(proj0.cpu(), exp0), "c2 forward without shifts must be bit-identical"
 
 
 def test_c3_backprojection_whole(ops, O, gpu):
@@ -148,38 +149,46 @@ def c4(gpu):
     return vol, rot, sh, g
 
 
-def test_c4_cubic_forward_sampled_poses(c4, ops, O):
+def test_c4_cubic_forward_whole(c4, ops, O):
     vol, rot, sh, _ = c4
-    say("c4 cubic forward, 2048 poses")
+    say("c4 cubic forward, all 2048 poses against the oracle")
+    vol_c, rot_c = vol.cpu(), rot.cpu()
     proj = ops.project_3d_to_2d_forw(vol, rot, sh, [256, 256], "cubic", 2.0, None)
-    exp = O.project_3d_to_2d_forw(vol.cpu(), rot[:, POSES].cpu(), sh[:, POSES].cpu(), [256, 256], "cubic", 2.0, None)
-    close(proj[:, POSES].cpu(), exp, GATHER_TOL[F32], "cubic forward, sampled poses")
+    exp = O.project_3d_to_2d_forw(vol_c, rot_c, sh.cpu(), [256, 256], "cubic", 2.0, None)
+    close(proj.cpu(), exp, GATHER_TOL[F32], "cubic forward, all poses")
+    del proj, exp
+    say("c4 cubic forward without shifts, all 2048 poses: bit-identical")
+    proj0 = ops.project_3d_to_2d_forw(vol, rot, None, [256, 256], "cubic", 2.0, None)
+    exp0 = O.project_3d_to_2d_forw(vol_c, rot_c, None, [256, 256], "cubic", 2.0, None)
+    assert torch.equal(proj0.cpu(), exp0), "cubic forward without shifts must be bit-identical"
 
 
-def test_c4_cubic_backward(c4, ops, O):
+@pytest.fixture(scope="module")
+def c4_back(c4, ops, O):
+    """c4's backward on the GPU and in the oracle, all 2048 poses, rotations and shifts requiring grad."""
     vol, rot, sh, g = c4
-    say("c4 cubic backward, 2048 poses; pose gradients of sampled poses")
+    say("c4 cubic backward, all 2048 poses: GPU and oracle")
     rg, sg = rot.clone().requires_grad_(True), sh.clone().requires_grad_(True)
-    grec, grot, gsh = ops.project_3d_to_2d_back(g, vol, rg, sg, "cubic", 2.0, None)
-    assert grec.shape == vol.shape and grot.shape == rot.shape and gsh.shape == sh.shape
-    vol_c = vol.cpu()
-    r_c = rot[:, POSES].cpu().requires_grad_(True)
-    s_c = sh[:, POSES].cpu().requires_grad_(True)
-    _, er, es = O.project_3d_to_2d_back(g[:, POSES].cpu(), vol_c, r_c, s_c, "cubic", 2.0, None)
-    close(grot[:, POSES].cpu(), er, SCATTER_TOL[F32], "rotation gradients, sampled poses")
-    close(gsh[:, POSES].cpu(), es, SCATTER_TOL[F32], "shift gradients, sampled poses")
-    for p0 in (0, 1000):
-        say(f"c4 reconstruction gradient over poses {p0}-{p0 + 47}, whole volume, also cell by cell")
-        sub = slice(p0, p0 + 48)
-        g_s = g[:, sub].contiguous()
-        grec_s, _, _ = ops.project_3d_to_2d_back(g_s, vol, rot[:, sub].contiguous(), sh[:, sub].contiguous(),
-                                                 "cubic", 2.0, None)
-        g_c = g_s.cpu()
-        eg, _, _ = O.project_3d_to_2d_back(g_c, vol_c, rot[:, sub].cpu(), sh[:, sub].cpu(), "cubic", 2.0, None)
-        close(grec_s.cpu(), eg, SCATTER_TOL[F32], f"reconstruction gradient, poses {p0}-{p0 + 47}")
-        check_scatter("project_3d_to_2d_back", (grec_s,),
-                      [g_c, vol_c, rot[:, sub], sh[:, sub], "cubic", 2.0, None], O,
-                      f"reconstruction gradient, poses {p0}-{p0 + 47}")
+    got = ops.project_3d_to_2d_back(g, vol, rg, sg, "cubic", 2.0, None)
+    assert got[0].shape == vol.shape and got[1].shape == rot.shape and got[2].shape == sh.shape
+    got = tuple(t.cpu() for t in got)
+    args = [g.cpu(), vol.cpu(), rot.cpu().requires_grad_(True), sh.cpu().requires_grad_(True), "cubic", 2.0, None]
+    exp = O.project_3d_to_2d_back(*args)
+    return got, exp, args
+
+
+def test_c4_cubic_backward_whole(c4_back):
+    got, exp, _ = c4_back
+    close(got[0], exp[0], SCATTER_TOL[F32], "reconstruction gradient, all poses")
+    close(got[1], exp[1], SCATTER_TOL[F32], "rotation gradients, all poses")
+    close(got[2], exp[2], SCATTER_TOL[F32], "shift gradients, all poses")
+
+
+def test_c4_reconstruction_gradient_cells(c4_back, O):
+    got, _, args = c4_back
+    say("c4 reconstruction gradient, all 2048 poses, cell by cell")
+    check_scatter("project_3d_to_2d_back", (got[0],), [a.detach() if isinstance(a, torch.Tensor) else a for a in args],
+                  O, "reconstruction gradient, all poses")
 
 
 # ----------------------------------------------------------------------------- c5 (batched 2D cubic)
@@ -193,7 +202,7 @@ def c5(gpu):
 
 
 ITEMS = [0, 15]
-PAIRS = [(0, 0), (0, 4095), (15, 2048), (15, 7)]
+PAIRS = [(15, 2048), (15, 7)]  # sampled poses of item 15 (item 0 is compared whole)
 
 
 def test_c5_batched_2d_cubic(c5, ops, O):
@@ -202,6 +211,11 @@ def test_c5_batched_2d_cubic(c5, ops, O):
     proj = ops.project_2d_forw(rec, rot, sh, [256, 256], "cubic", 2.0, 64.0)
     assert proj.shape == (16, 4096, 256, 129) and proj.numel() > 2 ** 31
     rec_c = rec.cpu()
+    r0, s0 = rot[0:1].cpu(), sh[0:1].cpu()
+    say("c5 forward, item 0, all 4096 poses against the oracle")
+    exp = O.project_2d_forw(rec_c[0:1], r0, s0, [256, 256], "cubic", 2.0, 64.0)
+    close(proj[0:1].cpu(), exp, GATHER_TOL[F32], "forward (item 0, all poses)")
+    del exp
     for b, p in PAIRS:
         exp = O.project_2d_forw(rec_c[b:b + 1], rot[b:b + 1, p:p + 1].cpu(), sh[b:b + 1, p:p + 1].cpu(), [256, 256],
                                 "cubic", 2.0, 64.0)
@@ -227,6 +241,14 @@ def test_c5_batched_2d_cubic(c5, ops, O):
     rg, sg = rot.clone().requires_grad_(True), sh.clone().requires_grad_(True)
     gproj, gwts, grot, gsh = ops.backproject_2d_back(gd, gw, proj, ones, rg, sg, "cubic", 2.0, 64.0)
     assert gproj.shape == proj.shape and gwts.shape == ones.shape
+    say("c5 backproject_2d_back, item 0, all 4096 poses against the oracle")
+    e = O.backproject_2d_back(gd[0:1].cpu(), gw[0:1].cpu(), proj[0:1].cpu(), ones[0:1].cpu(),
+                              r0.clone().requires_grad_(True), s0.clone().requires_grad_(True), "cubic", 2.0, 64.0)
+    close(gproj[0:1].cpu(), e[0], GATHER_TOL[F32], "grad_projections (item 0, all poses)")
+    close(gwts[0:1].cpu(), e[1], GATHER_TOL[F32], "grad_weights (item 0, all poses)")
+    close(grot[0:1].cpu(), e[2], SCATTER_TOL[F32], "grad_rotations (item 0, all poses)")
+    close(gsh[0:1].cpu(), e[3], SCATTER_TOL[F32], "grad_shifts (item 0, all poses)")
+    del e
     for b, p in PAIRS:
         r_c = rot[b:b + 1, p:p + 1].cpu().requires_grad_(True)
         s_c = sh[b:b + 1, p:p + 1].cpu().requires_grad_(True)
@@ -238,14 +260,17 @@ def test_c5_batched_2d_cubic(c5, ops, O):
         close(gsh[b:b + 1, p:p + 1].cpu(), e[3], SCATTER_TOL[F32], f"grad_shifts (item {b}, pose {p})")
     del ones, gwts
 
-    say("c5 project_2d_back: reconstruction gradient of item 0 over all its poses, and the rotation and "
-        "shift gradients of sampled (item, pose) pairs")
+    say("c5 project_2d_back, item 0, all 4096 poses against the oracle: reconstruction, rotation and shift "
+        "gradients")
     grec, grot, gsh = ops.project_2d_back(gproj, rec, rg, sg, "cubic", 2.0, 64.0)
     assert grec.shape == rec.shape and grot.shape == rot.shape and gsh.shape == sh.shape
     g0 = gproj[0:1].cpu()
-    eg, _, _ = O.project_2d_back(g0, rec_c[0:1], rot[0:1].cpu(), sh[0:1].cpu(), "cubic", 2.0, 64.0)
+    eg, er, es = O.project_2d_back(g0, rec_c[0:1], r0.clone().requires_grad_(True), s0.clone().requires_grad_(True),
+                                   "cubic", 2.0, 64.0)
     close(grec[0:1].cpu(), eg, SCATTER_TOL[F32], "reconstruction gradient (item 0)")
-    check_scatter("project_2d_back", (grec[0:1],), [g0, rec_c[0:1], rot[0:1], sh[0:1], "cubic", 2.0, 64.0], O,
+    close(grot[0:1].cpu(), er, SCATTER_TOL[F32], "project_2d_back grad_rotations (item 0, all poses)")
+    close(gsh[0:1].cpu(), es, SCATTER_TOL[F32], "project_2d_back grad_shifts (item 0, all poses)")
+    check_scatter("project_2d_back", (grec[0:1],), [g0, rec_c[0:1], r0, s0, "cubic", 2.0, 64.0], O,
                   "reconstruction gradient (item 0)")
     for b, p in PAIRS:
         r_c = rot[b:b + 1, p:p + 1].cpu().requires_grad_(True)

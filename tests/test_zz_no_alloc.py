@@ -41,19 +41,22 @@ def _inputs(B, N, P, n, seed, mix):
             elif k == 2:
                 rot[0, p] = shear @ rot[0, p]
             elif k == 3:
-                rot[0, p] *= 0.6  # beyond the tiled scale range: per-pixel kernels
+                rot[0, p] *= 0.4  # beyond the tiled scale range: per-pixel kernels
     rot = rot.float()
     shifts = (torch.rand(1, P, 2, generator=g) - 0.5) * 6
     return rec, rot, shifts
 
 
-def _call(name, rec, rot, shifts, n, interp, os_):
-    out = hip_path._poisoned((rec.shape[0], rot.shape[1], n, n // 2 + 1), torch.complex64)
+def _launch(name, rec, rot, shifts, out, n, interp, os_, stream):
     B, D, N, H = rec.shape
     capi.call(name, capi.TP_F32, hip_path._p(rec), B, D, N, H, hip_path._p(rot), rot.shape[0], rot.shape[1],
               hip_path._p(shifts), shifts.shape[0] if shifts is not None else 1, n,
-              capi.TP_CUBIC if interp == "cubic" else capi.TP_LINEAR, float(os_), 0, 0.0, hip_path._p(out),
-              hip_path._stream())
+              capi.TP_CUBIC if interp == "cubic" else capi.TP_LINEAR, float(os_), 0, 0.0, hip_path._p(out), stream)
+
+
+def _call(name, rec, rot, shifts, n, interp, os_):
+    out = hip_path._poisoned((rec.shape[0], rot.shape[1], n, n // 2 + 1), torch.complex64)
+    _launch(name, rec, rot, shifts, out, n, interp, os_, hip_path._stream())
     torch.cuda.synchronize()
     return out.cpu()
 
@@ -86,3 +89,47 @@ def test_noalloc_calls_in_a_row_keep_no_state(gpu):
         got = _call("tp_project_3d_to_2d_forw_noalloc", d_rec, d_rot, None, 24, "linear", 2.0)
         want = _call("tp_project_3d_to_2d_forw", d_rec, d_rot, None, 24, "linear", 2.0)
         assert torch.equal(got, want)
+
+
+def test_noalloc_captured_on_a_stream_no_call_has_used(gpu):
+    """The entry point needs no per-stream scratch: captured in a HIP graph on a stream that no call
+    has used (where the allocating entry point fails, since it would have to allocate the stream's
+    scratch during capture), its replays give exactly the allocating entry point's projections,
+    also after new poses are written into the captured input.  Each replay's output starts as NaN."""
+    n = 24
+    rec, rot, shifts = _inputs(1, 48, 96, n, 31, mix=True)
+    d_rec, d_rot, d_sh = rec.to(gpu), rot.to(gpu), shifts.to(gpu)
+    shape = (1, rot.shape[1], n, n // 2 + 1)
+    # the first call on this device sets up its static scratch; it is made eagerly here, so that the
+    # test also holds when it runs alone
+    _call("tp_project_3d_to_2d_forw_noalloc", d_rec, d_rot, d_sh, n, "linear", 2.0)
+    torch.cuda.synchronize()
+
+    unused = torch.cuda.Stream()
+    out0 = torch.empty(shape, dtype=torch.complex64, device=gpu)
+    g0 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g0, stream=unused):
+        with pytest.raises(RuntimeError, match="first call on a stream allocates"):
+            _launch("tp_project_3d_to_2d_forw", d_rec, d_rot, d_sh, out0, n, "linear", 2.0,
+                    _P(unused.cuda_stream))
+    torch.cuda.synchronize()
+
+    fresh = torch.cuda.Stream()
+    out = hip_path._poisoned(shape, torch.complex64)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=fresh):
+        _launch("tp_project_3d_to_2d_forw_noalloc", d_rec, d_rot, d_sh, out, n, "linear", 2.0, _P(fresh.cuda_stream))
+    torch.cuda.synchronize()
+
+    _, new_rot, _ = _inputs(1, 48, 96, n, 32, mix=True)
+    for replay in range(3):
+        if replay == 2:
+            d_rot.copy_(new_rot.to(gpu))  # new poses in the captured input
+        out.fill_(complex(float("nan"), float("nan")))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = _call("tp_project_3d_to_2d_forw", d_rec, d_rot, d_sh, n, "linear", 2.0)
+        print(f"[noalloc] replay {replay}", flush=True)
+        got = out.cpu()
+        assert not torch.isnan(torch.view_as_real(got)).any(), f"replay {replay}: unwritten elements"
+        assert torch.equal(got, want), f"replay {replay}: projections differ"
