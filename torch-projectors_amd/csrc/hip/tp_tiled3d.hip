@@ -1453,6 +1453,8 @@ hipError_t scatter_kp_osx(const Geom& g, const TileSpec& ts, const void* src, co
                           const void* shifts, void* dst, void* wdst, CallPoses* cp, int gl, hipStream_t s) {
     if (ts.kp_scatter >= 6)
         return scatter_launch<CUBIC, MODE, WEIGHTS, 6, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
+    if (ts.kp_scatter >= 4)
+        return scatter_launch<CUBIC, MODE, WEIGHTS, 4, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
     if (ts.kp_scatter >= 3)
         return scatter_launch<CUBIC, MODE, WEIGHTS, 3, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
     return scatter_launch<CUBIC, MODE, WEIGHTS, 1, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
