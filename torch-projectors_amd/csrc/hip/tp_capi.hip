@@ -124,7 +124,7 @@ int poses_per_batch(double w, double eps, double os) {
 // Poses per wavefront batch of the 3D scatter, whose lanes take the batch's rows (all its poses' in
 // turn) in blocks of 64: about 64 / (typical rows of a pose), measured best at 6 for a pose with
 // about 10 rows (a 17-voxel box at oversampling 2) and at 4 for the cubic stencil's 19-voxel box;
-// poses with more rows share the batch with fewer.
+// poses with more rows share the batch with fewer.  (The cubic kernels take at most 4.)
 int scatter_poses_per_batch(double w, double eps, double os) {
     const int rows = int(std::floor(1.5 * (w + 2.0 * eps) / os)) + 2;
     return rows <= 14 ? 6 : (rows <= 21 ? 4 : (rows <= 32 ? 3 : 1));

@@ -77,7 +77,10 @@ struct TileSpec {
     float os, inv_os;         // oversampling and its inverse
     float smax;               // bound on |c*os| over the pixel grid
     int cmax, rmin, rmax;     // pixel-grid limits of c and r (grid and cutoff)
-    int kp_forw, kp_scatter;  // poses per wavefront batch (forward 1, 2 or 4; scatter 1, 3 or 6)
+    // poses per wavefront batch by the rows a pose's box spans: kp_forw 1, 2 or 4 (the forward
+    // launches 1, 3 or 5 of them, the gradient modes 1, 2 or 4); kp_scatter 1, 3, 4 or 6 (cubic
+    // at most 4)
+    int kp_forw, kp_scatter;
     bool os_exact;            // float(os) == os: c * os can be formed in float exactly as in double
     BinGrid sbins;            // pose bins of the scatter tile grid (list null: none)
 };

@@ -887,10 +887,12 @@ struct TapMap {
     int lmin[3];
 };
 
-// Per-wave copy of a pose of the scatter's current batch: columns 0 and 1 of
-// the matrix (R6 = R[0], R[1], R[3], R[4], R[6], R[7]), the shifts, the pose's
+// Per-wave copy of a pose of the scatter's batches: columns 0 and 1 of the
+// matrix (R6 = R[0], R[1], R[3], R[4], R[6], R[7]), the shifts, the pose's
 // first pixel in the projections, the first row of its samples in the box and
-// the index of that row in the batch's flattened row list.
+// the index of that row in the batch's flattened row list.  With carried
+// windows a wave keeps two sets (the current batch and the one before, whose
+// samples a carried window may still hold).
 struct ScSlot {
     float R6[6];
     float s0, s1;
@@ -990,7 +992,15 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
     __shared__ double acc_w[WEIGHTS ? S3 : 1];
     __shared__ unsigned short plist[kChunk];
     __shared__ int pcnt[2];
-    __shared__ ScSlot slots[NW][KP];
+    // CARRY (cubic): a row block's last, partial window of samples is not deposited at once but
+    // filled up with the following samples, across batches.  At the cubic stencil's ~26 active
+    // lanes per tap an LDS atomic instruction costs about as much as with more lanes, so fuller
+    // windows take fewer instructions (3-4 % faster).  At the linear stencil's ~37 an
+    // instruction's cost grows with its lanes and carried windows measured no faster, so the
+    // linear kernels deposit every row block's windows in it.
+    constexpr bool CARRY = CUBIC;
+    static_assert(!CARRY || KP <= 4, "two pose sets per wave within four workgroups' LDS per CU");
+    __shared__ ScSlot slots[NW][CARRY ? 2 * KP : KP];
     __shared__ unsigned char marks[NW][64];
     __shared__ int gen_sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1086,18 +1096,38 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                 // during this one), and the batch's rows, all poses' in turn, are spread over the
                 // wave's lanes in blocks of 64, so that a lane computes one row's column span
                 int base = wave * KP;
+                constexpr bool PREFETCH = !CARRY;  // (a carried window takes those registers)
                 float Rn[9], Sn[2];
-                if (base < np) load_pose(rotb, shb, pose_at(min(base + (pose_lane ? lane : 0), np - 1)), Rn, Sn);
-                for (; base < np; base += NW * KP) {
+                if (PREFETCH && base < np)
+                    load_pose(rotb, shb, pose_at(min(base + (pose_lane ? lane : 0), np - 1)), Rn, Sn);
+                // the window being formed: lanes below m hold samples of earlier batches (their
+                // row, column, pose slot, validity and loaded value), carried until 64 lanes are
+                // filled.  Batch j writes its poses to slot set j mod 2; a window still holding
+                // samples of batch j - 1 when batch j ends is deposited then, as is every window
+                // at the end of the pass.
+                int m = 0, buf = 0;
+                unsigned krw = 0;  // the window sample's pose slot and row (kr_pack)
+                int cc = 0;
+                bool ok = false;
+                Cx<float> v = {0.f, 0.f};
+                float wv = 0.f;
+                for (; base < np; base += NW * KP, buf ^= CARRY ? KP : 0) {
+                    const bool last = base + NW * KP >= np;
+                    bool prev = m > 0;  // the window holds samples of the previous batch
                     const bool sv = pose_lane && base + lane < np;
                     const int pp = pose_at(min(base + (pose_lane ? lane : 0), np - 1));
                     float R[9], Sh[2];
+                    if constexpr (PREFETCH) {
 #pragma unroll
-                    for (int e = 0; e < 9; ++e) R[e] = Rn[e];
-                    Sh[0] = Sn[0];
-                    Sh[1] = Sn[1];
-                    if (base + NW * KP < np)
-                        load_pose(rotb, shb, pose_at(min(base + NW * KP + (pose_lane ? lane : 0), np - 1)), Rn, Sn);
+                        for (int e = 0; e < 9; ++e) R[e] = Rn[e];
+                        Sh[0] = Sn[0];
+                        Sh[1] = Sn[1];
+                        if (base + NW * KP < np)
+                            load_pose(rotb, shb, pose_at(min(base + NW * KP + (pose_lane ? lane : 0), np - 1)), Rn,
+                                      Sn);
+                    } else {
+                        load_pose(rotb, shb, pp, R, Sh);
+                    }
                     int r0 = 0, r1 = -1;
                     if (sv) box_rows<GEN>(R, lo, hi, ts, r0, r1);
                     const int nr = sv ? max(0, r1 - r0 + 1) : 0;
@@ -1105,7 +1135,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                     const int start = rincl - nr;  // the pose's first row in the batch's row list
                     const int rows = __builtin_amdgcn_readlane(rincl, 63);
                     if (sv) {
-                        ScSlot& sd = slots[wave][lane];
+                        ScSlot& sd = slots[wave][buf + lane];
                         sd.R6[0] = R[0];
                         sd.R6[1] = R[1];
                         sd.R6[2] = R[3];
@@ -1120,13 +1150,15 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                     }
                     __builtin_amdgcn_wave_barrier();
                     int pcarry = 0;
-                    for (int rbase = 0; rbase < rows; rbase += 64) {
+                    // (a batch without rows still runs one empty block when a window is carried, to
+                    // deposit it: its samples' slots are overwritten by the next batch)
+                    for (int rbase = 0; rbase < rows || (CARRY && rbase == 0 && m > 0); rbase += 64) {
                         // row rbase + lane of the batch: its pose (the pose lane whose rows hold it)
-                        const int k = window_owner(nr, start, rbase, pcarry, marks[wave]);
+                        const int k = max(0, window_owner(nr, start, rbase, pcarry, marks[wave]));
                         const int f = rbase + lane;
                         int c0 = 0, cnt = 0, r = 0;
                         if (f < rows) {
-                            const ScSlot& sd = slots[wave][k];
+                            const ScSlot& sd = slots[wave][buf + k];
                             float R6[6];
 #pragma unroll
                             for (int e = 0; e < 6; ++e) R6[e] = sd.R6[e];
@@ -1135,55 +1167,101 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                             row_span6(R6, r, lo, hi, ts, cut2, c0, c1);
                             cnt = max(0, c1 - c0 + 1);
                         }
-                        const unsigned kr = kr_pack(k, r);
+                        const unsigned kr = kr_pack(buf + k, r);
                         const int incl = dpp_scan_add(cnt);
                         const int excl = incl - cnt;
                         const int total = __builtin_amdgcn_readlane(incl, 63);
                         const int cx = c0 - excl;  // column of flattened sample e in this row: cx + e
+                        // the batch's last block deposits the window if the pass ends here, or if the
+                        // window would still hold samples of the previous batch
+                        const bool flush = !CARRY || (rbase + 64 >= rows && (last || (prev && m + total < 64)));
                         int carry = 0;
-                        // sample e0 + lane of this row block: owner lane, pixel, validity and the
-                        // element to load (element 0 for lanes without a sample, so that every
-                        // load is issued on every path: a load under a branch makes the compiler
-                        // wait for it before the previous window's taps).  The owner row's pose
-                        // and row come from its lane in one word.
-                        auto locate = [&](int e0, int& rr, int& cc, int& sl, bool& ok, int64_t& pidx) {
+                        // sample e0 + lane of this row block (e < 0: a carried lane): owner lane, pixel,
+                        // validity and the element to load (element 0 for lanes without a sample, so
+                        // that every load is issued on every path: a load under a branch makes the
+                        // compiler wait for it before the previous window's taps).  The owner row's
+                        // pose slot and row come from its lane in one word.
+                        auto locate = [&](int e0, unsigned& krl, int& rr_, int& cc_, int& sl_, bool& ok_,
+                                          int64_t& pidx) {
                             const int e = e0 + lane;
                             const int lw = window_owner(cnt, excl, e0, carry, marks[wave]);
-                            cc = __shfl(cx, lw, 64) + e;
-                            const unsigned krl = unsigned(__shfl(int(kr), lw, 64));
-                            sl = int(krl >> 16);
-                            rr = int(krl & 0xffffu) - int(kRowBias);
-                            ok = e < total;
-                            const ScSlot& sd = slots[wave][sl];
-                            ok = ok && !filtered(float(rr), float(cc), cut2) &&
-                                 !(cc == 0 && (rr == g.n / 2 || rr < 0));  // Friedel half of x = 0
-                            const int pix = int(__umul24(unsigned(rr >= 0 ? rr : rr + g.n), unsigned(g.hp))) + cc;
-                            pidx = ok ? sd.base + pix : 0;
+                            cc_ = __shfl(cx, lw, 64) + e;
+                            krl = unsigned(__shfl(int(kr), lw, 64));
+                            sl_ = int(krl >> 16);
+                            rr_ = int(krl & 0xffffu) - int(kRowBias);
+                            ok_ = (!CARRY || e >= 0) && e < total;
+                            ok_ = ok_ && !filtered(float(rr_), float(cc_), cut2) &&
+                                  !(cc_ == 0 && (rr_ == g.n / 2 || rr_ < 0));  // Friedel half of x = 0
+                            const int pix = int(__umul24(unsigned(rr_ >= 0 ? rr_ : rr_ + g.n), unsigned(g.hp))) + cc_;
+                            pidx = ok_ ? slots[wave][sl_].base + pix : 0;
                         };
-                        int rr, cc, sl;
-                        bool ok;
-                        int64_t pidx;
-                        locate(0, rr, cc, sl, ok, pidx);
-                        Cx<float> v = src[pidx];
-                        float wv = WEIGHTS ? weights[pidx] : 0.f;
-                        for (int e0 = 0; e0 < total; e0 += 64) {
-                            // the next sample's loads are in flight while this one is spread
-                            int rr2 = 0, cc2 = 0, sl2 = 0;
-                            bool ok2 = false;
-                            int64_t pidx2 = 0;
-                            if (e0 + 64 < total) locate(e0 + 64, rr2, cc2, sl2, ok2, pidx2);
-                            const Cx<float> v2 = src[pidx2];
-                            const float wv2 = WEIGHTS ? weights[pidx2] : 0.f;
-                            if (ok)
-                                scatter_sample<CUBIC, MODE, WEIGHTS, OSX>(g, slots[wave][sl], rr, cc, v, wv,
-                                                                     shifts != nullptr, pass == 1, tm, acc_re,
-                                                                     acc_im, acc_w);
-                            rr = rr2;
-                            cc = cc2;
-                            sl = sl2;
-                            ok = ok2;
-                            v = v2;
-                            wv = wv2;
+                        if constexpr (CARRY) {
+                            // the carried lanes stay; the others take samples 0 .. 63 - m of this block.
+                            // Full windows are deposited, the last partial one waits unless flushed.
+                            int e0 = -m;
+                            {
+                                unsigned kr2;
+                                int rr2, cc2, sl2;
+                                bool ok2;
+                                int64_t pidx2;
+                                locate(e0, kr2, rr2, cc2, sl2, ok2, pidx2);
+                                const Cx<float> v2 = src[pidx2];
+                                const float wv2 = WEIGHTS ? weights[pidx2] : 0.f;
+                                const bool keep = lane < m;
+                                krw = keep ? krw : kr2;
+                                cc = keep ? cc : cc2;
+                                ok = keep ? ok : ok2;
+                                v = keep ? v : v2;
+                                wv = keep ? wv : wv2;
+                            }
+                            for (; e0 + 64 <= total || (flush && e0 < total); e0 += 64) {
+                                // the next window's loads are in flight while this one is spread
+                                unsigned kr2 = 0;
+                                int rr2, cc2 = 0, sl2;
+                                bool ok2 = false;
+                                int64_t pidx2 = 0;
+                                if (e0 + 64 < total) locate(e0 + 64, kr2, rr2, cc2, sl2, ok2, pidx2);
+                                const Cx<float> v2 = src[pidx2];
+                                const float wv2 = WEIGHTS ? weights[pidx2] : 0.f;
+                                if (ok)
+                                    scatter_sample<CUBIC, MODE, WEIGHTS, OSX>(
+                                        g, slots[wave][krw >> 16], int(krw & 0xffffu) - int(kRowBias), cc, v, wv,
+                                        shifts != nullptr, pass == 1, tm, acc_re, acc_im, acc_w);
+                                krw = kr2;
+                                cc = cc2;
+                                ok = ok2;
+                                v = v2;
+                                wv = wv2;
+                                prev = false;
+                            }
+                            m = max(0, total - e0);
+                        } else {
+                            unsigned krl;
+                            int rr, cc_w, sl;
+                            bool okw;
+                            int64_t pidx;
+                            locate(0, krl, rr, cc_w, sl, okw, pidx);
+                            Cx<float> vw = src[pidx];
+                            float wvw = WEIGHTS ? weights[pidx] : 0.f;
+                            for (int e0 = 0; e0 < total; e0 += 64) {
+                                // the next window's loads are in flight while this one is spread
+                                int rr2 = 0, cc2 = 0, sl2 = 0;
+                                bool ok2 = false;
+                                int64_t pidx2 = 0;
+                                if (e0 + 64 < total) locate(e0 + 64, krl, rr2, cc2, sl2, ok2, pidx2);
+                                const Cx<float> v2 = src[pidx2];
+                                const float wv2 = WEIGHTS ? weights[pidx2] : 0.f;
+                                if (okw)
+                                    scatter_sample<CUBIC, MODE, WEIGHTS, OSX>(g, slots[wave][sl], rr, cc_w, vw, wvw,
+                                                                         shifts != nullptr, pass == 1, tm, acc_re,
+                                                                         acc_im, acc_w);
+                                rr = rr2;
+                                cc_w = cc2;
+                                sl = sl2;
+                                okw = ok2;
+                                vw = v2;
+                                wvw = wv2;
+                            }
                         }
                     }
                     __builtin_amdgcn_wave_barrier();
@@ -1451,8 +1529,11 @@ hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, co
 template <bool CUBIC, int MODE, bool WEIGHTS, bool OSX>
 hipError_t scatter_kp_osx(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
                           const void* shifts, void* dst, void* wdst, CallPoses* cp, int gl, hipStream_t s) {
-    if (ts.kp_scatter >= 6)
-        return scatter_launch<CUBIC, MODE, WEIGHTS, 6, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
+    // (the cubic stencil carries windows across batches and keeps two pose sets: at most 4 poses)
+    if constexpr (!CUBIC)
+        if (ts.kp_scatter >= 6)
+            return scatter_launch<CUBIC, MODE, WEIGHTS, 6, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl,
+                                                                s);
     if (ts.kp_scatter >= 4)
         return scatter_launch<CUBIC, MODE, WEIGHTS, 4, OSX>(g, ts, src, weights, rot, shifts, dst, wdst, cp, gl, s);
     if (ts.kp_scatter >= 3)
