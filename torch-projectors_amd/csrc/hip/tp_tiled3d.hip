@@ -166,6 +166,21 @@ __device__ __forceinline__ void rotate_slice(const float* __restrict__ R, float 
     x[2] = R[6] * sc + R[7] * sr;
 }
 
+// rotate_slice on the R6 layout (the same products in the same order).
+template <bool OSX>
+__device__ __forceinline__ void rotate_slice6(const float* __restrict__ R6, float r, float c, double os, float* x) {
+    const float sc = OSX ? c * float(os) : float(double(c) * os), sr = OSX ? r * float(os) : float(double(r) * os);
+    x[0] = R6[0] * sc + R6[1] * sr;
+    x[1] = R6[2] * sc + R6[3] * sr;
+    x[2] = R6[4] * sc + R6[5] * sr;
+}
+// row_span on the R6 layout.
+__device__ __forceinline__ void row_span6(const float* R6, int r, const float* lo, const float* hi,
+                                          const TileSpec& ts, float cut2, int& c0, int& c1) {
+    const float R[9] = {R6[0], R6[1], 0.f, R6[2], R6[3], 0.f, R6[4], R6[5], 0.f};
+    row_span(R, r, lo, hi, ts, cut2, c0, c1);
+}
+
 // Per-wave sample queue.  A row block's samples are written once, in
 // flattened order, as packed (slot, c, r) entries; windows of 64 lanes then
 // read their samples straight from the queue.  Rows hold `cnt` samples from
@@ -187,13 +202,24 @@ __device__ __forceinline__ void q_fill(unsigned* q, int r, int c0, int cnt, int 
     for (int e = lo; e < hi; ++e) q[e - q0] = q_pack(r, c0 + (e - excl), slot);
     __builtin_amdgcn_wave_barrier();
 }
+// The same for entries [q0, q0 + room) written after the first `at` entries of the queue.
+__device__ __forceinline__ void q_fill_at(unsigned* q, int at, int r, int c0, int cnt, int excl, int slot, int q0,
+                                          int room) {
+    __builtin_amdgcn_wave_barrier();  // the previous entries have been read
+    const int lo = max(excl, q0), hi = min(excl + cnt, q0 + room);
+    for (int e = lo; e < hi; ++e) q[at + (e - q0)] = q_pack(r, c0 + (e - excl), slot);
+    __builtin_amdgcn_wave_barrier();
+}
 
-// Per-wave copy of the poses of one batch; `base` is the pose's first pixel
-// in the [B, P, n, n/2+1] projections.  The forward's batches also keep the
-// first row of the pose's samples in the box and the index of that row in the
-// batch's flattened row list.
+// Per-wave copy of a pose of a wave batch: columns 0 and 1 of the matrix
+// (R6 = R[0], R[1], R[3], R[4], R[6], R[7]: the tiled kernels read no other
+// entry), the shifts, the pose's first pixel in the [B, P, n, n/2+1]
+// projections, the first row of its samples in the box and the index of that
+// row in the batch's flattened row list.  Kernels that carry a partly filled
+// sample window into the next batch keep two sets per wave (the current
+// batch's and the previous one's, whose samples the carried window may hold).
 struct Slot {
-    float R[9];
+    float R6[6];
     float s0, s1;
     int64_t base;
     int r0, start;
@@ -548,10 +574,21 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
     static_assert(CH <= int(kPoseMask) + 1, "pose index must fit below the flag bits");
     __shared__ unsigned short plist[CH];
     __shared__ int pcount;
-    __shared__ unsigned short gst[GEN ? NW * 128 : 1];  // GEN culling: gathered plane hits per wave
     constexpr int QCAP = 256;
-    __shared__ Slot slots[NW][KP];
-    __shared__ unsigned queue[NW][QCAP];
+    // CARRY (cubic forward): a wave's last, partly filled window of samples waits for its next
+    // batch's samples (a cubic sample's 64 taps make each window costly; 3 % faster), with two
+    // pose sets per wave.  The linear forward measured 1 % slower with it: most of its waves take
+    // only one or two batches of a tile, and a wave's last batch deposits its window anyway.
+    // The sample queues are idle while a phase's poses are culled, so the GEN cull gathers its
+    // plane hits (128 per wave) in their memory.
+    constexpr bool CARRY = FLAT && CUBIC;
+    __shared__ Slot slots[NW][CARRY ? 2 * KP : KP];
+    __shared__ union {
+        unsigned q[NW][QCAP];
+        unsigned short gst[NW][2 * QCAP];
+    } qmem;
+    auto& queue = qmem.q;
+    static_assert(2 * QCAP >= 128, "GEN culling gathers up to 128 plane hits per wave");
     __shared__ unsigned char marks[FLAT ? NW : 1][64];  // FLAT: pose lookup of the batch's rows
     __shared__ int gen_sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -609,7 +646,7 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
         const Cx<VS>* recb = rec + b * g.vol;
         bool loaded = false;
         for (int pbase = p0; pbase < p1; pbase += CH) {
-            const int np = GEN ? cull_chunk_gen<NT, CH>(rotb, p1, pbase, lo, hi, plist, &pcount, gst + wave * 128)
+            const int np = GEN ? cull_chunk_gen<NT, CH>(rotb, p1, pbase, lo, hi, plist, &pcount, qmem.gst[wave])
                                : cull_chunk<NT, false, CH, GEN>(rotb, p1, pbase, lo, hi, lo, hi, plist, &pcount, all_rot);
             if (np == 0) continue;
             auto pose_of = [&](unsigned e) { return pbase + int(e & kPoseMask); };
@@ -668,7 +705,12 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
             int base = wave * KP;
             float Rn[9], Sn[2];
             load_pose(rotb, shifts ? shifts + sb * g.P * 2 : nullptr, pose_of(plist[min(base + slot, np - 1)]), Rn, Sn);
-            for (; base < np; base += NW * KP) {
+            // CARRY: the wave's queue starts with the mq samples of a partly filled window, the first
+            // mprev of them the previous batch's; batch j takes slot set (j mod 2) * KP (buf)
+            int mq = 0, mprev = 0, buf = 0;
+            for (; base < np; base += NW * KP, buf ^= CARRY ? KP : 0) {
+                const bool last = base + NW * KP >= np;
+                mprev = mq;
                 const bool sv = pose_lane && base + slot < np;
                 const int pp = pose_of(plist[min(base + slot, np - 1)]);
                 float R[9], Sh[2];
@@ -693,9 +735,13 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
                 const int start = rincl - nr;
                 const int rows = FLAT ? __builtin_amdgcn_readlane(rincl, 63) : 0;
                 if (jrow == 0 && sv) {
-                    Slot& sd = slots[wave][slot];
-#pragma unroll
-                    for (int e = 0; e < 9; ++e) sd.R[e] = R[e];
+                    Slot& sd = slots[wave][buf + slot];
+                    sd.R6[0] = R[0];
+                    sd.R6[1] = R[1];
+                    sd.R6[2] = R[3];
+                    sd.R6[3] = R[4];
+                    sd.R6[4] = R[6];
+                    sd.R6[5] = R[7];
                     sd.s0 = Sh[0];
                     sd.s1 = Sh[1];
                     sd.base = (b * g.P + pp) * int64_t(g.npix);
@@ -706,21 +752,24 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
                 int pcarry = 0;
                 // row blocks: FLAT, 64 rows of the batch at a time; otherwise RPS rows per pose while
                 // some pose has rows left
-                for (int rbase = 0; FLAT ? rbase < rows : __ballot(nr > rbase) != 0; rbase += RPS) {
+                // (CARRY: a batch without rows still runs one empty block when a window is carried, to
+                // deposit it: its samples' slot set is the next batch's)
+                for (int rbase = 0; FLAT ? rbase < rows || (CARRY && rbase == 0 && mq > 0) : __ballot(nr > rbase) != 0;
+                     rbase += RPS) {
                     int r, c0 = 0, cnt = 0, sk = slot;
                     if constexpr (FLAT) {
                         // row rbase + lane of the batch: its pose (the pose lane whose rows hold it)
-                        sk = window_owner(nr, start, rbase, pcarry, marks[wave]);
+                        sk = max(0, window_owner(nr, start, rbase, pcarry, marks[wave]));
                         const int f = rbase + lane;
                         r = 0;
                         if (f < rows) {
-                            const Slot& sd = slots[wave][sk];
-                            float Rk[9];
+                            const Slot& sd = slots[wave][buf + sk];
+                            float R6[6];
 #pragma unroll
-                            for (int e = 0; e < 9; ++e) Rk[e] = (e % 3 == 2) ? 0.f : sd.R[e];
+                            for (int e = 0; e < 6; ++e) R6[e] = sd.R6[e];
                             r = sd.r0 + (f - sd.start);
                             int c1;
-                            row_span(Rk, r, lo, hi, ts, cut2, c0, c1);
+                            row_span6(R6, r, lo, hi, ts, cut2, c0, c1);
                             cnt = max(0, c1 - c0 + 1);
                         }
                     } else {
@@ -735,25 +784,22 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
                     const int incl = dpp_scan_add(cnt);
                     const int excl = incl - cnt;
                     const int total = __builtin_amdgcn_readlane(incl, 63);
-                    for (int q0 = 0; q0 < total; q0 += QCAP) {
-                      q_fill<QCAP>(queue[wave], r, c0, cnt, excl, sk, q0);
-                      const int m = min(QCAP, total - q0);
-                      for (int e0 = 0; e0 < m; e0 += 64) {
-                        if (e0 + lane >= m) continue;
+                    // queue entry qi: the sample, whose pose is slot `sl` of slot set `sset`
+                    auto sample = [&](int qi, int sset) {
                         int rr, cc, sl;
-                        q_unpack(queue[wave][e0 + lane], rr, cc, sl);
+                        q_unpack(queue[wave][qi], rr, cc, sl);
                         // every field of the sample's pose slot is read before the tests, so that the
                         // reads go out together (one LDS round trip) instead of one per test
-                        const Slot& sdl = slots[wave][sl];
+                        const Slot& sdl = slots[wave][sset + sl];
                         Slot sd;
 #pragma unroll
-                        for (int e = 0; e < 9; ++e) sd.R[e] = (e % 3 == 2) ? 0.f : sdl.R[e];
+                        for (int e = 0; e < 6; ++e) sd.R6[e] = sdl.R6[e];
                         sd.s0 = sdl.s0;
                         sd.s1 = sdl.s1;
                         sd.base = sdl.base;
                         const float fr = float(rr), fc = float(cc);
                         float x[3];
-                        rotate_slice<OSX>(sd.R, fr, fc, g.os, x);
+                        rotate_slice6<OSX>(sd.R6, fr, fc, g.os, x);
                         const int fxc = int(floorf(x[0])), fxr = int(floorf(x[1])), fxd = int(floorf(x[2]));
                         // outside the cutoff, the Friedel half of the x = 0 line (the backward ops skip
                         // it), or not owned by this tile
@@ -761,7 +807,7 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
                         if (GMODE != 0) skip |= (cc == 0) & ((rr == g.n / 2) | (rr < 0));
                         skip |= (fxc < tc) | (fxc >= tc + L) | (fxr < tr) | (fxr >= tr + L) | (fxd < td) | (fxd >= td + LD);
                         asm volatile("" ::"v"(sd.s0), "v"(sd.s1), "v"(int(sd.base)), "v"(int(sd.base >> 32)));
-                        if (skip) continue;
+                        if (skip) return;
                         // staged cell of the tap at floor(x); the interpolation reads its taps at
                         // constant offsets from it (the interpolators split x the same way)
                         const unsigned eb = __umul24(__umul24(unsigned(fxd - (td - LO)), unsigned(W)) + unsigned(fxr - (tr - LO)),
@@ -826,7 +872,41 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
                             const Cx<float> mod = shifts ? cmul(ip.v, ph) : ip.v;
                             grad_terms<KS>(ip, gg, g0, mod, fr, fc, grot != nullptr, gshift != nullptr, sl, acc);
                         }
-                      }
+                    };
+                    if constexpr (CARRY) {
+                        // the batch's last block deposits a partial window if the phase ends here, or if
+                        // the window would still hold samples of the previous batch (whose slot set the
+                        // next batch takes)
+                        const bool flush = rbase + RPS >= rows && (last || (mprev > 0 && mq + total < 64));
+                        for (int q0 = 0;;) {
+                            // entries [q0, q0 + room) of this block follow the mq carried ones
+                            const int room = QCAP - mq;
+                            q_fill_at(queue[wave], mq, r, c0, cnt, excl, sk, q0, room);
+                            const int n = min(room, total - q0), avail = mq + n;
+                            const bool done = q0 + n >= total;
+                            const int wend = done && flush ? avail : (avail & ~63);
+                            for (int e0 = 0; e0 < wend; e0 += 64)
+                                if (e0 + lane < wend) sample(e0 + lane, e0 == 0 && lane < mprev ? buf ^ KP : buf);
+                            if (wend > 0) mprev = 0;
+                            // a partial window waits at the queue's front
+                            const int left = avail - wend;
+                            if (wend > 0 && left > 0) {
+                                const unsigned e = lane < left ? queue[wave][wend + lane] : 0u;
+                                __builtin_amdgcn_wave_barrier();
+                                if (lane < left) queue[wave][lane] = e;
+                                __builtin_amdgcn_wave_barrier();
+                            }
+                            mq = left;
+                            q0 += n;
+                            if (done) break;
+                        }
+                    } else {
+                        for (int q0 = 0; q0 < total; q0 += QCAP) {
+                            q_fill<QCAP>(queue[wave], r, c0, cnt, excl, sk, q0);
+                            const int m = min(QCAP, total - q0);
+                            for (int e0 = 0; e0 < m; e0 += 64)
+                                if (e0 + lane < m) sample(e0 + lane, 0);
+                        }
                     }
                 }
                 if constexpr (GRADS) {
@@ -887,38 +967,12 @@ struct TapMap {
     int lmin[3];
 };
 
-// Per-wave copy of a pose of the scatter's batches: columns 0 and 1 of the
-// matrix (R6 = R[0], R[1], R[3], R[4], R[6], R[7]), the shifts, the pose's
-// first pixel in the projections, the first row of its samples in the box and
-// the index of that row in the batch's flattened row list.  With carried
-// windows a wave keeps two sets (the current batch and the one before, whose
-// samples a carried window may still hold).
-struct ScSlot {
-    float R6[6];
-    float s0, s1;
-    int64_t base;
-    int r0, start;
-};
-// rotate_slice on the R6 layout (the same products in the same order).
-template <bool OSX>
-__device__ __forceinline__ void rotate_slice6(const float* __restrict__ R6, float r, float c, double os, float* x) {
-    const float sc = OSX ? c * float(os) : float(double(c) * os), sr = OSX ? r * float(os) : float(double(r) * os);
-    x[0] = R6[0] * sc + R6[1] * sr;
-    x[1] = R6[2] * sc + R6[3] * sr;
-    x[2] = R6[4] * sc + R6[5] * sr;
-}
-// row_span on the R6 layout.
-__device__ __forceinline__ void row_span6(const float* R6, int r, const float* lo, const float* hi,
-                                          const TileSpec& ts, float cut2, int& c0, int& c1) {
-    const float R[9] = {R6[0], R6[1], 0.f, R6[2], R6[3], 0.f, R6[4], R6[5], 0.f};
-    row_span(R, r, lo, hi, ts, cut2, c0, c1);
-}
 // A sample's row as (batch pose, row) in one word: row + bias in bits 0-15, pose in 16-31.
 constexpr unsigned kRowBias = 0x8000u;
 __device__ __forceinline__ unsigned kr_pack(int k, int r) { return ((unsigned(r) + kRowBias) & 0xffffu) | (unsigned(k) << 16); }
 
 template <bool CUBIC, int MODE, bool WEIGHTS, bool OSX>
-__device__ __forceinline__ void scatter_sample(const Geom& g, const ScSlot& sd, int rr, int cc, Cx<float> v,
+__device__ __forceinline__ void scatter_sample(const Geom& g, const Slot& sd, int rr, int cc, Cx<float> v,
                                                float wpix, bool shifted, bool flip, const TapMap& tm,
                                                double* acc_re, double* acc_im, double* acc_w) {
     constexpr int K = CUBIC ? 4 : 2;  // taps at floor(x) - (CUBIC ? 1 : 0) + j, j < K
@@ -1000,7 +1054,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
     // linear kernels deposit every row block's windows in it.
     constexpr bool CARRY = CUBIC;
     static_assert(!CARRY || KP <= 4, "two pose sets per wave within four workgroups' LDS per CU");
-    __shared__ ScSlot slots[NW][CARRY ? 2 * KP : KP];
+    __shared__ Slot slots[NW][CARRY ? 2 * KP : KP];
     __shared__ unsigned char marks[NW][64];
     __shared__ int gen_sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1135,7 +1189,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                     const int start = rincl - nr;  // the pose's first row in the batch's row list
                     const int rows = __builtin_amdgcn_readlane(rincl, 63);
                     if (sv) {
-                        ScSlot& sd = slots[wave][buf + lane];
+                        Slot& sd = slots[wave][buf + lane];
                         sd.R6[0] = R[0];
                         sd.R6[1] = R[1];
                         sd.R6[2] = R[3];
@@ -1158,7 +1212,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                         const int f = rbase + lane;
                         int c0 = 0, cnt = 0, r = 0;
                         if (f < rows) {
-                            const ScSlot& sd = slots[wave][buf + k];
+                            const Slot& sd = slots[wave][buf + k];
                             float R6[6];
 #pragma unroll
                             for (int e = 0; e < 6; ++e) R6[e] = sd.R6[e];
