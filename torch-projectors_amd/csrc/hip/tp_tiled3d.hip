@@ -574,7 +574,9 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
     static_assert(CH <= int(kPoseMask) + 1, "pose index must fit below the flag bits");
     __shared__ unsigned short plist[CH];
     __shared__ int pcount;
-    constexpr int QCAP = 256;
+    // sample queue entries per wave (the backprojection backward's second staged tile takes LDS,
+    // and a workgroup above 53760 bytes leaves two per CU: LDS is allocated in 1280-byte granules)
+    constexpr int QCAP = (GMODE == 2 && WG) ? 192 : 256;
     // CARRY (cubic forward): a wave's last, partly filled window of samples waits for its next
     // batch's samples (a cubic sample's 64 taps make each window costly; 3 % faster), with two
     // pose sets per wave.  The linear forward measured 1 % slower with it: most of its waves take
