@@ -247,16 +247,21 @@ tp::TileSpec2 tile_spec2(const tp::Geom& g, bool cubic) {
     ts.cmax = std::min(g.n / 2, cl);
     ts.rmin = std::max(g.n / 2 + 1 - g.n, -cl);
     ts.rmax = std::min(g.n / 2, cl);
-    // gather: square tiles over the signed plane within the radius (+2), pose ranges as the scatter
+    // gather: square tiles over the signed plane within the radius (+2), and pose ranges
     constexpr int GT = tp::kGat2;
     const int half_g = int(std::ceil((rho_unit + 3.0) / GT)), half_g2 = int(std::ceil((rho + 2.0) / GT));
     ts.gnt = 2 * half_g;
     ts.gorg = -half_g * GT;
     ts.gnt2 = 2 * half_g2;
     ts.gorg2 = -half_g2 * GT;
+    // A gather's pose range writes only its own poses' pixels (its pose-gradient atomics are one
+    // set per tile and pose whatever the ranges), so its ranges go down to 16 poses: a small call
+    // (256 poses over 64 tiles) then fills the GPU, where ranges of at least 128 left it 128 work
+    // items.
     const int64_t gtiles = g.B * int64_t(ts.gnt) * ts.gnt;
     const int64_t gwant = gtiles > 0 ? (4096 + gtiles - 1) / gtiles : 1;
-    ts.gksplit = int(std::max<int64_t>(1, std::min(gwant, most)));
+    const int64_t gmost = std::max<int64_t>(1, g.P / 16);
+    ts.gksplit = int(std::max<int64_t>(1, std::min(gwant, gmost)));
     ts.gprange = int((g.P + ts.gksplit - 1) / ts.gksplit);
     const double gw = GT + 2.0 * ts.eps;
     const int grows = int(std::ceil(std::sqrt(2.0) * gw / g.os)) + 2;
