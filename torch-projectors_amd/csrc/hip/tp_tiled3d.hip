@@ -39,14 +39,15 @@
 //                workgroup per work item over the grid their samples reach;
 //   GEN = true   the other tiled poses (scaled, anisotropically magnified or
 //                sheared matrices), launched after the first on a small
-//                persistent grid.  Its workgroups first find the call's
-//                largest singular value among such poses, and exit at once
-//                when there is none, so rotation-only calls pay one short
-//                launch.  A sample x = sc a + sr b of such a pose has
-//                sc = as . x and sr = bs . x with the dual basis (as, bs),
-//                which bounds the rows and the half plane sc >= 0 that can
-//                reach a box; the grid reaches samples up to kScaleMax times
-//                farther out.  Scatters add their tiles into the volume.
+//                persistent grid.  A per-call pre-pass (k_call_poses)
+//                records the largest singular value among such poses; the
+//                workgroups exit at once when there is none, so rotation-only
+//                calls pay one short launch.  A sample x = sc a + sr b of
+//                such a pose has sc = as . x and sr = bs . x with the dual
+//                basis (as, bs), which bounds the rows and the half plane
+//                sc >= 0 that can reach a box; the grid reaches samples up to
+//                kScaleMax times farther out.  Scatters add their tiles into
+//                the volume.
 #include <type_traits>
 
 #include "tp_device.hh"
