@@ -58,7 +58,11 @@ def build_lib(jobs=8):
 
     def compile_one(src):
         obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-        _run([HIPCC, *KERNEL_FLAGS, "-c", src, "-o", obj])
+        # the compiler's per-kernel register / scratch / LDS / occupancy report, kept beside the
+        # object (tests/test_kernel_resources_cpu.py checks the budgets of the tiled kernels)
+        out = _run([HIPCC, *KERNEL_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", src, "-o", obj])
+        with open(os.path.join(BUILD, os.path.basename(src) + ".resources.txt"), "w") as f:
+            f.write(out)
         return obj
 
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
