@@ -38,11 +38,15 @@
 //   GEN = false  rotations (columns orthonormal to kRotationTol), one
 //                workgroup per work item over the grid their samples reach;
 //   GEN = true   the other tiled poses (scaled, anisotropically magnified or
-//                sheared matrices), launched after the first on a small
-//                persistent grid.  A per-call pre-pass (k_call_poses)
-//                records the largest singular value among such poses; the
-//                workgroups exit at once when there is none, so rotation-only
-//                calls pay one short launch.  A sample x = sc a + sr b of
+//                sheared matrices), launched after the first on a smaller
+//                grid (the forward's: a quarter of the rotation grid's
+//                workgroups, each stepping over the slots; the scatter's:
+//                persistent, with per-XCD counters).  A per-call pre-pass
+//                (k_call_poses) records the largest singular value among
+//                such poses; the workgroups exit at once when there is none,
+//                so rotation-only calls pay one short launch (and the
+//                rotation kernels, when the call has no rotation, exit at
+//                their first slot).  A sample x = sc a + sr b of
 //                such a pose has sc = as . x and sr = bs . x with the dual
 //                basis (as, bs), which bounds the rows and the half plane
 //                sc >= 0 that can reach a box; the grid reaches samples up to
@@ -624,7 +628,9 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
     const int64_t items = g.B * (int64_t(fc1 - fc0) * (fc1 - fc0) * (fd1 - fd0) * ts.ksplit + int64_t(nt) * nt * ntd);
     const float cut2 = float(g.cut2);
     const int N = g.N, H = g.H;
-    for (Slots<GEN> sl(xcd_per<kRunForw>(items), slot_counters<GEN>(cp, gl), &gen_sh); sl.ok(); sl.next(&gen_sh)) {
+    // (GEN: the grid holds a quarter of the rotation kernel's slots and steps over the rest)
+    for (Slots<false> sl(xcd_per<kRunForw>(items), nullptr, &gen_sh); sl.ok(); sl.next(&gen_sh)) {
+        if (!any_rot) return;  // rotation kernel, no rotation in the call (its flags were read above)
         const int64_t slot_i = sl.s;
         const int64_t w = xcd_item<kRunForw>(slot_i);
         if (w >= items) continue;
@@ -643,7 +649,6 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
             dist2 += q * q;
         }
         if (dist2 > rho2) continue;
-        if (!any_rot) return;  // rotation kernel, no rotation in the call
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
         const float* rotb = rot + rb * g.P * 9;
         const Cx<VS>* recb = rec + b * g.vol;
@@ -1077,13 +1082,13 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
         if (!(rho_k > 0.f)) return;  // no such pose in this call
     }
     for (Slots<GEN> sl(xcd_per<kRunScatter>(items), slot_counters<GEN>(cp, gl), &gen_sh); sl.ok(); sl.next(&gen_sh)) {
+        if (!GEN && !any_rot && call_reach(&cp->gen_reach) > 0.f) return;  // GEN stores every tile
         const int64_t slot_i = sl.s;
         const int64_t w = xcd_item<kRunScatter>(slot_i);
         if (w >= items) continue;
         const Item it = item_of(w, g.B, int(g.P), ts.ntd, ts.ntr, ts.ntc, ts.sd0, ts.sd1, ts.sr0, ts.sr1, 0, ts.sc1,
                                 ts.ksplit, ts.prange);
         if (it.skip) continue;
-        if (!GEN && !any_rot && call_reach(&cp->gen_reach) > 0.f) return;  // GEN stores every tile
         const int64_t b = it.b;
         // stored cells of this tile, signed coordinates: d, r in [-N/2+1, N/2], c in [0, N/2]
         const int tc = it.kc * SC, tr = -half + 1 + it.kr * SR, td = -half + 1 + it.kd * SD;
@@ -1507,22 +1512,32 @@ __global__ __launch_bounds__(kBinThreads) void k_pose_bins(Geom g, const float* 
     }
 }
 
-// Work items of the forward tile grid: the unit grid (rotations), or for GEN the whole wide
-// grid, a bound on the part of it that a call's reach selects (the kernel's persistent grid).
-template <bool GEN>
+// Work items of the rotation kernels' forward tile grid (the unit grid).
 int64_t forw_items(const Geom& g, const TileSpec& ts) {
-    const int nt = GEN ? ts.nt2 : ts.nt, ntd = GEN ? ts.ntfd2 : ts.ntfd;
-    const int fc = GEN ? ts.fc1_2 - ts.fc0_2 : ts.fc1 - ts.fc0, fd = GEN ? ts.fd1_2 - ts.fd0_2 : ts.fd1 - ts.fd0;
-    return g.B * (int64_t(fc) * fc * fd * ts.ksplit + int64_t(nt) * nt * ntd);
+    const int fc = ts.fc1 - ts.fc0, fd = ts.fd1 - ts.fd0;
+    return g.B * (int64_t(fc) * fc * fd * ts.ksplit + int64_t(ts.nt) * ts.nt * ts.ntfd);
 }
 // Workgroups of a launch of `kernel` over `items`: one per item (rotations), or the persistent
-// GEN grid.
+// GEN grid (the scatter's).
 template <bool GEN, int RUN>
 unsigned grid_of(int64_t items, const void* kernel, int threads) {
     const int64_t slots = kXcds * xcd_per<RUN>(items);
     if (!GEN) return grid_for(slots);
     const int64_t most = gen_grid(kernel, threads);
     return grid_for(slots > most ? most : slots);
+}
+
+// GEN forward-family grid: a quarter of the rotation kernel's slots (a multiple of kXcds), each
+// workgroup stepping over the GEN grid's slots by the grid size.  As many workgroups as the
+// rotation kernel's would make a call without such poses pay for their empty launch (about 10 us
+// at the headline); a persistent grid (a multiple of kXcds workgroups per CU) balances the tiles'
+// uneven work worse: at poses scaled by 1.02 the forward took 0.87 ms with the persistent grid
+// and per-XCD counters, 0.77 / 0.74 / 0.74 ms with an eighth / a quarter / half of the rotation
+// slots, 0.83 ms with a sixteenth (and 1.29 against 1.69 ms with poses scaled by 1.4).
+constexpr int kGenForwShare = 4;
+inline unsigned gen_forw_grid(const Geom& g, const TileSpec& ts) {
+    const int64_t w = kXcds * xcd_per<kRunForw>(forw_items(g, ts)) / kGenForwShare;
+    return grid_for(std::max<int64_t>(kXcds, (w + kXcds - 1) / kXcds * kXcds));
 }
 
 // One forward-family kernel (GMODE 0, 1, 2) for rotations, then for the other tiled poses.
@@ -1532,13 +1547,13 @@ hipError_t forw_both(const Geom& g, const TileSpec& ts, const void* rec, const v
                      void* wout, hipStream_t s) {
     const auto kr = k_forw3_tiled<CUBIC, KP, OSX, GMODE, RS, WG, VS, false>;
     const auto kg = k_forw3_tiled<CUBIC, KP, OSX, GMODE, RS, WG, VS, true>;
-    hipLaunchKernelGGL(kr, dim3(grid_of<false, kRunForw>(forw_items<false>(g, ts), (const void*)kr, kForwThreads)),
+    hipLaunchKernelGGL(kr, dim3(grid_of<false, kRunForw>(forw_items(g, ts), (const void*)kr, kForwThreads)),
                        dim3(kForwThreads), 0, s, g, ts,
                        (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out, cp, gl,
                        (const Cx<float>*)gsrc, (float*)grot, (float*)gshift, (const float*)gw, (float*)wout);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kg, dim3(grid_of<true, kRunForw>(forw_items<true>(g, ts), (const void*)kg, kForwThreads)),
+    hipLaunchKernelGGL(kg, dim3(gen_forw_grid(g, ts)),
                        dim3(kForwThreads), 0, s, g, ts,
                        (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out, cp, gl,
                        (const Cx<float>*)gsrc, (float*)grot, (float*)gshift, (const float*)gw, (float*)wout);

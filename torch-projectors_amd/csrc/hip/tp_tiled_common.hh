@@ -181,11 +181,15 @@ template <bool GEN>
 __device__ __forceinline__ unsigned* slot_counters(CallPoses* cp, int gl) { return cp->next[2 * gl + (GEN ? 1 : 0)]; }
 // Fields of the call summary read with a vector load where they are used (a
 // scalar load is hoisted to the kernel's start and waited for with the next).
+// The pre-pass wrote them in an earlier kernel of the stream, so an L2-cached
+// load sees them: a relaxed atomic of workgroup scope is such a load (an agent-
+// scope one bypasses the L2 on every workgroup of a one-per-tile grid: a call
+// without rotations spent 85 us in each rotation kernel's empty workgroups).
 __device__ __forceinline__ int call_flag(const int* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 __device__ __forceinline__ float call_reach(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // Tiles per half axis of a tile grid with edge `edge` centred on the origin
