@@ -10,6 +10,12 @@ the backprojected volumes within relative L2 1e-5 (they differ only in the order
 The second test captures calls that do use the stream's pose bins (the warm-up had as many poses),
 then grows that workspace with an eager call of twice the poses on the same stream: the replays
 must still read the workspace the capture recorded, which stays allocated.
+
+The third captures a forward that uses the stream's list of the rotation kernels' work items in
+reach (made by the warm-up of the same geometry), then runs forwards of five other geometries on
+the capture stream, which replace every list the stream keeps (four): the replays must still read
+the list the capture recorded, and the other geometries' forwards must equal the same calls on
+another stream.
 """
 import pytest
 import torch
@@ -149,3 +155,43 @@ def test_fourier_transforms_replayed_after_plan_eviction(gpu):
         print(f"[graph] fourier replay {replay}", flush=True)
         assert _rel(spec_g, spec_e) <= 1e-6, f"replay {replay}: spectrum {_rel(spec_g, spec_e):.3e}"
         assert _rel(back_g, back_e) <= 1e-6, f"replay {replay}: inverse {_rel(back_g, back_e):.3e}"
+
+
+def test_replay_after_the_forward_lists_turned_over(gpu):
+    T = torch.ops.torch_projectors
+    gen = torch.Generator().manual_seed(8100)
+    P, n, os_, N = 24, 32, 2.0, 64
+    vol = torch.randn(1, N, N, N // 2 + 1, generator=gen, dtype=torch.complex64).to(gpu)
+    rot = _rotations(P, gen).to(gpu)
+    sh = (torch.rand(1, P, 2, generator=gen) * 4 - 2).to(gpu)
+
+    def fwd(v, r, s, m):
+        return T.project_3d_to_2d_forw(v, r, s, [m, m], "linear", os_, None)
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fwd(vol, rot, sh, n)  # the stream's area, with the list of this geometry
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        proj_g = fwd(vol, rot, sh, n)
+    torch.cuda.synchronize()
+
+    others = [(16, 64), (24, 64), (40, 64), (48, 64), (16, 32)]  # (projection size, volume size)
+    vols = {m: torch.randn(1, m, m, m // 2 + 1, generator=gen, dtype=torch.complex64).to(gpu) for m in (32, 64)}
+    for replay in range(3):
+        with torch.cuda.stream(stream):
+            outs = [fwd(vols[vn], rot, sh, pn) for pn, vn in others]  # new lists on the capture stream
+        torch.cuda.synchronize()
+        for (pn, vn), o in zip(others, outs):
+            assert torch.equal(o, fwd(vols[vn], rot, sh, pn)), f"geometry n={pn} N={vn} differs between streams"
+        graph.replay()
+        torch.cuda.synchronize()
+        proj_e = fwd(vol, rot, sh, n)
+        torch.cuda.synchronize()
+        print(f"[graph] replay {replay} after the lists turned over", flush=True)
+        assert torch.equal(proj_g, proj_e), f"replay {replay}: projections differ"
+

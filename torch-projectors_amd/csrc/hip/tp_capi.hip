@@ -11,6 +11,7 @@
 // tp_project_3d_to_2d_forw_noalloc uses a static device array instead.
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -305,6 +306,19 @@ struct StreamScratch {
     // until the process ends; growth is geometric, so these stay a small multiple of the last).
     bool bins_captured = false;
     std::vector<void*> bins_retired;
+    // The rotation forward kernels' lists of work items in reach (tp::TileSpec::flist) of the
+    // last few geometries; a list that a capture has used is retired in the same way.
+    struct ForwList {
+        std::vector<int64_t> key;
+        int* p = nullptr;
+        size_t cap = 0;
+        int64_t count = 0;
+        bool captured = false;
+        uint64_t used = 0;
+    };
+    ForwList flists[4];
+    uint64_t flist_tick = 0;
+    std::vector<void*> flist_retired;
 };
 std::mutex g_scratch_mu;
 std::map<std::pair<int, hipStream_t>, std::unique_ptr<StreamScratch>> g_scratch;
@@ -398,6 +412,75 @@ struct CallScratch {
         if (capturing) area->bins_captured = true;
         return area->bins;
     }
+    // The rotation forward kernels' list of work items in reach for the geometry of g and ts
+    // (tp::forw_reach_items), or nullptr (the kernels then take every work item of their grid).
+    // The area keeps the lists of its last four geometries; another geometry is listed on the host
+    // and copied in on the call's stream, which is then synchronised (once per new geometry). A
+    // stream under graph capture takes a list that the area holds for its geometry, else none, and
+    // a list that a capture has used is retired, never rewritten or freed.
+    const int* forw_list(const tp::Geom& g, const tp::TileSpec& ts, hipStream_t st, int64_t& count) {
+        if (static_area || !area) return nullptr;
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        const bool capturing = cs != hipStreamCaptureStatusNone;
+        uint32_t rho_bits = 0, eps_bits = 0;
+        std::memcpy(&rho_bits, &ts.rho_unit, 4);
+        std::memcpy(&eps_bits, &ts.eps, 4);
+        // everything the list depends on (the pose count only through ksplit)
+        const std::vector<int64_t> key{g.B, ts.nt, ts.org, ts.ntfd, ts.orgd, ts.fc0, ts.fc1, ts.fd0, ts.fd1,
+                                       ts.ksplit, int64_t(rho_bits), int64_t(eps_bits)};
+        StreamScratch::ForwList* victim = nullptr;
+        for (StreamScratch::ForwList& f : area->flists) {
+            if (f.p && f.key == key) {
+                f.used = ++area->flist_tick;
+                if (capturing) f.captured = true;
+                count = f.count;
+                return f.p;
+            }
+            if (!victim || (victim->p && (!f.p || f.used < victim->used))) victim = &f;
+        }
+        if (capturing) return nullptr;
+        std::vector<int> host;
+        const int64_t items = tp::forw_reach_items(g, ts, host);
+        if (items > int64_t(INT32_MAX) || host.empty()) return nullptr;
+        const size_t need = host.size() * sizeof(int);
+        // queued work may still read the list that is replaced
+        if (hipStreamSynchronize(st) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        StreamScratch::ForwList& f = *victim;
+        f.key.clear();
+        if (f.p && (f.captured || need > f.cap)) {
+            if (f.captured) area->flist_retired.push_back(f.p);
+            else (void)hipFree(f.p);
+            f.p = nullptr;
+            f.cap = 0;
+            f.captured = false;
+        }
+        if (!f.p) {
+            const size_t cap = need + need / 4;
+            if (hipMalloc(reinterpret_cast<void**>(&f.p), cap) != hipSuccess) {
+                f.p = nullptr;
+                (void)hipGetLastError();
+                return nullptr;
+            }
+            f.cap = cap;
+        }
+        if (hipMemcpyAsync(f.p, host.data(), need, hipMemcpyHostToDevice, st) != hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        f.key = key;
+        f.count = int64_t(host.size());
+        f.used = ++area->flist_tick;
+        count = f.count;
+        return f.p;
+    }
     int get(hipStream_t st) {
         if (p) return TP_OK;
         if (static_area) {
@@ -481,6 +564,16 @@ int make_bins(bool cubic, const tp::Geom& g, tp::TileSpec& ts, const void* rot, 
     return TP_OK;
 }
 
+// The rotation forward kernels' work items in reach (tp::TileSpec::flist), when the call's
+// (device, stream) area can hold them.
+int use_forw_list(const tp::Geom& g, tp::TileSpec& ts, CallScratch& sc, hipStream_t s) {
+    TP_TRY(sc.get(s));
+    int64_t count = 0;
+    ts.flist = sc.forw_list(g, ts, s, count);
+    ts.fcount = ts.flist ? count : 0;
+    return TP_OK;
+}
+
 // TP_F16S: the volume is stored as complex half; it is widened exactly to
 // fp32 on load and everything else (poses, arithmetic, projections) is the
 // TP_F32 path.
@@ -508,6 +601,7 @@ int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int6
     if (use_tiles(dim, dt, os, n)) {
         tp::TileSpec ts = tile_spec(g, cubic);
         TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(use_forw_list(g, ts, sc, s));
         TP_TRY(launched(tp::launch_project3_forw_tiled(cubic, g, ts, rec, rot, shifts, out, sc.p, 0, s, rec_half),
                         "tiled projection launch"));
         return launched(tp::launch_project_forw(dim, kdt, cubic, g, rec, rot, shifts, out, s, true),
@@ -564,6 +658,7 @@ int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, in
         tp::TileSpec ts = tile_spec(g, cubic);
         TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s));
         TP_TRY(make_bins(cubic, g, ts, rot, sc, s));
+        TP_TRY(use_forw_list(g, ts, sc, s));
         TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, sc.p, 0,
                                                   s),
                         "tiled reconstruction-gradient launch"));
@@ -664,6 +759,7 @@ int backproject_back(int dim, int dtype, const void* gdata, const void* gw, int6
     if (tiles) {
         tp::TileSpec ts = tile_spec(g, cubic);
         TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s));
+        TP_TRY(use_forw_list(g, ts, sc, s));
         TP_TRY(launched(tp::launch_bpback3_tiled(cubic, g, ts, gdata, gw, proj, rot, shifts, gproj, gweights, grot,
                                                  gshift, sc.p, 0, s),
                         "tiled backprojection backward launch"));

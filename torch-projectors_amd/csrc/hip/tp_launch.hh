@@ -4,6 +4,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <vector>
 #include <stdint.h>
 
 namespace tp {
@@ -83,7 +85,17 @@ struct TileSpec {
     int kp_forw, kp_scatter;
     bool os_exact;            // float(os) == os: c * os can be formed in float exactly as in double
     BinGrid sbins;            // pose bins of the scatter tile grid (list null: none)
+    // forward: the rotation kernels' work items whose tiles the rotations' samples can reach, in
+    // work-item order (forw_reach_items), fcount of them; flist null: every work item of the grid
+    // (about half of the headline's tiles lie outside that sphere)
+    const int* flist;
+    int64_t fcount;
 };
+
+// The work items of the rotation kernels' forward tile grid (ts's nt, ntfd, core tiles and
+// ksplit) whose tiles lie within rho_unit + 1 (and a margin) of the origin, in increasing order,
+// appended to `out`; returns the grid's item count.  Host code, for TileSpec::flist.
+int64_t forw_reach_items(const Geom& g, const TileSpec& ts, std::vector<int>& out);
 
 // Tile-owner kernels of the fp32 2D operators (tp_tiled2d.hip).
 constexpr int kTile2C = 32, kTile2R = 16;  // scatter tile edges (c, r): fp64 accumulators

@@ -260,7 +260,7 @@ struct Item {
     int p0, p1;
     bool core, skip;
 };
-__device__ __forceinline__ Item item_of(int64_t w, int64_t B, int P, int nd, int nr, int nc, int d0, int d1, int r0,
+__host__ __device__ inline Item item_of(int64_t w, int64_t B, int P, int nd, int nr, int nc, int d0, int d1, int r0,
                                         int r1, int c0, int c1, int ksplit, int prange) {
     Item it;
     const int cd = d1 - d0, cr = r1 - r0, cc = c1 - c0;
@@ -625,15 +625,20 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
         fd1 = min(ntd, max(fd0, ts.fd1_2 - offd));
     }
     const float rho2 = rho_k * rho_k;
-    const int64_t items = g.B * (int64_t(fc1 - fc0) * (fc1 - fc0) * (fd1 - fd0) * ts.ksplit + int64_t(nt) * nt * ntd);
+    int64_t items = g.B * (int64_t(fc1 - fc0) * (fc1 - fc0) * (fd1 - fd0) * ts.ksplit + int64_t(nt) * nt * ntd);
+    // rotations: the slots may index the list of the work items in reach (the others' workgroups
+    // would only start and leave)
+    const int* __restrict__ flist = GEN ? nullptr : ts.flist;
+    if (flist) items = ts.fcount;
     const float cut2 = float(g.cut2);
     const int N = g.N, H = g.H;
     // (GEN: the grid holds a quarter of the rotation kernel's slots and steps over the rest)
     for (Slots<false> sl(xcd_per<kRunForw>(items), nullptr, &gen_sh); sl.ok(); sl.next(&gen_sh)) {
         if (!any_rot) return;  // rotation kernel, no rotation in the call (its flags were read above)
         const int64_t slot_i = sl.s;
-        const int64_t w = xcd_item<kRunForw>(slot_i);
-        if (w >= items) continue;
+        const int64_t wi = xcd_item<kRunForw>(slot_i);
+        if (wi >= items) continue;
+        const int64_t w = flist ? int64_t(flist[wi]) : wi;
         const Item it = item_of(w, g.B, int(g.P), ntd, nt, nt, fd0, fd1, fc0, fc1, fc0, fc1, ts.ksplit, ts.prange);
         if (it.skip) continue;
         const int64_t b = it.b;
@@ -1547,7 +1552,8 @@ hipError_t forw_both(const Geom& g, const TileSpec& ts, const void* rec, const v
                      void* wout, hipStream_t s) {
     const auto kr = k_forw3_tiled<CUBIC, KP, OSX, GMODE, RS, WG, VS, false>;
     const auto kg = k_forw3_tiled<CUBIC, KP, OSX, GMODE, RS, WG, VS, true>;
-    hipLaunchKernelGGL(kr, dim3(grid_of<false, kRunForw>(forw_items(g, ts), (const void*)kr, kForwThreads)),
+    const int64_t rot_items = ts.flist ? ts.fcount : forw_items(g, ts);
+    hipLaunchKernelGGL(kr, dim3(grid_of<false, kRunForw>(rot_items, (const void*)kr, kForwThreads)),
                        dim3(kForwThreads), 0, s, g, ts,
                        (const Cx<VS>*)rec, (const float*)rot, (const float*)shifts, (Cx<float>*)out, cp, gl,
                        (const Cx<float>*)gsrc, (float*)grot, (float*)gshift, (const float*)gw, (float*)wout);
@@ -1665,6 +1671,28 @@ hipError_t forw_store(bool cubic, const Geom& g, const TileSpec& ts, const void*
 }
 
 }  // namespace
+
+int64_t forw_reach_items(const Geom& g, const TileSpec& ts, std::vector<int>& out) {
+    const int64_t items = forw_items(g, ts);
+    // the rotation kernel's test (dist2 > rho2: the tile holds no sample) with a margin, so that
+    // every tile the kernel would take is listed whatever the rounding
+    const float rho = ts.rho_unit + 1.0f, rho2 = rho * rho * 1.001f + 4.0f;
+    for (int64_t w = 0; w < items; ++w) {
+        const Item it = item_of(w, g.B, int(g.P), ts.ntfd, ts.nt, ts.nt, ts.fd0, ts.fd1, ts.fc0, ts.fc1, ts.fc0,
+                                ts.fc1, ts.ksplit, ts.prange);
+        if (it.skip) continue;
+        const int tc = ts.org + it.kc * L, tr = ts.org + it.kr * L, td = ts.orgd + it.kd * LD;
+        const float lo[3] = {float(tc) - ts.eps, float(tr) - ts.eps, float(td) - ts.eps};
+        const float hi[3] = {float(tc + L) + ts.eps, float(tr + L) + ts.eps, float(td + LD) + ts.eps};
+        float dist2 = 0.f;
+        for (int k = 0; k < 3; ++k) {
+            const float q = lo[k] > 0.f ? lo[k] : (hi[k] < 0.f ? -hi[k] : 0.f);
+            dist2 += q * q;
+        }
+        if (dist2 <= rho2) out.push_back(int(w));
+    }
+    return items;
+}
 
 hipError_t launch_pose_bins(const Geom& g, const void* rot, const BinGrid& bg, const BinBox& bb, const CallPoses* cp,
                             hipStream_t s) {
