@@ -521,21 +521,27 @@ struct CallScratch {
     }
 };
 
-// Summary of the call's poses for its tiled kernels (tp::launch_call_poses).
-int call_poses(int dim, const tp::Geom& g, const void* rot, float rho_unit, CallScratch& sc, hipStream_t s) {
+// Summary of the call's poses for its tiled kernels (tp::launch_call_poses), which also clears the
+// counts of the pose bins that plan_bins laid out in ts (if any).
+int call_poses(int dim, const tp::Geom& g, const void* rot, float rho_unit, CallScratch& sc, hipStream_t s,
+               const tp::TileSpec* ts = nullptr) {
     TP_TRY(sc.get(s));
-    return launched(tp::launch_call_poses(dim, g.B_rot * g.P, rot, rho_unit, sc.p, s), "pose summary launch");
+    int* zero = ts && ts->sbins.list ? ts->sbins.count : nullptr;
+    const int64_t nzero = zero ? g.B_rot * int64_t(ts->sbins.n) : 0;
+    return launched(tp::launch_call_poses(dim, g.B_rot * g.P, rot, rho_unit, sc.p, s, zero, nzero),
+                    "pose summary launch");
 }
 
-// Pose bins of the tiled 3D scatter's tile grid for this call (tp::BinGrid), in 2 x 2 x 2 tiles,
-// filled by launch_pose_bins after the call's pose summary.  None below kBinsMinPoses poses,
-// from 65536 poses (list entries are 16-bit), beyond kBinsMaxBytes or tp::kBinMaxGroups
-// workgroups of the pre-pass, and none without a workspace: the scatter then culls every pose of
-// each tile.
+// Pose bins of the tiled 3D scatter's tile grid for this call (tp::BinGrid), in 2 x 2 x 2 tiles:
+// plan_bins lays them out in the stream's workspace (ts.sbins; the pose summary then clears their
+// counts) and fill_bins fills them after the summary.  None below kBinsMinPoses poses, from 65536
+// poses (list entries are 16-bit), beyond kBinsMaxBytes or tp::kBinMaxGroups workgroups of the
+// pre-pass, and none without a workspace: the scatter then culls every pose of each tile.
 constexpr int64_t kBinsMinPoses = 16;
 constexpr size_t kBinsMaxBytes = size_t(1) << 30;
-int make_bins(bool cubic, const tp::Geom& g, tp::TileSpec& ts, const void* rot, CallScratch& sc, hipStream_t s) {
+int plan_bins(const tp::Geom& g, tp::TileSpec& ts, CallScratch& sc, hipStream_t s) {
     ts.sbins = tp::BinGrid{};
+    TP_TRY(sc.get(s));
     if (g.P < kBinsMinPoses || g.P >= 65536) return TP_OK;
     tp::BinGrid sb{};
     sb.nb[0] = (ts.ntc + 1) / 2;
@@ -552,6 +558,15 @@ int make_bins(bool cubic, const tp::Geom& g, tp::TileSpec& ts, const void* rot, 
     if (!w) return TP_OK;
     sb.count = reinterpret_cast<int*>(w);
     sb.list = reinterpret_cast<unsigned short*>(w + counts);
+    ts.sbins = sb;
+    return TP_OK;
+}
+// The bins' pre-pass, which also zeroes the core tiles' cells of dst and wdst (dst null: not; the
+// scatter then zeroes them itself).
+int fill_bins(bool cubic, const tp::Geom& g, tp::TileSpec& ts, const void* rot, void* dst, void* wdst,
+              CallScratch& sc, hipStream_t s) {
+    ts.core_zeroed = false;
+    if (!ts.sbins.list) return TP_OK;
     // a bin's box holds its tiles' box-1 boxes (the tile dilated by the stencil and the slack) with
     // half a voxel to spare
     const float half = float(g.N / 2), pad = 0.5f;
@@ -559,8 +574,8 @@ int make_bins(bool cubic, const tp::Geom& g, tp::TileSpec& ts, const void* rot, 
     const tp::BinBox bb{{0.f, -half + 1.f, -half + 1.f},
                         {2.f * tp::kScTC, 2.f * tp::kScTR, 2.f * tp::kScTD},
                         sl + ts.eps + pad, sh + ts.eps + pad, ts.rho_unit + 1.0f};
-    TP_TRY(launched(tp::launch_pose_bins(g, rot, sb, bb, sc.p, s), "pose-bin launch"));
-    ts.sbins = sb;
+    TP_TRY(launched(tp::launch_pose_bins(g, rot, ts.sbins, bb, sc.p, s, ts, dst, wdst), "pose-bin launch"));
+    ts.core_zeroed = dst != nullptr;
     return TP_OK;
 }
 
@@ -656,8 +671,9 @@ int project_back(int dim, int dtype, const void* gproj, int64_t B, int64_t P, in
     CallScratch sc;
     if (tiles) {
         tp::TileSpec ts = tile_spec(g, cubic);
-        TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s));
-        TP_TRY(make_bins(cubic, g, ts, rot, sc, s));
+        TP_TRY(plan_bins(g, ts, sc, s));
+        TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s, &ts));
+        TP_TRY(fill_bins(cubic, g, ts, rot, grec, nullptr, sc, s));
         TP_TRY(use_forw_list(g, ts, sc, s));
         TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 1, g, ts, gproj, nullptr, rot, shifts, grec, nullptr, sc.p, 0,
                                                   s),
@@ -710,8 +726,9 @@ int backproject_forw(int dim, int dtype, const void* proj, int64_t B, int64_t P,
     CallScratch sc;
     if (tiles) {
         tp::TileSpec ts = tile_spec(g, cubic);
-        TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s));
-        TP_TRY(make_bins(cubic, g, ts, rot, sc, s));
+        TP_TRY(plan_bins(g, ts, sc, s));
+        TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s, &ts));
+        TP_TRY(fill_bins(cubic, g, ts, rot, data, weights ? wrec : nullptr, sc, s));
         TP_TRY(launched(tp::launch_scatter3_tiled(cubic, 0, g, ts, proj, weights, rot, shifts, data, wrec, sc.p, 0, s),
                         "tiled backprojection launch"));
     }

@@ -90,6 +90,7 @@ struct TileSpec {
     // (about half of the headline's tiles lie outside that sphere)
     const int* flist;
     int64_t fcount;
+    bool core_zeroed;         // scatter: the bin pre-pass has zeroed the core tiles' cells
 };
 
 // The work items of the rotation kernels' forward tile grid (ts's nt, ntfd, core tiles and
@@ -137,14 +138,18 @@ constexpr int kCallScratchBytes = 256;
 static_assert(sizeof(CallPoses) <= kCallScratchBytes, "call scratch");
 
 // Fill *cp for the B_rot * P poses at rot (dim 2 or 3), rho_unit = the
-// TileSpec/TileSpec2 field of the call.
-hipError_t launch_call_poses(int dim, int64_t poses, const void* rot, float rho_unit, CallPoses* cp, hipStream_t s);
+// TileSpec/TileSpec2 field of the call; also zero the `nzero` ints at `zero`
+// (the call's pose-bin counts, or none).
+hipError_t launch_call_poses(int dim, int64_t poses, const void* rot, float rho_unit, CallPoses* cp, hipStream_t s,
+                             int* zero = nullptr, int64_t nzero = 0);
 
-// Fill the pose bins bg (list and count allocated by the caller) of the scatter tile grid whose
-// bin boxes bb describes, for the B_rot * P poses at rot; after launch_call_poses has filled *cp
-// (bins beyond the reach of the call's tiled poses stay empty, bb.reach being the rotations').
+// Fill the pose bins bg (list and count allocated by the caller, the counts zeroed by
+// launch_call_poses, which has also filled *cp) of the scatter tile grid whose bin boxes bb
+// describes, for the B_rot * P poses at rot (bins beyond the reach of the call's tiled poses stay
+// empty, bb.reach being the rotations').  With dst, the same workgroups zero the scatter's core
+// tiles' cells of dst (and wdst) that ts describes, which the core pieces then add into.
 hipError_t launch_pose_bins(const Geom& g, const void* rot, const BinGrid& bg, const BinBox& bb, const CallPoses* cp,
-                            hipStream_t s);
+                            hipStream_t s, const TileSpec& ts, void* dst, void* wdst);
 
 constexpr int kBlock = 256;
 constexpr int64_t kMaxGrid = int64_t(1) << 22;

@@ -2,7 +2,8 @@
 // tp_launch.hh): whether any pose is a rotation, whether every pose is one,
 // and the reach of the other tiled poses (rho_unit times their largest
 // singular value, plus a voxel).
-// It also clears the work counters of the call's GEN kernels.
+// It also clears the work counters of the call's GEN kernels and, for a 3D
+// scatter with pose bins, the bins' counts.
 #include "tp_device.hh"
 #include "tp_launch.hh"
 #include "tp_tiled_common.hh"
@@ -15,7 +16,9 @@ constexpr int kPoseThreads = 1024;
 
 template <int DIM>
 __global__ __launch_bounds__(kPoseThreads) void k_call_poses(const float* __restrict__ rot, int64_t poses,
-                                                             float rho_unit, CallPoses* __restrict__ cp) {
+                                                             float rho_unit, CallPoses* __restrict__ cp,
+                                                             int* __restrict__ zero, int64_t nzero) {
+    for (int64_t i = threadIdx.x; i < nzero; i += kPoseThreads) zero[i] = 0;
     constexpr int RS = DIM == 2 ? 4 : 9, U = 4;  // U poses per lane in flight
     __shared__ int part[kPoseThreads / 64][3];
     float m = 0.f;  // largest singular value of a tiled pose that is not a rotation (0: none)
@@ -66,11 +69,14 @@ __global__ __launch_bounds__(kPoseThreads) void k_call_poses(const float* __rest
 
 }  // namespace
 
-hipError_t launch_call_poses(int dim, int64_t poses, const void* rot, float rho_unit, CallPoses* cp, hipStream_t s) {
+hipError_t launch_call_poses(int dim, int64_t poses, const void* rot, float rho_unit, CallPoses* cp, hipStream_t s,
+                             int* zero, int64_t nzero) {
     if (dim == 2)
-        hipLaunchKernelGGL(k_call_poses<2>, dim3(1), dim3(kPoseThreads), 0, s, (const float*)rot, poses, rho_unit, cp);
+        hipLaunchKernelGGL(k_call_poses<2>, dim3(1), dim3(kPoseThreads), 0, s, (const float*)rot, poses, rho_unit, cp,
+                           zero, nzero);
     else
-        hipLaunchKernelGGL(k_call_poses<3>, dim3(1), dim3(kPoseThreads), 0, s, (const float*)rot, poses, rho_unit, cp);
+        hipLaunchKernelGGL(k_call_poses<3>, dim3(1), dim3(kPoseThreads), 0, s, (const float*)rot, poses, rho_unit, cp,
+                           zero, nzero);
     return hipGetLastError();
 }
 

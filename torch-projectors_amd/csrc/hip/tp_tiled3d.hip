@@ -1404,14 +1404,13 @@ __global__ __launch_bounds__(kBlock) void k_mirror_x0(Geom g, Cx<float>* __restr
 }
 
 // Zero the stored cells of the scatter core tiles, which their pose-range
-// pieces then accumulate into with atomics.
-template <bool WEIGHTS>
-__global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<float>* __restrict__ dst,
-                                                      float* __restrict__ wdst) {
+// pieces then accumulate into with atomics: cells e0, e0 + step, ... (wdst may be null).
+__device__ __forceinline__ void zero_core_cells(const Geom& g, const TileSpec& ts, Cx<float>* __restrict__ dst,
+                                                float* __restrict__ wdst, int64_t e0, int64_t step) {
     const int N = g.N, H = g.H, half = N / 2;
     const int dd = (ts.sd1 - ts.sd0) * SD, rr = (ts.sr1 - ts.sr0) * SR, cc = ts.sc1 * SC;
     const int64_t cells = int64_t(dd) * rr * cc;
-    for (int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x; e < g.B * cells; e += int64_t(gridDim.x) * kBlock) {
+    for (int64_t e = e0; e < g.B * cells; e += step) {
         const int64_t b = e / cells;
         const int64_t q = e - b * cells;
         const int c = int(q % cc), r = -half + 1 + ts.sr0 * SR + int((q / cc) % rr),
@@ -1420,8 +1419,14 @@ __global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<fl
         const int re = r < 0 ? r + N : r, de = d < 0 ? d + N : d;
         const int64_t idx = b * g.vol + (int64_t(de) * N + re) * H + c;
         dst[idx] = Cx<float>{0.f, 0.f};
-        if (WEIGHTS) wdst[idx] = 0.f;
+        if (wdst) wdst[idx] = 0.f;
     }
+}
+template <bool WEIGHTS>
+__global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<float>* __restrict__ dst,
+                                                      float* __restrict__ wdst) {
+    zero_core_cells(g, ts, dst, WEIGHTS ? wdst : nullptr, int64_t(blockIdx.x) * kBlock + threadIdx.x,
+                    int64_t(gridDim.x) * kBlock);
 }
 
 // Pose bins (launch_pose_bins): one workgroup per rotation batch item, row of bins along c (bins
@@ -1431,11 +1436,16 @@ __global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<fl
 // them there.  A bin's list is thus in no particular order (the scatter's tiles cull it into
 // per-tile lists that are unordered anyway).  A bin box holds every tile box of its 2 x 2 x 2 tiles
 // with half a voxel to spare on each side, far beyond the rounding of either plane test, so a pose
-// that crosses a tile's box is in its bin.  The counts start at zero (launch_pose_bins clears them).
+// that crosses a tile's box is in its bin.  The counts start at zero (the pose pre-pass clears
+// them).  With dst, the workgroups first zero the scatter's core cells (zero_core_cells).
 constexpr int kBinThreads = 256, kBinPer = kBinPoses / kBinThreads;
 static_assert(kBinPer * kBinThreads == kBinPoses, "bin pre-pass shape");
 __global__ __launch_bounds__(kBinThreads) void k_pose_bins(Geom g, const float* __restrict__ rot, BinGrid bg,
-                                                           BinBox bb, const CallPoses* __restrict__ cp) {
+                                                           BinBox bb, const CallPoses* __restrict__ cp, TileSpec ts,
+                                                           Cx<float>* __restrict__ dst, float* __restrict__ wdst) {
+    if (dst)
+        zero_core_cells(g, ts, dst, wdst, int64_t(blockIdx.x) * kBinThreads + threadIdx.x,
+                        int64_t(gridDim.x) * kBinThreads);
     const int lane = threadIdx.x & 63;
     const int nrow = bg.nb[1] * bg.nb[2];
     const int64_t blocks = (g.P + kBinPoses - 1) / kBinPoses;
@@ -1570,7 +1580,7 @@ template <bool CUBIC, int MODE, bool WEIGHTS, int KP, bool OSX>
 hipError_t scatter_launch(const Geom& g, const TileSpec& ts, const void* src, const void* weights, const void* rot,
                           const void* shifts, void* dst, void* wdst, CallPoses* cp, int gl, hipStream_t s) {
     const int64_t score = int64_t(ts.sd1 - ts.sd0) * (ts.sr1 - ts.sr0) * ts.sc1 * ts.ksplit;
-    if (score > 0) {
+    if (score > 0 && !ts.core_zeroed) {
         const int64_t cells = g.B * int64_t((ts.sd1 - ts.sd0) * SD) * ((ts.sr1 - ts.sr0) * SR) * (ts.sc1 * SC);
         int64_t blocks = (cells + kBlock - 1) / kBlock;
         if (blocks > 65536) blocks = 65536;
@@ -1695,13 +1705,11 @@ int64_t forw_reach_items(const Geom& g, const TileSpec& ts, std::vector<int>& ou
 }
 
 hipError_t launch_pose_bins(const Geom& g, const void* rot, const BinGrid& bg, const BinBox& bb, const CallPoses* cp,
-                            hipStream_t s) {
+                            hipStream_t s, const TileSpec& ts, void* dst, void* wdst) {
     const int64_t blocks = g.B_rot * int64_t(bg.nb[1]) * bg.nb[2] * ((g.P + kBinPoses - 1) / kBinPoses);
-    if (blocks == 0) return hipSuccess;
-    if (blocks > kBinMaxGroups) return hipErrorInvalidValue;  // make_bins keeps calls below it
-    const hipError_t e = launch_zero(bg.count, g.B_rot * int64_t(bg.n), s);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_pose_bins, dim3(unsigned(blocks)), dim3(kBinThreads), 0, s, g, (const float*)rot, bg, bb, cp);
+    if (blocks == 0 || blocks > kBinMaxGroups) return hipErrorInvalidValue;  // make_bins keeps calls within
+    hipLaunchKernelGGL(k_pose_bins, dim3(unsigned(blocks)), dim3(kBinThreads), 0, s, g, (const float*)rot, bg, bb, cp,
+                       ts, (Cx<float>*)dst, (float*)wdst);
     return hipGetLastError();
 }
 
