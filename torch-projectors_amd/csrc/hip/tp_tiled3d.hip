@@ -1684,23 +1684,36 @@ hipError_t forw_store(bool cubic, const Geom& g, const TileSpec& ts, const void*
 
 int64_t forw_reach_items(const Geom& g, const TileSpec& ts, std::vector<int>& out) {
     const int64_t items = forw_items(g, ts);
+    if (items > int64_t(INT32_MAX)) return items;
     // the rotation kernel's test (dist2 > rho2: the tile holds no sample) with a margin, so that
     // every tile the kernel would take is listed whatever the rounding
     const float rho = ts.rho_unit + 1.0f, rho2 = rho * rho * 1.001f + 4.0f;
-    for (int64_t w = 0; w < items; ++w) {
-        const Item it = item_of(w, g.B, int(g.P), ts.ntfd, ts.nt, ts.nt, ts.fd0, ts.fd1, ts.fc0, ts.fc1, ts.fc0,
-                                ts.fc1, ts.ksplit, ts.prange);
-        if (it.skip) continue;
-        const int tc = ts.org + it.kc * L, tr = ts.org + it.kr * L, td = ts.orgd + it.kd * LD;
-        const float lo[3] = {float(tc) - ts.eps, float(tr) - ts.eps, float(td) - ts.eps};
-        const float hi[3] = {float(tc + L) + ts.eps, float(tr + L) + ts.eps, float(td + LD) + ts.eps};
-        float dist2 = 0.f;
-        for (int k = 0; k < 3; ++k) {
-            const float q = lo[k] > 0.f ? lo[k] : (hi[k] < 0.f ? -hi[k] : 0.f);
-            dist2 += q * q;
+    auto axis2 = [&](int t, int edge) {  // squared distance of [t, t + edge] (+ slack) from 0
+        const float lo = float(t) - ts.eps, hi = float(t + edge) + ts.eps;
+        const float q = lo > 0.f ? lo : (hi < 0.f ? -hi : 0.f);
+        return q * q;
+    };
+    // the core pieces (item_of's first items) lie within 40 voxels of the origin: all listed
+    const int cd = ts.fd1 - ts.fd0, cc = ts.fc1 - ts.fc0;
+    const int64_t ncore = g.B * int64_t(cd) * cc * cc * ts.ksplit;
+    for (int64_t w = 0; w < ncore; ++w) out.push_back(int(w));
+    // then every tile of each batch item in item_of's order (kd, kr, kc), the core tiles skipped
+    // when they are split
+    const int nt = ts.nt, nd = ts.ntfd;
+    for (int64_t b = 0; b < g.B; ++b)
+        for (int kd = 0; kd < nd; ++kd) {
+            const float d2 = axis2(ts.orgd + kd * LD, LD);
+            for (int kr = 0; kr < nt; ++kr) {
+                const float r2 = axis2(ts.org + kr * L, L);
+                if (d2 + r2 > rho2) continue;
+                const int64_t row = ncore + b * int64_t(nd) * nt * nt + (int64_t(kd) * nt + kr) * nt;
+                const bool core_row = ts.ksplit > 1 && kd >= ts.fd0 && kd < ts.fd1 && kr >= ts.fc0 && kr < ts.fc1;
+                for (int kc = 0; kc < nt; ++kc) {
+                    if (core_row && kc >= ts.fc0 && kc < ts.fc1) continue;
+                    if (d2 + r2 + axis2(ts.org + kc * L, L) <= rho2) out.push_back(int(row + kc));
+                }
+            }
         }
-        if (dist2 <= rho2) out.push_back(int(w));
-    }
     return items;
 }
 
