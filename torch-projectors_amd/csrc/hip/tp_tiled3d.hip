@@ -1107,11 +1107,6 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
         const float hi2[3] = {float(fc0 + SC + SH) + ts.eps, float(fr0 + SR + SH) + ts.eps,
                               float(fd0 + SD + SH) + ts.eps};
         static_assert(SL - SH == 1, "box 2 is box 1 negated when the stencil reaches one cell further below");
-        for (int e = tid; e < S3; e += NT) {
-            acc_re[e] = 0.0;
-            acc_im[e] = 0.0;
-            if (WEIGHTS) acc_w[e] = 0.0;
-        }
         const int64_t rb = g.B_rot == 1 ? 0 : b, sb = g.B_shift == 1 ? 0 : b;
         const float* rotb = rot + rb * g.P * 9;
         const int64_t pose0 = b * g.P;
@@ -1124,6 +1119,15 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
         }
         // (a rotation kernel without rotations in the call only stores zeros)
         const int pend = (dist2 > rho_k * rho_k || (!GEN && !any_rot)) ? it.p0 : it.p1;
+        // a tile that no pose can reach stores zeros without its accumulators (about half of the
+        // tiles of a volume lie beyond the samples' sphere)
+        const bool empty = pend == it.p0;
+        if (!empty)
+            for (int e = tid; e < S3; e += NT) {
+                acc_re[e] = 0.0;
+                acc_im[e] = 0.0;
+                if (WEIGHTS) acc_w[e] = 0.0;
+            }
 
         const float* shb = shifts ? shifts + sb * g.P * 2 : nullptr;
         bool touched = false;  // GEN: some pose reaches the tile
@@ -1341,6 +1345,7 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
         // adds onto what the rotation kernel wrote: core pieces with atomics, the other tiles (one
         // workgroup each) by a plain read and write; without rotations in the call it stores them
         if (GEN && !touched && (it.core || any_rot)) continue;
+        if (empty && it.core) continue;  // (adds nothing)
         __syncthreads();
         {
             // each lane keeps one (c, r) of the tile and steps along d
@@ -1362,6 +1367,9 @@ __global__ __launch_bounds__(kScatterThreads) __attribute__((amdgpu_waves_per_eu
                         const Cx<float> o = dst[idx];
                         dst[idx] = Cx<float>{o.re + float(acc_re[a]), o.im + float(acc_im[a])};
                         if (WEIGHTS) wdst[idx] += float(acc_w[a]);
+                    } else if (empty) {
+                        dst[idx] = Cx<float>{0.f, 0.f};
+                        if (WEIGHTS) wdst[idx] = 0.f;
                     } else {
                         dst[idx] = Cx<float>{float(acc_re[a]), float(acc_im[a])};
                         if (WEIGHTS) wdst[idx] = float(acc_w[a]);
