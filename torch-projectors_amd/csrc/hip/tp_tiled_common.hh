@@ -108,7 +108,10 @@ __device__ __forceinline__ int64_t xcd_item(int64_t slot) {
 static_assert(kXcds == kXcdCount, "XCD count");
 
 // Slot sequence of a tiled kernel (slots map to work items through xcd_item).
-//   GEN = false: one slot per workgroup (the grid covers every slot).
+//   GEN = false: slot blockIdx.x, then every gridDim.x-th one (one slot per
+//                workgroup when the grid covers every slot, as the rotation
+//                kernels' grids do; the GEN forward's grid is a quarter of
+//                that and steps).
 //   GEN = true:  a persistent grid of the workgroups that fit on the device
 //                at once (gen_grid); a workgroup takes batches of kGrab slots
 //                of its XCD (blockIdx.x mod kXcds) from that XCD's counter in
