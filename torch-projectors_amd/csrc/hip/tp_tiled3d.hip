@@ -36,7 +36,9 @@
 // handle the others and write the masked pixels of the forward.  Each kernel
 // comes in two instantiations:
 //   GEN = false  rotations (columns orthonormal to kRotationTol), one
-//                workgroup per work item over the grid their samples reach;
+//                workgroup per work item over the grid their samples reach
+//                (the forward family's: per work item of TileSpec::flist,
+//                the tiles within that reach, when the C ABI has the list);
 //   GEN = true   the other tiled poses (scaled, anisotropically magnified or
 //                sheared matrices), launched after the first on a smaller
 //                grid (the forward's: a quarter of the rotation grid's
