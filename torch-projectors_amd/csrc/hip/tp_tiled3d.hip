@@ -262,7 +262,7 @@ struct Item {
     int p0, p1;
     bool core, skip;
 };
-__host__ __device__ inline Item item_of(int64_t w, int64_t B, int P, int nd, int nr, int nc, int d0, int d1, int r0,
+__device__ __forceinline__ Item item_of(int64_t w, int64_t B, int P, int nd, int nr, int nc, int d0, int d1, int r0,
                                         int r1, int c0, int c1, int ksplit, int prange) {
     Item it;
     const int cd = d1 - d0, cr = r1 - r0, cc = c1 - c0;
@@ -1555,8 +1555,8 @@ unsigned grid_of(int64_t items, const void* kernel, int threads) {
 // GEN forward-family grid: a quarter of the rotation kernel's slots (a multiple of kXcds), each
 // workgroup stepping over the GEN grid's slots by the grid size.  As many workgroups as the
 // rotation kernel's would make a call without such poses pay for their empty launch (about 10 us
-// at the headline); a persistent grid (a multiple of kXcds workgroups per CU) balances the tiles'
-// uneven work worse: at poses scaled by 1.02 the forward took 0.87 ms with the persistent grid
+// at the headline); a persistent grid (the workgroups that fit on the device at once) balances
+// the tiles' uneven work worse: at poses scaled by 1.02 the forward took 0.87 ms with the persistent grid
 // and per-XCD counters, 0.77 / 0.74 / 0.74 ms with an eighth / a quarter / half of the rotation
 // slots, 0.83 ms with a sixteenth (and 1.29 against 1.69 ms with poses scaled by 1.4).
 constexpr int kGenForwShare = 4;
