@@ -131,7 +131,18 @@ int scatter_poses_per_batch(double w, double eps, double os) {
     return rows <= 14 ? 6 : (rows <= 21 ? 4 : (rows <= 32 ? 3 : 1));
 }
 
-tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
+// Poses per range of the forward projection's rotation kernel's core tiles: 2048 at oversampling 2
+// and above, fewer as the oversampling (and so the spacing of a pose's samples) shrinks, so that a
+// range holds about as many samples: at oversampling 1 a core tile holds four times the samples
+// per pose, and unsplit core tiles became the critical path there (the published rows' linear
+// batch-1 forward 0.50 -> 0.86 ms at 2048), so it takes 512 like the rest.
+int64_t forw_poses_per_range(double os) {
+    const double r = 2048.0 * (os / 2.0) * (os / 2.0);
+    return r >= 2048.0 ? 2048 : (r <= 512.0 || !(r == r) ? 512 : int64_t(r));
+}
+// pkf: poses per range of the rotation forward-family kernels' core tiles (forward projections
+// take forw_poses_per_range, their backward ops the scatter's 512).
+tp::TileSpec tile_spec(const tp::Geom& g, bool cubic, int64_t pkf = 512) {
     constexpr int L = tp::kTileEdge;
     tp::TileSpec ts{};
     // radius bound of the active pixels: the cutoff disc, within the pixel grid
@@ -175,12 +186,19 @@ tp::TileSpec tile_spec(const tp::Geom& g, bool cubic) {
     ts.sr0 = std::max(0, (-rc + half - 1) / tp::kScTR);
     ts.sr1 = std::min(ts.ntr, (rc + half - 1) / tp::kScTR + 1);
     ts.sc1 = std::min(ts.ntc, rc / tp::kScTC + 1);
-    const int64_t pk = 512;  // poses per range
+    // poses per range: the scatter's core tiles carry the most work of its grid and split at 512
+    // (at 1024 the headline backprojection took 1.41 ms against 1.34), as do the kernels of the
+    // other tiled poses and the gradient modes (1-4 % slower at 2048); the rotation forward
+    // projection's split at pkf (at oversampling 2, c2's forward 0.317 ms at 512 against 0.299 at
+    // 2048, the headline's the same)
+    const int64_t pk = 512;
     ts.ksplit = int(std::max<int64_t>(1, (g.P + pk - 1) / pk));
     ts.prange = int((g.P + ts.ksplit - 1) / ts.ksplit);
+    ts.fksplit = int(std::max<int64_t>(1, (g.P + pkf - 1) / pkf));
+    ts.fprange = int((g.P + ts.fksplit - 1) / ts.fksplit);
     if (ts.ksplit == 1)  // nothing to split
-        ts.fc1 = ts.fc0 = ts.fd1 = ts.fd0 = ts.fc1_2 = ts.fc0_2 = ts.fd1_2 = ts.fd0_2 = ts.sd1 = ts.sd0 = ts.sr1 =
-            ts.sr0 = ts.sc1 = 0;
+        ts.fc1_2 = ts.fc0_2 = ts.fd1_2 = ts.fd0_2 = ts.sd1 = ts.sd0 = ts.sr1 = ts.sr0 = ts.sc1 = 0;
+    if (ts.fksplit == 1) ts.fc1 = ts.fc0 = ts.fd1 = ts.fd0 = 0;
     ts.rho = float(rho);
     ts.rho_unit = float(rho_unit);
     ts.os = float(g.os);
@@ -429,9 +447,9 @@ struct CallScratch {
         uint32_t rho_bits = 0, eps_bits = 0;
         std::memcpy(&rho_bits, &ts.rho_unit, 4);
         std::memcpy(&eps_bits, &ts.eps, 4);
-        // everything the list depends on (the pose count only through ksplit)
+        // everything the list depends on (the pose count only through fksplit)
         const std::vector<int64_t> key{g.B, ts.nt, ts.org, ts.ntfd, ts.orgd, ts.fc0, ts.fc1, ts.fd0, ts.fd1,
-                                       ts.ksplit, int64_t(rho_bits), int64_t(eps_bits)};
+                                       ts.fksplit, int64_t(rho_bits), int64_t(eps_bits)};
         StreamScratch::ForwList* victim = nullptr;
         for (StreamScratch::ForwList& f : area->flists) {
             if (f.p && f.key == key) {
@@ -614,7 +632,7 @@ int project_forw(int dim, int dtype, const void* rec, int64_t B, int64_t D, int6
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool cubic = interp == TP_CUBIC;
     if (use_tiles(dim, dt, os, n)) {
-        tp::TileSpec ts = tile_spec(g, cubic);
+        tp::TileSpec ts = tile_spec(g, cubic, forw_poses_per_range(os));
         TP_TRY(call_poses(3, g, rot, ts.rho_unit, sc, s));
         TP_TRY(use_forw_list(g, ts, sc, s));
         TP_TRY(launched(tp::launch_project3_forw_tiled(cubic, g, ts, rec, rot, shifts, out, sc.p, 0, s, rec_half),

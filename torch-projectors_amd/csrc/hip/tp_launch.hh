@@ -72,7 +72,8 @@ struct TileSpec {
     int fc0_2, fc1_2, fd0_2, fd1_2;  // and its core tiles (the same voxels as fc0.. fd1)
     int ntd, ntr, ntc;        // scatter: tiles along d, r, c of the stored half volume
     int sd0, sd1, sr0, sr1, sc1;  // scatter core tiles: [sd0, sd1) x [sr0, sr1) x [0, sc1)
-    int ksplit, prange;       // pose ranges per core tile, poses per range
+    int ksplit, prange;       // pose ranges per core tile, poses per range (the scatters, GEN gathers)
+    int fksplit, fprange;     // the same for the rotation forward-family kernels (fc0.. fd1)
     float rho;                // bound on |x| of every active sample of a tiled pose (singular values <= kScaleMax)
     float rho_unit;           // the same for singular values <= 1, less the +1 voxel margin
     float eps;                // slack (voxels) added to every enumeration box
@@ -94,7 +95,7 @@ struct TileSpec {
 };
 
 // The work items of the rotation kernels' forward tile grid (ts's nt, ntfd, core tiles and
-// ksplit) whose tiles lie within rho_unit + 1 (and a margin) of the origin, in increasing order,
+// fksplit) whose tiles lie within rho_unit + 1 (and a margin) of the origin, in increasing order,
 // appended to `out`; returns the grid's item count.  Host code, for TileSpec::flist.
 int64_t forw_reach_items(const Geom& g, const TileSpec& ts, std::vector<int>& out);
 

@@ -627,7 +627,9 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
         fd1 = min(ntd, max(fd0, ts.fd1_2 - offd));
     }
     const float rho2 = rho_k * rho_k;
-    int64_t items = g.B * (int64_t(fc1 - fc0) * (fc1 - fc0) * (fd1 - fd0) * ts.ksplit + int64_t(nt) * nt * ntd);
+    // core tiles in pose ranges: the rotation kernels' split, or the other poses' (the scatter's)
+    const int ksplit = GEN ? ts.ksplit : ts.fksplit, prange = GEN ? ts.prange : ts.fprange;
+    int64_t items = g.B * (int64_t(fc1 - fc0) * (fc1 - fc0) * (fd1 - fd0) * ksplit + int64_t(nt) * nt * ntd);
     // rotations: the slots may index the list of the work items in reach (the others' workgroups
     // would only start and leave)
     const int* __restrict__ flist = GEN ? nullptr : ts.flist;
@@ -641,7 +643,7 @@ __attribute__((amdgpu_waves_per_eu(forw_waves_per_eu<CUBIC, GMODE, VS, GEN>())))
         const int64_t wi = xcd_item<kRunForw>(slot_i);
         if (wi >= items) continue;
         const int64_t w = flist ? int64_t(flist[wi]) : wi;
-        const Item it = item_of(w, g.B, int(g.P), ntd, nt, nt, fd0, fd1, fc0, fc1, fc0, fc1, ts.ksplit, ts.prange);
+        const Item it = item_of(w, g.B, int(g.P), ntd, nt, nt, fd0, fd1, fc0, fc1, fc0, fc1, ksplit, prange);
         if (it.skip) continue;
         const int64_t b = it.b;
         const int tc = org + it.kc * L, tr = org + it.kr * L, td = orgd + it.kd * LD;
@@ -1540,7 +1542,7 @@ __global__ __launch_bounds__(kBinThreads) void k_pose_bins(Geom g, const float* 
 // Work items of the rotation kernels' forward tile grid (the unit grid).
 int64_t forw_items(const Geom& g, const TileSpec& ts) {
     const int fc = ts.fc1 - ts.fc0, fd = ts.fd1 - ts.fd0;
-    return g.B * (int64_t(fc) * fc * fd * ts.ksplit + int64_t(ts.nt) * ts.nt * ts.ntfd);
+    return g.B * (int64_t(fc) * fc * fd * ts.fksplit + int64_t(ts.nt) * ts.nt * ts.ntfd);
 }
 // Workgroups of a launch of `kernel` over `items`: one per item (rotations), or the persistent
 // GEN grid (the scatter's).
@@ -1705,7 +1707,7 @@ int64_t forw_reach_items(const Geom& g, const TileSpec& ts, std::vector<int>& ou
     };
     // the core pieces (item_of's first items) lie within 40 voxels of the origin: all listed
     const int cd = ts.fd1 - ts.fd0, cc = ts.fc1 - ts.fc0;
-    const int64_t ncore = g.B * int64_t(cd) * cc * cc * ts.ksplit;
+    const int64_t ncore = g.B * int64_t(cd) * cc * cc * ts.fksplit;
     for (int64_t w = 0; w < ncore; ++w) out.push_back(int(w));
     // then every tile of each batch item in item_of's order (kd, kr, kc), the core tiles skipped
     // when they are split
@@ -1717,7 +1719,7 @@ int64_t forw_reach_items(const Geom& g, const TileSpec& ts, std::vector<int>& ou
                 const float r2 = axis2(ts.org + kr * L, L);
                 if (d2 + r2 > rho2) continue;
                 const int64_t row = ncore + b * int64_t(nd) * nt * nt + (int64_t(kd) * nt + kr) * nt;
-                const bool core_row = ts.ksplit > 1 && kd >= ts.fd0 && kd < ts.fd1 && kr >= ts.fc0 && kr < ts.fc1;
+                const bool core_row = ts.fksplit > 1 && kd >= ts.fd0 && kd < ts.fd1 && kr >= ts.fc0 && kr < ts.fc1;
                 for (int kc = 0; kc < nt; ++kc) {
                     if (core_row && kc >= ts.fc0 && kc < ts.fc1) continue;
                     if (d2 + r2 + axis2(ts.org + kc * L, L) <= rho2) out.push_back(int(row + kc));
