@@ -1444,8 +1444,8 @@ __global__ __launch_bounds__(kBlock) void k_zero_core(Geom g, TileSpec ts, Cx<fl
 // Pose bins (launch_pose_bins): one workgroup per rotation batch item, row of bins along c (bins
 // differ there only in their c extent) and block of kBinPoses poses, so each pose is loaded once per
 // row.  A lane tests its poses against every bin of the row with the tiles' plane test (a bit per
-// bin); per bin, a wave reserves room for its hits with one atomic on the bin's count and writes
-// them there.  A bin's list is thus in no particular order (the scatter's tiles cull it into
+// bin); a wave reserves room for its hits in every bin of the row at once (one atomic instruction,
+// a lane per bin, on the bins' counts) and writes them there.  A bin's list is thus in no particular order (the scatter's tiles cull it into
 // per-tile lists that are unordered anyway).  A bin box holds every tile box of its 2 x 2 x 2 tiles
 // with half a voxel to spare on each side, far beyond the rounding of either plane test, so a pose
 // that crosses a tile's box is in its bin.  The counts start at zero (the pose pre-pass clears
@@ -1513,18 +1513,23 @@ __global__ __launch_bounds__(kBinThreads) void k_pose_bins(Geom g, const float* 
 #pragma unroll
             for (int u = 0; u < kBinPer; ++u) hits[u] |= (p[u] < P && plane_hits(R[u], lo, hi)) ? 1u << i : 0u;
         }
+        // the wave's hits per bin of the group (lane i: bin i0 + i), then the room in every bin of
+        // the group with one atomic instruction (one round trip, not one per bin)
+        int room = 0;
         for (int i = 0; i < ng; ++i) {
-            uint64_t m[kBinPer];
             int total = 0;
 #pragma unroll
-            for (int u = 0; u < kBinPer; ++u) {
-                m[u] = __ballot((hits[u] >> i) & 1u);
-                total += __popcll(m[u]);
-            }
-            if (total == 0) continue;
-            int base = 0;
-            if (lane == 0) base = atomicAdd(&bg.count[bin0 + i0 + i], total);
-            base = __builtin_amdgcn_readfirstlane(base);
+            for (int u = 0; u < kBinPer; ++u) total += __popcll(__ballot((hits[u] >> i) & 1u));
+            if (lane == i) room = total;
+        }
+        int first = 0;
+        if (lane < ng && room > 0) first = atomicAdd(&bg.count[bin0 + i0 + lane], room);
+        for (int i = 0; i < ng; ++i) {
+            if (__builtin_amdgcn_readlane(room, i) == 0) continue;
+            uint64_t m[kBinPer];
+#pragma unroll
+            for (int u = 0; u < kBinPer; ++u) m[u] = __ballot((hits[u] >> i) & 1u);
+            int base = __builtin_amdgcn_readlane(first, i);
             unsigned short* out = bg.list + (bin0 + i0 + i) * g.P;
 #pragma unroll
             for (int u = 0; u < kBinPer; ++u) {
