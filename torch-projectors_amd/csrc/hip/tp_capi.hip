@@ -187,7 +187,8 @@ tp::TileSpec tile_spec(const tp::Geom& g, bool cubic, int64_t pkf = 512) {
     ts.sr1 = std::min(ts.ntr, (rc + half - 1) / tp::kScTR + 1);
     ts.sc1 = std::min(ts.ntc, rc / tp::kScTC + 1);
     // poses per range: the scatter's core tiles carry the most work of its grid and split at 512
-    // (at 1024 the headline backprojection took 1.41 ms against 1.34), as do the kernels of the
+    // (at 1024 the headline backprojection took 1.41 ms against 1.34; backprojection_ranges
+    // lengthens them for calls of more than 2048 poses), as do the kernels of the
     // other tiled poses and the gradient modes (1-4 % slower at 2048); the rotation forward
     // projection's split at pkf (at oversampling 2, c2's forward 0.317 ms at 512 against 0.299 at
     // 2048, the headline's the same)
